@@ -1,0 +1,24 @@
+/* libtinyinfer_backend.so — entry points with no counterpart in the reference ABI.
+ *
+ * ti_amd_gemm_i8_fused: the W8A16 linear with the epilogues the GPT-2 runtime
+ * fuses into the GEMM (the reference runs them as separate kernels:
+ * reference llm/src/runtime.cu:149-153 residual adds, :151 gelu_new):
+ *   epilogue 0: y = fp16_rn(acc + bias)
+ *   epilogue 1: y = fp16_rn(gelu_tanh(fp16_rn(acc + bias)))
+ *   epilogue 2: y = fp16_rn(residual + fp16_rn(acc + bias))   (residual may equal y)
+ * a fp16 [M,K], q int8 [K,N], scales fp32 [N], bias fp16 [N] or null, y fp16 [M,N].
+ * For callers that want the fused decode/prefill kernels standalone (the
+ * configs[1] sweep, tests).  Validation and status codes as ti_v2_gemm_ex_i8. */
+#ifndef TINYINFER_AMD_EXT_H
+#define TINYINFER_AMD_EXT_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const float* scales,
+                         const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m,
+                         int n, int k, int epilogue, uintptr_t stream, int device);
+#ifdef __cplusplus
+}
+#endif
+#endif

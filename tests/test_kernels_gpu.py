@@ -1,0 +1,391 @@
+"""GPU parity of the gfx950 kernels, called through the C ABI (NativeOps mirror of
+reference llm/native_ops.py and ctypes), against the CPU oracle on identical
+seeded inputs.
+
+Tolerances (stated per north star): fp16 linear and attention outputs within
+rtol 1e-2 / atol 2e-2 of the oracle's fp32-accumulate result; FP32 LayerNorm and
+Softmax within 1e-4 relative; fp16 row ops within 1e-2/2e-2 (the reference's own
+kernel gate, reference bench/v2/kernels/correctness.py:6).  Each test prints the
+case it runs before launching, so a failing GPU run names its case.
+"""
+import ctypes as C
+import gc
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 2e-2
+
+
+def torch():
+    import torch as t
+    return t
+
+
+def dev(a, dtype=None):
+    t = torch()
+    x = t.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        x = x.view(dtype)
+    return x.cuda()
+
+
+def host(x):
+    torch().cuda.synchronize()
+    return x.cpu().numpy()
+
+
+def hbits(x):
+    return host(x.view(torch().int16)).view(np.uint16)
+
+
+def f16(a):
+    return np.asarray(a, np.float16).view(np.uint16)
+
+
+def h(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float64)
+
+
+def say(*args):
+    print("[case]", *args, flush=True)
+
+
+def close(actual, expected, rtol=RTOL, atol=ATOL):
+    actual, expected = np.asarray(actual, np.float64), np.asarray(expected, np.float64)
+    assert np.all(np.isfinite(actual))
+    err = np.abs(actual - expected)
+    bad = err > atol + rtol * np.abs(expected)
+    assert not bad.any(), f"max abs err {err.max():.3g} at {np.argwhere(bad)[:3].tolist()}"
+    return float(err.max())
+
+
+# ---------------------------------------------------------------- GEMM
+def gemm_case(ops, m, n, k, config, int8, seed=0):
+    t = torch()
+    rng = np.random.default_rng(seed + 1000 * m + n + 7 * k + config)
+    a = f16(rng.standard_normal((m, k)) * 0.25)
+    w = f16(rng.standard_normal((k, n)) * 0.25)
+    bias = f16(rng.standard_normal(n) * 0.1)
+    if int8:
+        wv = w.copy()
+        wv[:, 0] = 0  # zero channel: scale 1, q 0 (reference correctness.py:202)
+        q, s = oracle.quantize(wv)
+        ref32 = oracle.linear(a, q=q, scales=s, bias_bits=bias, out_dtype="f32")
+        ref16 = oracle.linear(a, q=q, scales=s, bias_bits=bias)
+        out32 = ops.gemm_int8(dev(a, t.float16), dev(q), dev(s), bias=dev(bias, t.float16), config=config,
+                              output_dtype=t.float32)
+        out16 = ops.gemm_int8(dev(a, t.float16), dev(q), dev(s), bias=dev(bias, t.float16), config=config)
+    else:
+        ref32 = oracle.linear(a, w_bits=w, bias_bits=bias, out_dtype="f32")
+        ref16 = oracle.linear(a, w_bits=w, bias_bits=bias)
+        out32 = ops.gemm(dev(a, t.float16), dev(w, t.float16), bias=dev(bias, t.float16), config=config,
+                         output_dtype=t.float32)
+        out16 = ops.gemm(dev(a, t.float16), dev(w, t.float16), bias=dev(bias, t.float16), config=config)
+    close(host(out32), ref32)
+    # fp32 output: only the summation order differs from the oracle
+    close(host(out32), ref32, rtol=1e-4, atol=1e-4 * max(1.0, np.abs(ref32).max()))
+    close(h(hbits(out16)), h(ref16))
+
+
+@pytest.mark.parametrize("int8", [True, False])
+@pytest.mark.parametrize("config", list(range(12)))
+def test_gemm_reference_gate_shapes(ops, golden, config, int8):
+    for m, n, k in golden["gemm_shapes"]["shapes"]:
+        say("gemm", m, n, k, "config", config, "int8", int8)
+        gemm_case(ops, m, n, k, config, int8)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 768, 3072), (3, 100, 1000), (8, 3072, 768), (20, 2304, 768),
+                                   (32, 768, 3072), (33, 70, 129), (64, 3072, 768), (100, 50, 40),
+                                   (2, 50257, 768)])
+def test_gemm_split_k_and_tiled_paths(ops, m, n, k):
+    say("gemm paths", m, n, k)
+    gemm_case(ops, m, n, k, 0, True, seed=1)
+
+
+def test_gemm_repeat_calls_are_identical(ops):
+    """The split-K arrival counters reset themselves: back-to-back launches agree."""
+    t = torch()
+    rng = np.random.default_rng(3)
+    a = dev(f16(rng.standard_normal((4, 3072))), t.float16)
+    q = dev(rng.integers(-127, 128, (3072, 768)).astype(np.int8))
+    s = dev(rng.uniform(1e-3, 1e-2, 768).astype(np.float32))
+    say("gemm repeat")
+    outs = [hbits(ops.gemm_int8(a, q, s)) for _ in range(4)]
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+
+
+def _fused(ops_lib, a, q, s, bias, y, res, m, n, k, epi):
+    t = torch()
+    fn = ops_lib.ti_amd_gemm_i8_fused
+    fn.argtypes = [C.c_void_p] * 6 + [C.c_int] * 4 + [C.c_size_t, C.c_int]
+    stream = t.cuda.current_stream()
+    ptr = lambda x: None if x is None else x.data_ptr()
+    st = fn(ptr(a), ptr(q), ptr(s), ptr(bias), ptr(y), ptr(res), m, n, k, epi, stream.cuda_stream, 0)
+    assert st == 0, ops_lib.ti_v2_last_error()
+
+
+@pytest.mark.parametrize("m", [1, 8, 64, 512])
+@pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768)])
+def test_w8a16_sweep_fused_bias_gelu(ops, m, k, n):
+    """A ~ N(0,1) fp16, q ~ U[-127,127], scales U[1e-3,1e-2] drawn
+    as fp16 and widened to fp32, bias N(0,0.02), fused bias+GELU, fp16 output."""
+    t = torch()
+    rng = np.random.default_rng(20261101 + m + n)
+    a = f16(rng.standard_normal((m, k)))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("sweep gelu", m, k, n)
+    y = t.empty((m, n), dtype=t.float16, device="cuda")
+    _fused(ops.lib, dev(a, t.float16), dev(q), dev(s), dev(bias, t.float16), y, None, m, n, k, 1)
+    ref = oracle.linear(a, q=q, scales=s, bias_bits=bias, gelu=True)
+    close(h(hbits(y)), h(ref))
+    # residual epilogue, in place (y = y + proj)
+    res = dev(f16(rng.standard_normal((m, n))), t.float16)
+    expect = h(hbits(res)) + h(oracle.linear(a, q=q, scales=s, bias_bits=bias))
+    _fused(ops.lib, dev(a, t.float16), dev(q), dev(s), dev(bias, t.float16), res, res, m, n, k, 2)
+    close(h(hbits(res)), expect.astype(np.float16).astype(np.float64))
+
+
+def test_legacy_fp32_gemm(ops):
+    t = torch()
+    rng = np.random.default_rng(4)
+    for m, n, k in ((1, 1, 1), (7, 13, 5), (65, 257, 300), (128, 96, 513)):
+        say("legacy gemm", m, n, k)
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+        out = host(ops.legacy_gemm(dev(a), dev(b)))
+        assert np.allclose(out, a.astype(np.float64) @ b, atol=1e-5 * k + 1e-5)
+
+
+# ---------------------------------------------------------------- attention
+@pytest.mark.parametrize("config", [0, 1])
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_reference_cases(ops, golden, d, config):
+    t = torch()
+    rng = np.random.default_rng(d + config)
+    for nq, nk, ql, kl, off, causal in golden["attention_cases"]["cases"]:
+        say("attention", d, config, nq, nk, ql, kl, off, causal)
+        q = f16(rng.standard_normal((2, 2, nq, d)) * 0.5)
+        k = f16(rng.standard_normal((2, 2, nk, d)) * 0.5)
+        v = f16(rng.standard_normal((2, 2, nk, d)))
+        out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
+                            kv_lengths=kl, query_offsets=off, causal=causal, config=config)
+        got = h(hbits(out))
+        ref = oracle.attention_f16(q, k, v, ql, kl, off, causal)
+        close(got, h(ref))
+        zero_rows = h(ref) == 0
+        rows_zero = np.all(zero_rows, axis=-1)
+        assert np.all(got[rows_zero] == 0), "all-masked output must be exactly zero"
+
+
+def test_decode_attention_config3(ops):
+    """B=32, H=12, D=64, one query per request, ragged
+    context lengths U[128,1024], Q/K/V ~ N(0,1)/8, FP32 softmax."""
+    t = torch()
+    rng = np.random.default_rng(20261101)
+    B, H, D = 32, 12, 64
+    L = rng.integers(128, 1025, B)
+    K = int(L.max())
+    q = f16(rng.standard_normal((B, H, 1, D)) / 8)
+    k = f16(rng.standard_normal((B, H, K, D)) / 8)
+    v = f16(rng.standard_normal((B, H, K, D)) / 8)
+    say("decode attention", B, H, D, K)
+    out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=[1] * B,
+                        kv_lengths=L.tolist(), query_offsets=(L - 1).tolist(), causal=True)
+    close(h(hbits(out)), h(oracle.attention_f16(q, k, v, [1] * B, L, L - 1, True)))
+
+
+@pytest.mark.parametrize("nq,nk", [(64, 64), (300, 300), (1, 2000), (3, 700)])
+def test_attention_prefill_and_long(ops, nq, nk):
+    t = torch()
+    rng = np.random.default_rng(nq + nk)
+    B, H, D = 2, 3, 64
+    ql = [nq, max(1, nq // 2)]
+    kl = [nk, max(1, nk - 5)]
+    off = [nk - nq, max(0, kl[1] - ql[1])]
+    q = f16(rng.standard_normal((B, H, nq, D)) * 0.5)
+    k = f16(rng.standard_normal((B, H, nk, D)) * 0.5)
+    v = f16(rng.standard_normal((B, H, nk, D)))
+    say("attention prefill", nq, nk)
+    out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
+                        kv_lengths=kl, query_offsets=off, causal=True)
+    close(h(hbits(out)), h(oracle.attention_f16(q, k, v, ql, kl, off, True)))
+
+
+# ---------------------------------------------------------------- row ops fp16
+@pytest.mark.parametrize("cols", [1, 7, 257, 768, 3072, 5000])
+def test_layernorm_gelu_softmax_f16(ops, cols):
+    t = torch()
+    rng = np.random.default_rng(cols)
+    x = f16(rng.standard_normal((3, cols)))
+    g, b = f16(rng.standard_normal(cols)), f16(rng.standard_normal(cols))
+    say("fp16 rowops", cols)
+    xd = dev(x, t.float16)
+    close(h(hbits(ops.layernorm(xd, dev(g, t.float16), dev(b, t.float16)))), h(oracle.layernorm_f16(x, g, b)))
+    close(h(hbits(ops.gelu_new(xd))), h(oracle.gelu_f16(x)))
+    close(h(hbits(ops.softmax(xd))), h(oracle.softmax_f16(x)))
+
+
+def test_rowops_f16_tight_against_oracle(ops):
+    """GPT-2 shapes: LN over 768 and GELU over 3072 land within one fp16 ulp."""
+    t = torch()
+    rng = np.random.default_rng(5)
+    x = f16(rng.standard_normal((64, 768)))
+    g, b = f16(1 + 0.02 * rng.standard_normal(768)), f16(0.02 * rng.standard_normal(768))
+    say("fp16 LN tight")
+    got = hbits(ops.layernorm(dev(x, t.float16), dev(g, t.float16), dev(b, t.float16)))
+    ref = oracle.layernorm_f16(x, g, b)
+    ulp = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+    assert ulp.max() <= 1
+    y = f16(rng.standard_normal((16, 3072)) * 2)
+    got = hbits(ops.gelu_new(dev(y, t.float16)))
+    assert np.abs(got.astype(np.int32) - oracle.gelu_f16(y).astype(np.int32)).max() <= 1
+
+
+# ---------------------------------------------------------------- row ops fp32 (legacy ABI)
+def _legacy():
+    from tinyinfer_amd import BACKEND_LIB
+    lib = C.CDLL(str(BACKEND_LIB))
+    p, i = C.c_void_p, C.c_int
+    lib.ti_cuda_softmax.argtypes = [p, p, i, i]
+    lib.ti_cuda_layernorm.argtypes = [p, p, p, p, i, i, C.c_float]
+    lib.ti_cuda_gemm.argtypes = [p, p, p, i, i, i]
+    return lib
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 768), (7, 4099), (3, 1), (33, 1000)])
+def test_fp32_layernorm_config2(rows, cols):
+    """LayerNorm [4096,768], eps 1e-5, gamma N(1,0.1), beta N(0,0.1),
+    x N(0,1); 1e-4 relative against the float64 reference."""
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(cols)).astype(np.float32)
+    dx, dg, db = dev(x), dev(g), dev(b)
+    y = torch().empty_like(dx)
+    say("fp32 layernorm", rows, cols)
+    _legacy().ti_cuda_layernorm(dx.data_ptr(), dg.data_ptr(), db.data_ptr(), y.data_ptr(), rows, cols, 1e-5)
+    ref = oracle.layernorm_f32_exact(x, g, b)
+    close(host(y), ref, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (17, 4097), (5, 31)])
+def test_fp32_softmax_config2(rows, cols):
+    rng = np.random.default_rng(rows * cols)
+    x = (3 * rng.standard_normal((rows, cols))).astype(np.float32)
+    x[0, ::5] = -np.inf
+    dx = dev(x)
+    y = torch().empty_like(dx)
+    say("fp32 softmax", rows, cols)
+    _legacy().ti_cuda_softmax(dx.data_ptr(), y.data_ptr(), rows, cols)
+    out = host(y)
+    ref = oracle.softmax_f32_exact(x)
+    close(out, ref, rtol=1e-4, atol=1e-8)
+    assert np.all(out[0, ::5] == 0)
+
+
+def test_fp32_layernorm_then_softmax_config2():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((4096, 768)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(768)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(768)).astype(np.float32)
+    dx, dg, db = dev(x), dev(g), dev(b)
+    mid = torch().empty_like(dx)
+    y = torch().empty_like(dx)
+    lib = _legacy()
+    say("fp32 LN->softmax")
+    lib.ti_cuda_layernorm(dx.data_ptr(), dg.data_ptr(), db.data_ptr(), mid.data_ptr(), 4096, 768, 1e-5)
+    lib.ti_cuda_softmax(mid.data_ptr(), y.data_ptr(), 4096, 768)
+    ref = oracle.softmax_f32_exact(oracle.layernorm_f32_exact(x, g, b))
+    close(host(y), ref, rtol=1e-4, atol=1e-8)
+
+
+def test_ti_cuda_gemm_legacy_order():
+    rng = np.random.default_rng(12)
+    m, k, n = 37, 70, 45
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    da, db = dev(a), dev(b)
+    y = torch().empty((m, n), dtype=torch().float32, device="cuda")
+    say("ti_cuda_gemm")
+    _legacy().ti_cuda_gemm(da.data_ptr(), db.data_ptr(), y.data_ptr(), m, k, n)
+    assert np.allclose(host(y), a.astype(np.float64) @ b, atol=1e-5 * k + 1e-5)
+
+
+# ---------------------------------------------------------------- contracts
+def test_invalid_contracts(ops):
+    """Wrapper-level rejections of reference correctness.py:286-302 and the native
+    status codes of reference tinyinfer_host_validation.hpp."""
+    t = torch()
+    a = t.ones((2, 3), device="cuda", dtype=t.float16)
+    b = t.ones((3, 4), device="cuda", dtype=t.float16)
+    for fn in (lambda: ops.gemm(a.cpu(), b), lambda: ops.gemm(a.float(), b), lambda: ops.gemm(a.t(), b),
+               lambda: ops.gemm(a, b, config=True), lambda: ops.gemm(a, b, config=12),
+               lambda: ops.gemm(a, b, bias=t.zeros(3, device=a.device, dtype=a.dtype)),
+               lambda: ops.gemm(a.clone().requires_grad_(), b)):
+        with pytest.raises((ValueError, TypeError)):
+            fn()
+    q = t.ones((1, 1, 1, 64), device="cuda", dtype=t.float16)
+    for fn in (lambda: ops.attention(q, q, q, q_lengths=[2]), lambda: ops.attention(q, q, q, query_offsets=[-1]),
+               lambda: ops.attention(q, q, q, kv_lengths=[True]), lambda: ops.attention(q, q, q, causal=1)):
+        with pytest.raises((ValueError, TypeError)):
+            fn()
+    lib = ops.lib
+    s = t.cuda.current_stream().cuda_stream
+    y = t.empty((2, 4), device="cuda", dtype=t.float16)
+    assert lib.ti_v2_gemm_ex_f16(a.data_ptr(), b.data_ptr(), None, y.data_ptr(), None, 2, 4, 3, 0, 12, s, 0) == 3
+    assert lib.ti_v2_gemm_ex_f16(a.data_ptr(), b.data_ptr(), None, y.data_ptr(), None, 2, 4, 3, 0, 6, s, 0) == 1
+    assert lib.ti_v2_gemm_ex_f16(a.data_ptr() + 1, b.data_ptr(), None, y.data_ptr(), None, 2, 4, 3, 0, 0, s, 0) == 1
+    assert lib.ti_v2_gemm_ex_f16(a.data_ptr(), b.data_ptr(), None, y.data_ptr(), None, 2, 4, 3, 2, 0, s, 0) == 1
+    assert lib.ti_v2_gemm_ex_f16(a.data_ptr(), b.data_ptr(), None, y.data_ptr(), None, 2, 4, 3, 0, 0, s, -1) == 1
+    assert lib.ti_v2_gemm_ex_f16(a.data_ptr(), b.data_ptr(), None, y.data_ptr(), None, 2, 4, 3, 0, 0, s, 7) == 2
+    assert b"device" in lib.ti_v2_last_error()
+    assert lib.ti_v2_layernorm_f16(a.data_ptr(), a.data_ptr(), a.data_ptr(), y.data_ptr(), 2, 3,
+                                   C.c_float(0.0), s, 0) == 1
+    assert lib.ti_v2_gelu_new_f16(a.data_ptr(), y.data_ptr(), 0, s, 0) == 1
+    m = t.zeros(1, dtype=t.int32, device="cuda")
+    assert lib.ti_v2_attention_f16(q.data_ptr(), q.data_ptr(), q.data_ptr(), q.data_ptr(), m.data_ptr(),
+                                   m.data_ptr(), m.data_ptr(), 1, 1, 1, 1, 64, 1, 2, s, 0) == 3
+    assert lib.ti_v2_attention_f16(q.data_ptr(), q.data_ptr(), q.data_ptr(), q.data_ptr(), m.data_ptr(),
+                                   m.data_ptr(), m.data_ptr(), 1, 1, 1, 1, 96, 1, 0, s, 0) == 1
+    assert lib.ti_v2_last_error() == b"invalid attention arguments"
+    t.cuda.synchronize()
+
+
+def test_non_default_stream_and_input_lifetime(ops):
+    """reference correctness.py:263-284: inputs allocated on the default stream,
+    consumed on a side stream behind queued work, then freed; record_stream keeps
+    their storage from being reused before the kernel ran."""
+    t = torch()
+    default = t.cuda.current_stream()
+    stream = t.cuda.Stream()
+    rng = np.random.default_rng(13)
+    an = f16(rng.standard_normal((33, 19)))
+    bn = f16(rng.standard_normal((19, 67)))
+    a, b = dev(an, t.float16), dev(bn, t.float16)
+    expected = h(an) @ h(bn)
+    stream.wait_stream(default)
+    say("stream lifetime")
+    with t.cuda.stream(stream):
+        blocker = t.ones((256, 256), device="cuda", dtype=t.float32) * 0.001
+        for _ in range(8):
+            blocker = blocker @ blocker
+        actual = ops.gemm(a, b, config=0, output_dtype=t.float32)
+    del a, b
+    gc.collect()
+    for _ in range(32):
+        tmp = t.empty((33, 19), device="cuda", dtype=t.float16)
+        tmp.fill_(123)
+        tmp2 = t.empty((19, 67), device="cuda", dtype=t.float16)
+        tmp2.fill_(124)
+    del tmp, tmp2, blocker
+    default.wait_stream(stream)
+    close(host(actual), expected)

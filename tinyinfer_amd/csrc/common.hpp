@@ -1,0 +1,73 @@
+// Shared device helpers for the gfx950 (CDNA4, wave64) kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tia {
+
+typedef _Float16 f16;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// fp16 bits <-> fp32.  The conversion to fp16 is v_cvt_f16_f32, which rounds to
+// nearest-even under the default wave mode register.
+__device__ __forceinline__ float h2f(uint16_t bits) { return float(__builtin_bit_cast(f16, bits)); }
+__device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, f16(v)); }
+__device__ __forceinline__ float rt16(float v) { return float(f16(v)); }
+
+// tanh-approximated GELU (GPT-2 "gelu_new"): 0.5 z (1 + tanh(sqrt(2/pi) (z + 0.044715 z^3))).
+// tanhf is ROCm's device libm.
+__device__ __forceinline__ float gelu_tanh(float z) {
+  return 0.5f * z * (1.f + tanhf(0.7978845608028654f * (z + 0.044715f * z * z * z)));
+}
+
+// Butterfly reductions across the 64 lanes of a wave.  Every lane ends with the
+// full result.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Reduction across a whole workgroup of NW waves through a small LDS array of
+// at least NW floats.  All threads return the total.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) lds[w] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += lds[i];
+  return t;
+}
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* lds) {
+  v = wave_max(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) lds[w] = v;
+  __syncthreads();
+  float t = lds[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) t = fmaxf(t, lds[i]);
+  return t;
+}
+
+}  // namespace tia

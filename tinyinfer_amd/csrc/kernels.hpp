@@ -1,0 +1,102 @@
+// Internal launcher interface shared by the v2 C ABI (backend_v2.hip), the
+// legacy ABI (backend_legacy.hip) and the GPT-2 runtime (llm_runtime.hip).
+// Everything here enqueues on the given stream and returns the launch status.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tia {
+
+// What a GEMM does with each finished fp32 accumulator C[m][n].
+enum EpiKind : int {
+  EPI_F16 = 0,       // y16[m][n] = fp16_rn(acc + bias[n])
+  EPI_F32 = 1,       // y32[m][n] = acc + bias[n]
+  EPI_GELU = 2,      // y16 = fp16_rn(gelu(fp16_rn(acc + bias)))
+  EPI_RESIDUAL = 3,  // y16 = fp16_rn(res[m][n] + fp16_rn(acc + bias)); res may alias y
+  EPI_RAW_F32 = 4,   // y32[m][n] = acc (the "separate" configs' workspace, no bias)
+  EPI_QKV = 5,       // EPI_F16 into y, plus K/V columns scattered into the slot cache
+};
+
+struct Epilogue {
+  int kind = EPI_F16;
+  const uint16_t* bias = nullptr;  // fp16 [N] or null
+  void* y = nullptr;
+  int64_t ldy = 0;                 // row stride of y, elements
+  const uint16_t* residual = nullptr;
+  int64_t ldr = 0;
+  // EPI_QKV: row m = b * qrows + t holds token t of request b; columns
+  // [hidden, 2 hidden) are K and [2 hidden, 3 hidden) are V, head h at h*64.
+  // Cache element ((((slot * layers + layer) * heads + h) * capacity + pos) * 64 + d),
+  // pos = offsets[b] + t, written only when t < qlens[b].
+  uint16_t* kcache = nullptr;
+  uint16_t* vcache = nullptr;
+  const int32_t* slots = nullptr;
+  const int32_t* offsets = nullptr;
+  const int32_t* qlens = nullptr;
+  int qrows = 1, hidden = 0, heads = 0, layer = 0, layers = 0, capacity = 0;
+};
+
+// Split-K partial sums and arrival counters used by the skinny (M <= 32) GEMM.
+// Counters must start at zero; every launch leaves them at zero again.
+struct Scratch {
+  float* partials = nullptr;
+  size_t partial_floats = 0;
+  int* counters = nullptr;
+  int counter_count = 0;
+};
+constexpr size_t kScratchPartialFloats = size_t(8) << 20;  // 32 MiB
+constexpr int kScratchCounters = 1 << 16;
+
+struct GemmArgs {
+  const uint16_t* a = nullptr;  // fp16 [M, lda]
+  int64_t lda = 0;
+  const void* w = nullptr;      // int8 or fp16 [K, N] row-major
+  bool w_int8 = true;
+  const float* scales = nullptr;  // fp32 [N] for int8 weights
+  int m = 0, n = 0, k = 0;
+  Epilogue epi;
+};
+
+hipError_t gemm(const GemmArgs& args, const Scratch* scratch, hipStream_t stream);
+// Per-(device, stream) scratch owned by the library, created on first use.
+// Returns nullptr (and sets *err) if it cannot be created.
+const Scratch* library_scratch(int device, hipStream_t stream, hipError_t* err);
+// y = ws + bias (fp16 or fp32 output): the separate-epilogue pass of configs 6..11.
+hipError_t bias_epilogue(const float* ws, const uint16_t* bias, void* y, int64_t count, int n,
+                         int dtype, hipStream_t stream);
+hipError_t legacy_gemm_f32(const float* a, const float* b, float* c, int m, int n, int k,
+                           hipStream_t stream);
+
+// Attention with generic strides (elements).  K/V of (b, h) start at
+// k + slot(b) * kv_sb + h * kv_sh with consecutive keys D elements apart, where
+// slot(b) = kv_slot ? kv_slot[b] : b.
+struct AttnArgs {
+  const uint16_t* q = nullptr;
+  int64_t q_sb = 0, q_sh = 0, q_sq = 0;
+  const uint16_t* k = nullptr;
+  const uint16_t* v = nullptr;
+  int64_t kv_sb = 0, kv_sh = 0;
+  const int32_t* kv_slot = nullptr;
+  uint16_t* out = nullptr;
+  int64_t o_sb = 0, o_sh = 0, o_sq = 0;
+  const int32_t* q_lengths = nullptr;
+  const int32_t* kv_lengths = nullptr;
+  const int32_t* offsets = nullptr;
+  int batch = 0, heads = 0, q_len = 0, kv_len = 0, head_dim = 64;
+  bool causal = true;
+  // kv_lengths[b] is ignored and offsets[b] + q_lengths[b] used instead when set
+  // (the runtime's slot cache: the visible length follows from the offset).
+  bool kv_from_offsets = false;
+};
+hipError_t attention(const AttnArgs& args, hipStream_t stream);
+
+hipError_t layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
+                         int rows, int cols, float eps, hipStream_t stream);
+hipError_t softmax_f16(const uint16_t* x, uint16_t* y, int rows, int cols, hipStream_t stream);
+hipError_t gelu_f16(const uint16_t* x, uint16_t* y, int64_t count, hipStream_t stream);
+hipError_t layernorm_f32(const float* x, const float* g, const float* b, float* y, int rows,
+                         int cols, float eps, hipStream_t stream);
+hipError_t softmax_f32(const float* x, float* y, int rows, int cols, hipStream_t stream);
+
+}  // namespace tia

@@ -1,0 +1,279 @@
+// Row-wise LayerNorm and last-axis Softmax (fp16 and fp32) and elementwise
+// tanh-GELU for gfx950.
+//
+// Rows up to 4096 columns take one wave per row: the row is read once into
+// registers with 16-byte loads, reduced with wave64 butterflies (no LDS, no
+// barriers), and written once — the HBM-minimal 2 x rows x cols x bytes.  Longer
+// or unaligned rows fall back to a 256-thread block per row that re-reads the
+// row from cache.  Semantics: LayerNorm y = (x - mean) * rsqrt(var + eps) * g + b
+// with two-pass mean/variance in fp32 (reference
+// kernels/src/cuda/tc/elementwise.cu:15-27, kernels/src/cuda/layernorm.cu:7-36);
+// softmax y = exp(x - max) / sum with -inf entries exactly 0 (reference
+// elementwise.cu:34-46, kernels/src/cuda/softmax.cu:19-53); fp16 storage rounds
+// to nearest-even.
+#include <algorithm>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace tia {
+namespace {
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
+};
+template <>
+struct Elem<uint16_t> {
+  static __device__ __forceinline__ float load(const uint16_t* p) { return h2f(*p); }
+  static __device__ __forceinline__ void store(uint16_t* p, float v) { *p = f2h(v); }
+};
+
+// VPL consecutive elements per lane per vector (16 bytes when VPL * sizeof(T) == 16).
+template <typename T, int VPL>
+__device__ __forceinline__ void load_vec(const T* p, float* out) {
+  if constexpr (VPL * sizeof(T) == 16) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[i] = __builtin_bit_cast(float, w[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) out[i] = h2f(uint16_t(w[i >> 1] >> (16 * (i & 1))));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) out[i] = Elem<T>::load(p + i);
+  }
+}
+template <typename T, int VPL>
+__device__ __forceinline__ void store_vec(T* p, const float* v) {
+  if constexpr (VPL * sizeof(T) == 16) {
+    uint32_t w[4];
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = __builtin_bit_cast(uint32_t, v[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = uint32_t(f2h(v[2 * i])) | (uint32_t(f2h(v[2 * i + 1])) << 16);
+    }
+    *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) Elem<T>::store(p + i, v[i]);
+  }
+}
+
+// One wave per row; lane l owns elements [VPL*l + 64*VPL*i, +VPL) for i < NV.
+template <typename T, int VPL, int NV>
+__global__ __launch_bounds__(256) void layernorm_wave(const T* x, const T* g, const T* b, T* y,
+                                                      int rows, int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + int64_t(row) * cols;
+  T* yr = y + int64_t(row) * cols;
+  float v[NV][VPL];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = VPL * lane + 64 * VPL * i;
+    if (c < cols) load_vec<T, VPL>(xr + c, v[i]);
+    else {
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) v[i][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) s += v[i][e];
+  }
+  const float mean = wave_sum(s) / float(cols);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = VPL * lane + 64 * VPL * i;
+    if (c < cols) {
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) {
+        const float d = v[i][e] - mean;
+        ss += d * d;
+      }
+    }
+  }
+  const float inv = rsqrtf(wave_sum(ss) / float(cols) + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = VPL * lane + 64 * VPL * i;
+    if (c < cols) {
+      float gv[VPL], bv[VPL], o[VPL];
+      load_vec<T, VPL>(g + c, gv);
+      load_vec<T, VPL>(b + c, bv);
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) o[e] = (v[i][e] - mean) * inv * gv[e] + bv[e];
+      store_vec<T, VPL>(yr + c, o);
+    }
+  }
+}
+
+template <typename T, int VPL, int NV>
+__global__ __launch_bounds__(256) void softmax_wave(const T* x, T* y, int rows, int cols) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + int64_t(row) * cols;
+  T* yr = y + int64_t(row) * cols;
+  const float ninf = -__builtin_huge_valf();
+  float v[NV][VPL];
+  float mx = ninf;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = VPL * lane + 64 * VPL * i;
+    if (c < cols) load_vec<T, VPL>(xr + c, v[i]);
+    else {
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) v[i][e] = ninf;
+    }
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) mx = fmaxf(mx, v[i][e]);
+  }
+  mx = wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) {
+      v[i][e] = __expf(v[i][e] - mx);
+      s += v[i][e];
+    }
+  const float inv = 1.f / wave_sum(s);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = VPL * lane + 64 * VPL * i;
+    if (c < cols) {
+      float o[VPL];
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) o[e] = v[i][e] * inv;
+      store_vec<T, VPL>(yr + c, o);
+    }
+  }
+}
+
+// Fallback: one 256-thread block per row, any width or alignment.
+template <typename T>
+__global__ __launch_bounds__(256) void layernorm_block(const T* x, const T* g, const T* b, T* y,
+                                                       int cols, float eps) {
+  __shared__ float lds[4];
+  const T* xr = x + int64_t(blockIdx.x) * cols;
+  T* yr = y + int64_t(blockIdx.x) * cols;
+  float s = 0.f;
+  for (int c = threadIdx.x; c < cols; c += 256) s += Elem<T>::load(xr + c);
+  const float mean = block_sum<4>(s, lds) / float(cols);
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    const float d = Elem<T>::load(xr + c) - mean;
+    ss += d * d;
+  }
+  const float inv = rsqrtf(block_sum<4>(ss, lds) / float(cols) + eps);
+  for (int c = threadIdx.x; c < cols; c += 256)
+    Elem<T>::store(yr + c, (Elem<T>::load(xr + c) - mean) * inv * Elem<T>::load(g + c) + Elem<T>::load(b + c));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_block(const T* x, T* y, int cols) {
+  __shared__ float lds[4];
+  const T* xr = x + int64_t(blockIdx.x) * cols;
+  T* yr = y + int64_t(blockIdx.x) * cols;
+  float mx = -__builtin_huge_valf();
+  for (int c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, Elem<T>::load(xr + c));
+  mx = block_max<4>(mx, lds);
+  float s = 0.f;
+  for (int c = threadIdx.x; c < cols; c += 256) s += __expf(Elem<T>::load(xr + c) - mx);
+  const float inv = 1.f / block_sum<4>(s, lds);
+  for (int c = threadIdx.x; c < cols; c += 256) Elem<T>::store(yr + c, __expf(Elem<T>::load(xr + c) - mx) * inv);
+}
+
+__global__ void gelu_kernel(const uint16_t* x, uint16_t* y, int64_t count, bool vec) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (vec) {
+    const int64_t nv = count / 8;
+    for (int64_t i = t; i < nv; i += stride) {
+      float v[8];
+      load_vec<uint16_t, 8>(x + 8 * i, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = gelu_tanh(v[e]);
+      store_vec<uint16_t, 8>(y + 8 * i, v);
+    }
+    for (int64_t i = nv * 8 + t; i < count; i += stride) y[i] = f2h(gelu_tanh(h2f(x[i])));
+  } else {
+    for (int64_t i = t; i < count; i += stride) y[i] = f2h(gelu_tanh(h2f(x[i])));
+  }
+}
+
+bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+template <typename T>
+hipError_t layernorm_dispatch(const T* x, const T* g, const T* b, T* y, int rows, int cols,
+                              float eps, hipStream_t st) {
+  constexpr int VPL = 16 / sizeof(T);
+  const bool vec = cols % VPL == 0 && al16(x) && al16(g) && al16(b) && al16(y);
+  const dim3 grid(unsigned((rows + 3) / 4)), block(256);
+  const int per = 64 * VPL;
+#define TIA_LN(V, NV) hipLaunchKernelGGL((layernorm_wave<T, V, NV>), grid, block, 0, st, x, g, b, y, rows, cols, eps)
+  if (vec && cols <= per) TIA_LN(VPL, 1);
+  else if (vec && cols <= 2 * per) TIA_LN(VPL, 2);
+  else if (vec && cols <= 4 * per) TIA_LN(VPL, 4);
+  else if (vec && cols <= 8 * per) TIA_LN(VPL, 8);
+  else if (vec && VPL == 4 && cols <= 16 * per) TIA_LN(VPL, 16);
+  else if (!vec && cols <= 64 * 16) TIA_LN(1, 16);
+  else hipLaunchKernelGGL((layernorm_block<T>), dim3(unsigned(rows)), block, 0, st, x, g, b, y, cols, eps);
+#undef TIA_LN
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t softmax_dispatch(const T* x, T* y, int rows, int cols, hipStream_t st) {
+  constexpr int VPL = 16 / sizeof(T);
+  const bool vec = cols % VPL == 0 && al16(x) && al16(y);
+  const dim3 grid(unsigned((rows + 3) / 4)), block(256);
+  const int per = 64 * VPL;
+#define TIA_SM(V, NV) hipLaunchKernelGGL((softmax_wave<T, V, NV>), grid, block, 0, st, x, y, rows, cols)
+  if (vec && cols <= per) TIA_SM(VPL, 1);
+  else if (vec && cols <= 2 * per) TIA_SM(VPL, 2);
+  else if (vec && cols <= 4 * per) TIA_SM(VPL, 4);
+  else if (vec && cols <= 8 * per) TIA_SM(VPL, 8);
+  else if (vec && VPL == 4 && cols <= 16 * per) TIA_SM(VPL, 16);
+  else if (!vec && cols <= 64 * 16) TIA_SM(1, 16);
+  else hipLaunchKernelGGL((softmax_block<T>), dim3(unsigned(rows)), block, 0, st, x, y, cols);
+#undef TIA_SM
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
+                         int rows, int cols, float eps, hipStream_t st) {
+  return layernorm_dispatch<uint16_t>(x, g, b, y, rows, cols, eps, st);
+}
+hipError_t softmax_f16(const uint16_t* x, uint16_t* y, int rows, int cols, hipStream_t st) {
+  return softmax_dispatch<uint16_t>(x, y, rows, cols, st);
+}
+hipError_t layernorm_f32(const float* x, const float* g, const float* b, float* y, int rows,
+                         int cols, float eps, hipStream_t st) {
+  return layernorm_dispatch<float>(x, g, b, y, rows, cols, eps, st);
+}
+hipError_t softmax_f32(const float* x, float* y, int rows, int cols, hipStream_t st) {
+  return softmax_dispatch<float>(x, y, rows, cols, st);
+}
+hipError_t gelu_f16(const uint16_t* x, uint16_t* y, int64_t count, hipStream_t st) {
+  const bool vec = al16(x) && al16(y);
+  const int64_t work = vec ? std::max<int64_t>(1, count / 8) : count;
+  const int64_t blocks = std::min<int64_t>((work + 255) / 256, 8192);
+  hipLaunchKernelGGL(gelu_kernel, dim3(unsigned(blocks)), dim3(256), 0, st, x, y, count, vec);
+  return hipGetLastError();
+}
+
+}  // namespace tia
