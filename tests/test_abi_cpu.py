@@ -15,9 +15,7 @@ from tinyinfer_amd import BACKEND_LIB, CODEC_LIB, LLM_LIB
 
 HEADERS = {"tinyinfer_backend_v2.h": BACKEND_LIB, "tinyinfer_backend.h": BACKEND_LIB,
            "tinyinfer_amd_ext.h": BACKEND_LIB,
-           "tinyinfer_host_codec.h": CODEC_LIB}
-if LLM_LIB.exists():
-    HEADERS["tinyinfer_llm.h"] = LLM_LIB
+           "tinyinfer_host_codec.h": CODEC_LIB, "tinyinfer_llm.h": LLM_LIB}
 
 
 def declared(header):

@@ -7,9 +7,11 @@
 //    with A padded to 16/32 rows.  A lane loads one dword (4 consecutive output
 //    columns) from 8 consecutive K rows, so the MFMA for "column slot" c covers
 //    columns {n0 + 4j + c}; the 4 waves of a workgroup split K, reduce through
-//    LDS, and workgroups split K further with fp32 partials and an arrival
-//    counter: the last workgroup of a column tile sums the partials in split
-//    order and runs the fused epilogue (bias / GELU / residual / KV scatter).
+//    LDS, and workgroups split K further: each writes fp32 partials and a
+//    second kernel sums them in split order and runs the fused epilogue (bias /
+//    GELU / residual / KV scatter).  (A single-kernel last-arrival reduction
+//    needs agent-scope release/acquire fences, which on the multi-XCD part
+//    write back and invalidate the whole L2 in every workgroup.)
 //  * tiled (M > 32, prefill): 64x64x32 tiles, A and the dequantised weight tile
 //    staged in LDS (weights transposed to [n][k] so both MFMA operands are one
 //    ds_read_b128 per lane), double buffered, same fused epilogues.
@@ -76,13 +78,13 @@ struct SkinnyParams {
   const void* w;
   const float* scales;
   int m, n, k;
+  int64_t ldw;         // row stride of W in elements (>= n)
   int ntile;           // ceil(N / 64)
   int steps;           // ceil(K / 32)
   int steps_per_block; // K steps owned by one workgroup (a multiple of 4)
   int splits;
   Epilogue epi;
   float* partials;     // [splits][M][N]
-  int* counters;       // [ntile]
 };
 
 constexpr int kSkinnyThreads = 256;
@@ -95,7 +97,7 @@ struct WFrag {
 };
 
 template <bool INT8, bool WVEC>
-__device__ __forceinline__ void load_wfrag(WFrag<INT8>& f, const void* w, int K, int N, int krow,
+__device__ __forceinline__ void load_wfrag(WFrag<INT8>& f, const void* w, int K, int N, int64_t LDW, int krow,
                                            int col) {
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
@@ -105,11 +107,11 @@ __device__ __forceinline__ void load_wfrag(WFrag<INT8>& f, const void* w, int K,
       uint32_t v = 0;
       if (k < K) {
         if constexpr (WVEC) {
-          if (col < N) v = *reinterpret_cast<const uint32_t*>(p + int64_t(k) * N + col);
+          if (col < N) v = *reinterpret_cast<const uint32_t*>(p + int64_t(k) * LDW + col);
         } else {
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            if (col + c < N) v |= uint32_t(uint8_t(p[int64_t(k) * N + col + c])) << (8 * c);
+            if (col + c < N) v |= uint32_t(uint8_t(p[int64_t(k) * LDW + col + c])) << (8 * c);
         }
       }
       f.d[r] = v;
@@ -119,7 +121,7 @@ __device__ __forceinline__ void load_wfrag(WFrag<INT8>& f, const void* w, int K,
       if (k < K) {
         if constexpr (WVEC) {
           if (col < N) {
-            const uint2 u = *reinterpret_cast<const uint2*>(p + int64_t(k) * N + col);
+            const uint2 u = *reinterpret_cast<const uint2*>(p + int64_t(k) * LDW + col);
             v0 = u.x;
             v1 = u.y;
           }
@@ -127,7 +129,7 @@ __device__ __forceinline__ void load_wfrag(WFrag<INT8>& f, const void* w, int K,
           uint16_t h[4] = {0, 0, 0, 0};
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            if (col + c < N) h[c] = p[int64_t(k) * N + col + c];
+            if (col + c < N) h[c] = p[int64_t(k) * LDW + col + c];
           v0 = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
           v1 = uint32_t(h[2]) | (uint32_t(h[3]) << 16);
         }
@@ -174,7 +176,6 @@ __device__ __forceinline__ half8_t afrag(const uint16_t* a, int64_t lda, int M, 
 template <bool INT8, int MT, bool WVEC, bool AVEC>
 __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) {
   __shared__ float red[4][MT * 16][65];
-  __shared__ int last_flag;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
 
@@ -203,8 +204,8 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) 
     WFrag<INT8> f0, f1;
     const int k0 = st * 32, k1 = (st + 4) * 32;
     const bool has1 = st + 4 < s_end;
-    load_wfrag<INT8, WVEC>(f0, p.w, p.k, p.n, k0 + 8 * g, col);
-    if (has1) load_wfrag<INT8, WVEC>(f1, p.w, p.k, p.n, k1 + 8 * g, col);
+    load_wfrag<INT8, WVEC>(f0, p.w, p.k, p.n, p.ldw, k0 + 8 * g, col);
+    if (has1) load_wfrag<INT8, WVEC>(f1, p.w, p.k, p.n, p.ldw, k1 + 8 * g, col);
     half8_t a0[MT], a1[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) a0[t] = afrag<AVEC>(p.a, p.lda, p.m, p.k, 16 * t + j, k0 + 8 * g);
@@ -238,42 +239,33 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) 
   __syncthreads();
 
   constexpr int kElems = MT * 16 * 64;
-  if (p.splits == 1) {
-    for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
-      const int row = e >> 6, cc = e & 63, n = n0 + cc;
-      if (row < p.m && n < p.n)
-        apply_epilogue(p.epi, row, n, red[0][row][cc] + red[1][row][cc] + red[2][row][cc] + red[3][row][cc]);
-    }
-    return;
-  }
   for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
     const int row = e >> 6, cc = e & 63, n = n0 + cc;
     if (row < p.m && n < p.n) {
       const float s = red[0][row][cc] + red[1][row][cc] + red[2][row][cc] + red[3][row][cc];
-      __hip_atomic_store(&p.partials[(int64_t(split) * p.m + row) * p.n + n], s, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      if (p.splits == 1) apply_epilogue(p.epi, row, n, s);
+      else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
     }
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int old = atomicAdd(&p.counters[tile], 1);
-    last_flag = (old == p.splits - 1);
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
-    const int row = e >> 6, cc = e & 63, n = n0 + cc;
-    if (row < p.m && n < p.n) {
-      float s = 0.f;
-      for (int sp = 0; sp < p.splits; ++sp)
-        s += __hip_atomic_load(&p.partials[(int64_t(sp) * p.m + row) * p.n + n], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-      apply_epilogue(p.epi, row, n, s);
+}
+
+// Second pass of a split-K launch: C[m][n] = sum of the split partials in split
+// order, then the epilogue.  The kernel boundary orders it after every partial.
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* partials, int splits, int m,
+                                                              int n, Epilogue epi) {
+  const int64_t total = int64_t(m) * n, stride = total;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
+    float s = 0.f;
+    int sp = 0;
+    for (; sp + 4 <= splits; sp += 4) {
+      const float a0 = partials[i + sp * stride], a1 = partials[i + (sp + 1) * stride];
+      const float a2 = partials[i + (sp + 2) * stride], a3 = partials[i + (sp + 3) * stride];
+      s = (((s + a0) + a1) + a2) + a3;
     }
+    for (; sp < splits; ++sp) s += partials[i + sp * stride];
+    const int row = int(i / n), col = int(i - int64_t(row) * n);
+    apply_epilogue(epi, row, col, s);
   }
-  if (threadIdx.x == 0) p.counters[tile] = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -285,6 +277,7 @@ struct TiledParams {
   const void* w;
   const float* scales;
   int m, n, k;
+  int64_t ldw;
   Epilogue epi;
 };
 constexpr int TBM = 64, TBN = 64, TBK = 32, TPAD = 40;  // LDS row pitch in halves
@@ -319,13 +312,13 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
         int8_t q[4] = {0, 0, 0, 0};
         if (k < p.k) {
           if (WVEC && col < p.n) {
-            const uint32_t v = *reinterpret_cast<const uint32_t*>(wp + int64_t(k) * p.n + col);
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(wp + int64_t(k) * p.ldw + col);
 #pragma unroll
             for (int c = 0; c < 4; ++c) q[c] = int8_t(v >> (8 * c));
           } else if (!WVEC) {
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-              if (col + c < p.n) q[c] = wp[int64_t(k) * p.n + col + c];
+              if (col + c < p.n) q[c] = wp[int64_t(k) * p.ldw + col + c];
           }
         }
 #pragma unroll
@@ -335,12 +328,12 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
         uint16_t h[4] = {0, 0, 0, 0};
         if (k < p.k) {
           if (WVEC && col < p.n) {
-            const uint2 u = *reinterpret_cast<const uint2*>(wp + int64_t(k) * p.n + col);
+            const uint2 u = *reinterpret_cast<const uint2*>(wp + int64_t(k) * p.ldw + col);
             h[0] = uint16_t(u.x); h[1] = uint16_t(u.x >> 16); h[2] = uint16_t(u.y); h[3] = uint16_t(u.y >> 16);
           } else if (!WVEC) {
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-              if (col + c < p.n) h[c] = wp[int64_t(k) * p.n + col + c];
+              if (col + c < p.n) h[c] = wp[int64_t(k) * p.ldw + col + c];
           }
         }
 #pragma unroll
@@ -463,6 +456,7 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   SkinnyParams p{};
   p.a = g.a; p.lda = g.lda; p.w = g.w; p.scales = g.scales;
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.ldw = g.ldw > 0 ? g.ldw : g.n;
   p.ntile = (g.n + 63) / 64;
   p.steps = (g.k + 31) / 32;
   // Choose the number of K splits: aim for ~2 workgroups per CU, at least 4
@@ -475,7 +469,6 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
     const int max_by_traffic = std::max(1, g.k / (16 * std::max(1, g.m)));
     splits = std::max(1, std::min(target, std::min(max_by_steps, max_by_traffic)));
     while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
-    if (p.ntile > s->counter_count) splits = 1;
   }
   int spb = (p.steps + splits - 1) / splits;
   spb = (spb + 3) / 4 * 4;
@@ -483,7 +476,6 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   p.steps_per_block = spb;
   p.splits = splits;
   p.partials = s ? s->partials : nullptr;
-  p.counters = s ? s->counters : nullptr;
   const dim3 grid(unsigned(p.ntile) * unsigned(splits));
 #define TIA_SKINNY(WV, AV) hipLaunchKernelGGL((skinny_kernel<INT8, MT, WV, AV>), grid, dim3(kSkinnyThreads), 0, stream, p)
   if (wvec && avec) TIA_SKINNY(true, true);
@@ -491,6 +483,12 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   else if (avec) TIA_SKINNY(false, true);
   else TIA_SKINNY(false, false);
 #undef TIA_SKINNY
+  if (splits > 1) {
+    const int64_t total = int64_t(g.m) * g.n;
+    const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 4096));
+    hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m,
+                       g.n, g.epi);
+  }
   return hipGetLastError();
 }
 
@@ -499,6 +497,7 @@ hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, hipStream_t str
   TiledParams p{};
   p.a = g.a; p.lda = g.lda; p.w = g.w; p.scales = g.scales;
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.ldw = g.ldw > 0 ? g.ldw : g.n;
   const dim3 grid(unsigned((g.n + TBN - 1) / TBN), unsigned((g.m + TBM - 1) / TBM));
 #define TIA_TILED(WV, AV) hipLaunchKernelGGL((tiled_kernel<INT8, WV, AV>), grid, dim3(256), 0, stream, p)
   if (wvec && avec) TIA_TILED(true, true);
@@ -514,7 +513,11 @@ hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, hipStream_t str
 hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream) {
   if (g.m <= 0 || g.n <= 0 || g.k <= 0) return hipErrorInvalidValue;
   const uintptr_t wp = reinterpret_cast<uintptr_t>(g.w), ap = reinterpret_cast<uintptr_t>(g.a);
-  const bool wvec = (g.n % 4 == 0) && (g.w_int8 ? wp % 4 == 0 : wp % 8 == 0);
+  // Whole 4-column groups may be loaded when rows are 4-aligned and the row
+  // pitch covers n rounded up to 4 (columns past n are padding, never stored).
+  const int64_t ldw = g.ldw > 0 ? g.ldw : g.n;
+  const bool wvec = ldw % 4 == 0 && ldw >= (int64_t(g.n) + 3) / 4 * 4 &&
+                    (g.w_int8 ? wp % 4 == 0 : wp % 8 == 0);
   const bool avec = (g.lda % 8 == 0) && (ap % 16 == 0);
   if (g.m <= 16) return g.w_int8 ? launch_skinny<true, 1>(g, wvec, avec, s, stream)
                                  : launch_skinny<false, 1>(g, wvec, avec, s, stream);
@@ -530,17 +533,18 @@ const Scratch* library_scratch(int device, hipStream_t stream, hipError_t* err) 
   auto it = table.find({device, stream});
   if (it != table.end()) return &it->second;
   Scratch s;
-  hipError_t e = hipMalloc(&s.partials, kScratchPartialFloats * sizeof(float));
-  if (e == hipSuccess) e = hipMalloc(&s.counters, kScratchCounters * sizeof(int));
-  if (e == hipSuccess) e = hipMemset(s.counters, 0, kScratchCounters * sizeof(int));
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &capture) == hipSuccess && capture != hipStreamCaptureStatusNone) {
+    // Allocation is not allowed under capture: the stream must run one call eagerly first.
+    *err = hipErrorStreamCaptureUnsupported;
+    return nullptr;
+  }
+  const hipError_t e = hipMalloc(&s.partials, kScratchPartialFloats * sizeof(float));
   if (e != hipSuccess) {
-    if (s.partials) (void)hipFree(s.partials);
-    if (s.counters) (void)hipFree(s.counters);
     *err = e;
     return nullptr;
   }
   s.partial_floats = kScratchPartialFloats;
-  s.counter_count = kScratchCounters;
   return &(table[{device, stream}] = s);
 }
 

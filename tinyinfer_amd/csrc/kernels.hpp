@@ -37,16 +37,13 @@ struct Epilogue {
   int qrows = 1, hidden = 0, heads = 0, layer = 0, layers = 0, capacity = 0;
 };
 
-// Split-K partial sums and arrival counters used by the skinny (M <= 32) GEMM.
-// Counters must start at zero; every launch leaves them at zero again.
+// Split-K partial sums of the skinny (M <= 32) GEMM: [splits][M][N] fp32.
+// Launches that share one Scratch must be ordered (same stream).
 struct Scratch {
   float* partials = nullptr;
   size_t partial_floats = 0;
-  int* counters = nullptr;
-  int counter_count = 0;
 };
 constexpr size_t kScratchPartialFloats = size_t(8) << 20;  // 32 MiB
-constexpr int kScratchCounters = 1 << 16;
 
 struct GemmArgs {
   const uint16_t* a = nullptr;  // fp16 [M, lda]
@@ -55,12 +52,14 @@ struct GemmArgs {
   bool w_int8 = true;
   const float* scales = nullptr;  // fp32 [N] for int8 weights
   int m = 0, n = 0, k = 0;
+  int64_t ldw = 0;                // row stride of W in elements; 0 means n
   Epilogue epi;
 };
 
 hipError_t gemm(const GemmArgs& args, const Scratch* scratch, hipStream_t stream);
-// Per-(device, stream) scratch owned by the library, created on first use.
-// Returns nullptr (and sets *err) if it cannot be created.
+// Per-(device, stream) scratch owned by the library, created on the first call
+// on that stream (never under graph capture).  Returns nullptr and sets *err if
+// it cannot be created.
 const Scratch* library_scratch(int device, hipStream_t stream, hipError_t* err);
 // y = ws + bias (fp16 or fp32 output): the separate-epilogue pass of configs 6..11.
 hipError_t bias_epilogue(const float* ws, const uint16_t* bias, void* y, int64_t count, int n,

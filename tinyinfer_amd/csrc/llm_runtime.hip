@@ -1,0 +1,787 @@
+// libtinyinfer_llm.so: the GPT-2 runtime ABI (include/tinyinfer_llm.h) on gfx950.
+//
+// Semantics follow reference llm/src/runtime.cu:86-211 (validation rules,
+// absolute positions, greedy loop, poisoning, internal scoring slot, trace
+// counters); the execution plan is MI355X-native:
+//  * per layer five launches: LN1 -> c_attn GEMM whose epilogue also writes K/V
+//    into the slot cache (no split/scatter/gather/pack kernels) -> attention
+//    reading the [slot][layer][head][pos][64] cache in place and writing merged
+//    heads -> c_proj GEMM + residual (in place) -> LN2 -> c_fc GEMM + GELU ->
+//    mlp.c_proj GEMM + residual (in place);
+//  * ln_f runs on the last row of each request only, the lm_head GEMM writes
+//    fp32 logits, a block-per-row argmax picks the lowest id on ties;
+//  * a decode step (every request appends one token) is captured once per
+//    batch size into a hipGraph whose kernels read all lengths, offsets and slots
+//    from device memory, so later steps are one graph launch between a pinned
+//    H2D copy of the step metadata and a D2H copy of the next tokens.
+#include <algorithm>
+#include <chrono>
+#include <climits>
+#include <cmath>
+#include <map>
+#include <memory>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/tinyinfer_backend_v2.h"
+#include "../../include/tinyinfer_llm.h"
+#include "artifact.hpp"
+#include "common.hpp"
+#include "kernels.hpp"
+
+using tia::art::Invalid;
+using tia::art::IOError;
+
+namespace {
+
+thread_local std::string error_text;
+constexpr int kScoreRows = 16;
+constexpr int kHeadDim = 64;
+
+struct GpuError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+void ck(hipError_t e) {
+  if (e != hipSuccess) throw GpuError(hipGetErrorString(e));
+}
+
+struct DeviceScope {
+  int previous = -1;
+  bool changed = false;
+  explicit DeviceScope(int device) {
+    ck(hipGetDevice(&previous));
+    if (previous != device) {
+      ck(hipSetDevice(device));
+      changed = true;
+    }
+  }
+  ~DeviceScope() {
+    if (changed) (void)hipSetDevice(previous);
+  }
+};
+
+// ---------------------------------------------------------------- kernels
+// x[row] = fp16(wte[id] + wpe[offset + t]) for t < qlens[b], else 0
+// (reference runtime.cu:25-30); 8 halves per thread.
+__global__ void embed_kernel(const int32_t* ids, const int32_t* qlens, const int32_t* offsets,
+                             const uint16_t* wte, const uint16_t* wpe, uint16_t* x, int rows, int qlen,
+                             int hidden) {
+  const int per_row = hidden / 8;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= int64_t(rows) * per_row) return;
+  const int row = int(i / per_row), c = int(i % per_row) * 8;
+  const int b = row / qlen, t = row - b * qlen;
+  tia::half8_t out;
+  if (t < qlens[b]) {
+    const tia::half8_t e = *reinterpret_cast<const tia::half8_t*>(wte + int64_t(ids[row]) * hidden + c);
+    const tia::half8_t p = *reinterpret_cast<const tia::half8_t*>(wpe + int64_t(offsets[b] + t) * hidden + c);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = tia::f16(float(e[k]) + float(p[k]));
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = tia::f16(0.f);
+  }
+  *reinterpret_cast<tia::half8_t*>(x + int64_t(row) * hidden + c) = out;
+}
+
+// out[b] = x[b * qlen + qlens[b] - 1] (reference runtime.cu:56-58).
+__global__ void gather_last_kernel(const uint16_t* x, uint16_t* out, const int32_t* qlens, int batch,
+                                   int qlen, int hidden) {
+  const int per_row = hidden / 8;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= batch * per_row) return;
+  const int b = i / per_row, c = (i % per_row) * 8;
+  *reinterpret_cast<tia::half8_t*>(out + int64_t(b) * hidden + c) =
+      *reinterpret_cast<const tia::half8_t*>(x + (int64_t(b) * qlen + qlens[b] - 1) * hidden + c);
+}
+
+// Greedy id per row: largest logit, lowest id on ties (reference runtime.cu:59-66).
+__global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int32_t* out, int vocab) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const float* row = logits + int64_t(blockIdx.x) * vocab;
+  float best = -__builtin_huge_valf();
+  int idx = INT_MAX;
+  for (int j = threadIdx.x; j < vocab; j += 256) {
+    const float v = row[j];
+    if (v > best) {  // j increases, so equality keeps the lower id
+      best = v;
+      idx = j;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (ov > best || (ov == best && oi < idx)) {
+      best = ov;
+      idx = oi;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = best;
+    si[threadIdx.x >> 6] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (sv[w] > best || (sv[w] == best && si[w] < idx)) {
+        best = sv[w];
+        idx = si[w];
+      }
+    out[blockIdx.x] = idx;
+  }
+}
+
+// Shifted-target NLL of one row in fp64 (reference runtime.cu:67-76).
+__global__ __launch_bounds__(256) void nll_kernel(const float* logits, const int32_t* tokens,
+                                                  const uint8_t* mask, double* loss, int first_position,
+                                                  int vocab) {
+  __shared__ float smax[4];
+  __shared__ double ssum[4];
+  const int row = blockIdx.x, pos = first_position + row;
+  const float* l = logits + int64_t(row) * vocab;
+  float m = -__builtin_huge_valf();
+  for (int j = threadIdx.x; j < vocab; j += 256) m = fmaxf(m, l[j]);
+  m = tia::wave_max(m);
+  if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+  double s = 0;
+  for (int j = threadIdx.x; j < vocab; j += 256) s += exp(double(l[j]) - double(m));
+  s = tia::wave_sum_d(s);
+  if ((threadIdx.x & 63) == 0) ssum[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const double total = ssum[0] + ssum[1] + ssum[2] + ssum[3];
+    loss[pos] = mask[pos] ? double(m) + log(total) - double(l[tokens[pos]]) : 0.0;
+  }
+}
+
+__global__ __launch_bounds__(256) void sum_kernel(const double* v, double* out, int n) {
+  __shared__ double s[4];
+  double acc = 0;
+  for (int i = threadIdx.x; i < n; i += 256) acc += v[i];
+  acc = tia::wave_sum_d(acc);
+  if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) *out = s[0] + s[1] + s[2] + s[3];
+}
+
+__global__ void zero_f64_kernel(double* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0;
+}
+
+unsigned blocks_for(int64_t n, int per = 256) { return unsigned((n + per - 1) / per); }
+using Clock = std::chrono::steady_clock;
+double ms_since(Clock::time_point t0) {
+  return std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+}
+
+}  // namespace
+
+struct ti_llm_model {
+  struct Linear {
+    const void* w = nullptr;
+    const float* scales = nullptr;
+    const uint16_t* bias = nullptr;
+    int k = 0, n = 0;
+    int64_t ldw = 0;
+  };
+
+  ti_llm_options opt{};
+  hipStream_t stream = nullptr;
+  bool poisoned = false;
+  bool quantized = true;
+  tia::art::Arch arch;
+  int L = 0, NH = 0, H = 0, V = 0;
+  std::vector<void*> allocations;
+  void* pinned = nullptr;
+  std::vector<Linear> c_attn, c_proj, c_fc, c_proj2;
+  Linear head;
+  const uint16_t *wte = nullptr, *wpe = nullptr, *lnf_g = nullptr, *lnf_b = nullptr;
+  std::vector<const uint16_t*> ln1_g, ln1_b, ln2_g, ln2_b;
+  uint16_t *x = nullptr, *norm = nullptr, *qkv = nullptr, *attn = nullptr, *mlp = nullptr, *last = nullptr;
+  uint16_t *kc = nullptr, *vc = nullptr;
+  float* logits = nullptr;
+  int32_t *d_meta = nullptr, *d_ids = nullptr, *d_slots = nullptr, *d_qlens = nullptr, *d_offsets = nullptr;
+  int32_t *d_next = nullptr, *d_score_tokens = nullptr;
+  uint8_t* d_score_mask = nullptr;
+  double *d_loss = nullptr, *d_loss_sum = nullptr;
+  int32_t *h_meta = nullptr, *h_ids = nullptr, *h_slots = nullptr, *h_qlens = nullptr, *h_offsets = nullptr;
+  int32_t* h_next = nullptr;
+  size_t meta_ints = 0;
+  tia::Scratch scratch;
+  std::vector<int32_t> lengths;
+  ti_llm_trace trace{};
+  std::map<int, hipGraphExec_t> decode_graphs;
+
+  template <class T>
+  T* alloc(size_t count) {
+    void* p = nullptr;
+    ck(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)));
+    allocations.push_back(p);
+    return static_cast<T*>(p);
+  }
+
+  ~ti_llm_model() {
+    int previous = -1;
+    (void)hipGetDevice(&previous);
+    (void)hipSetDevice(opt.device);
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& g : decode_graphs) (void)hipGraphExecDestroy(g.second);
+    for (void* p : allocations) (void)hipFree(p);
+    if (pinned) (void)hipHostFree(pinned);
+    if (stream) (void)hipStreamDestroy(stream);
+    if (previous >= 0) (void)hipSetDevice(previous);
+  }
+
+  void check() const {
+    if (poisoned) throw GpuError("model poisoned by an earlier execution failure; destroy and recreate it");
+  }
+
+  void init(const tia::art::Artifact& a) {
+    arch = a.arch;
+    L = arch.layers;
+    NH = arch.heads;
+    H = arch.hidden;
+    V = arch.vocab;
+    if (opt.capacity > arch.capacity) throw Invalid("capacity exceeds the model's position table");
+    quantized = a.precision == "int8";
+    const std::string lin = quantized ? "int8" : "float16";
+    std::set<std::string> used;
+    uint8_t* base = alloc<uint8_t>(a.binary.size());
+    ck(hipMemcpy(base, a.binary.data(), a.binary.size(), hipMemcpyHostToDevice));
+    auto tensor = [&](const std::string& name, std::vector<int> shape, const std::string& dtype) {
+      const auto& t = a.require(name, shape, dtype);
+      used.insert(name);
+      return static_cast<const void*>(base + t.offset);
+    };
+    auto half = [&](const std::string& name, std::vector<int> shape) {
+      return static_cast<const uint16_t*>(tensor(name, shape, "float16"));
+    };
+    wte = half("transformer.wte.weight", {V, H});
+    wpe = half("transformer.wpe.weight", {arch.capacity, H});
+    lnf_g = half("transformer.ln_f.weight", {H});
+    lnf_b = half("transformer.ln_f.bias", {H});
+    auto linear = [&](const std::string& p, int k, int n) {
+      Linear l;
+      l.k = k;
+      l.n = n;
+      l.ldw = n;
+      l.w = tensor(p + ".weight", {k, n}, lin);
+      l.bias = half(p + ".bias", {n});
+      if (quantized) l.scales = static_cast<const float*>(tensor(p + ".weight.scales", {n}, "float32"));
+      return l;
+    };
+    for (int l = 0; l < L; ++l) {
+      const std::string p = "transformer.h." + std::to_string(l) + ".";
+      ln1_g.push_back(half(p + "ln_1.weight", {H}));
+      ln1_b.push_back(half(p + "ln_1.bias", {H}));
+      ln2_g.push_back(half(p + "ln_2.weight", {H}));
+      ln2_b.push_back(half(p + "ln_2.bias", {H}));
+      c_attn.push_back(linear(p + "attn.c_attn", H, 3 * H));
+      c_proj.push_back(linear(p + "attn.c_proj", H, H));
+      c_fc.push_back(linear(p + "mlp.c_fc", H, 4 * H));
+      c_proj2.push_back(linear(p + "mlp.c_proj", 4 * H, H));
+    }
+    // The tied head [H, V] gets a 64-column-aligned row pitch so every row is
+    // dword aligned for the vectorized weight loads.
+    {
+      const size_t width = quantized ? 1 : 2;
+      const void* src = tensor("lm_head.weight", {H, V}, lin);
+      (void)src;
+      const auto& t = a.require("lm_head.weight", {H, V}, lin);
+      head.k = H;
+      head.n = V;
+      head.ldw = (int64_t(V) + 63) / 64 * 64;
+      uint8_t* padded = alloc<uint8_t>(size_t(H) * size_t(head.ldw) * width);
+      ck(hipMemset(padded, 0, size_t(H) * size_t(head.ldw) * width));
+      ck(hipMemcpy2D(padded, size_t(head.ldw) * width, a.binary.data() + t.offset, size_t(V) * width,
+                     size_t(V) * width, size_t(H), hipMemcpyHostToDevice));
+      head.w = padded;
+      if (quantized) head.scales = static_cast<const float*>(tensor("lm_head.weight.scales", {V}, "float32"));
+    }
+    if (used.size() != a.tensors.size()) throw Invalid("unexpected tensor(s) in artifact");
+
+    const size_t rows = size_t(opt.max_batch) * opt.capacity;
+    x = alloc<uint16_t>(rows * H);
+    norm = alloc<uint16_t>(rows * H);
+    qkv = alloc<uint16_t>(rows * 3 * H);
+    attn = alloc<uint16_t>(rows * H);
+    mlp = alloc<uint16_t>(rows * 4 * H);
+    last = alloc<uint16_t>(size_t(std::max(opt.max_batch, kScoreRows)) * H);
+    const size_t cache = size_t(opt.cache_slots + 1) * L * NH * opt.capacity * kHeadDim;
+    kc = alloc<uint16_t>(cache);
+    vc = alloc<uint16_t>(cache);
+    logits = alloc<float>(size_t(std::max(opt.max_batch, kScoreRows)) * V);
+    // Step metadata: ids[rows] | slots[B] | qlens[B] | offsets[B], mirrored in pinned host memory.
+    meta_ints = rows + 3 * size_t(opt.max_batch);
+    d_meta = alloc<int32_t>(meta_ints);
+    d_ids = d_meta;
+    d_slots = d_ids + rows;
+    d_qlens = d_slots + opt.max_batch;
+    d_offsets = d_qlens + opt.max_batch;
+    d_next = alloc<int32_t>(opt.max_batch);
+    d_score_tokens = alloc<int32_t>(opt.capacity);
+    d_score_mask = alloc<uint8_t>(opt.capacity);
+    d_loss = alloc<double>(opt.capacity);
+    d_loss_sum = alloc<double>(1);
+    ck(hipHostMalloc(&pinned, (meta_ints + opt.max_batch) * sizeof(int32_t), hipHostMallocDefault));
+    h_meta = static_cast<int32_t*>(pinned);
+    h_ids = h_meta;
+    h_slots = h_ids + rows;
+    h_qlens = h_slots + opt.max_batch;
+    h_offsets = h_qlens + opt.max_batch;
+    h_next = h_meta + meta_ints;
+    scratch.partials = alloc<float>(tia::kScratchPartialFloats);
+    scratch.partial_floats = tia::kScratchPartialFloats;
+    lengths.assign(opt.cache_slots + 1, 0);
+    ck(hipStreamSynchronize(stream));
+  }
+
+  // ---------------------------------------------------------------- launch helpers
+  void gemm(const uint16_t* a, int m, const Linear& w, tia::Epilogue epi) {
+    tia::GemmArgs g;
+    g.a = a;
+    g.lda = w.k;
+    g.w = w.w;
+    g.w_int8 = quantized;
+    g.scales = w.scales;
+    g.m = m;
+    g.n = w.n;
+    g.k = w.k;
+    g.ldw = w.ldw;
+    g.epi = epi;
+    ck(tia::gemm(g, &scratch, stream));
+  }
+
+  // One pass of the transformer over rows [b, qlen] whose metadata is already on
+  // the device; leaves the residual stream in x.
+  void layers(int b, int qlen) {
+    const int rows = b * qlen;
+    embed_kernel<<<blocks_for(int64_t(rows) * H / 8), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, x,
+                                                                          rows, qlen, H);
+    ck(hipGetLastError());
+    for (int l = 0; l < L; ++l) {
+      ck(tia::layernorm_f16(x, ln1_g[l], ln1_b[l], norm, rows, H, 1e-5f, stream));
+      tia::Epilogue e;
+      e.kind = tia::EPI_QKV;
+      e.bias = c_attn[l].bias;
+      e.y = qkv;
+      e.ldy = 3 * H;
+      e.kcache = kc;
+      e.vcache = vc;
+      e.slots = d_slots;
+      e.offsets = d_offsets;
+      e.qlens = d_qlens;
+      e.qrows = qlen;
+      e.hidden = H;
+      e.heads = NH;
+      e.layer = l;
+      e.layers = L;
+      e.capacity = opt.capacity;
+      gemm(norm, rows, c_attn[l], e);
+
+      tia::AttnArgs at;
+      const int64_t head_stride = int64_t(opt.capacity) * kHeadDim;
+      at.q = qkv;
+      at.q_sb = int64_t(qlen) * 3 * H;
+      at.q_sh = kHeadDim;
+      at.q_sq = 3 * H;
+      at.k = kc + int64_t(l) * NH * head_stride;
+      at.v = vc + int64_t(l) * NH * head_stride;
+      at.kv_sb = int64_t(L) * NH * head_stride;
+      at.kv_sh = head_stride;
+      at.kv_slot = d_slots;
+      at.out = attn;
+      at.o_sb = int64_t(qlen) * H;
+      at.o_sh = kHeadDim;
+      at.o_sq = H;
+      at.q_lengths = d_qlens;
+      at.kv_lengths = d_qlens;
+      at.offsets = d_offsets;
+      at.kv_from_offsets = true;
+      at.batch = b;
+      at.heads = NH;
+      at.q_len = qlen;
+      at.kv_len = opt.capacity;
+      at.head_dim = kHeadDim;
+      at.causal = true;
+      ck(tia::attention(at, stream));
+
+      tia::Epilogue r;
+      r.kind = tia::EPI_RESIDUAL;
+      r.bias = c_proj[l].bias;
+      r.y = x;
+      r.ldy = H;
+      r.residual = x;
+      r.ldr = H;
+      gemm(attn, rows, c_proj[l], r);
+      ck(tia::layernorm_f16(x, ln2_g[l], ln2_b[l], norm, rows, H, 1e-5f, stream));
+      tia::Epilogue gl;
+      gl.kind = tia::EPI_GELU;
+      gl.bias = c_fc[l].bias;
+      gl.y = mlp;
+      gl.ldy = 4 * H;
+      gemm(norm, rows, c_fc[l], gl);
+      r.bias = c_proj2[l].bias;
+      gemm(mlp, rows, c_proj2[l], r);
+    }
+  }
+
+  // ln_f of each request's last row, fp32 logits without bias, argmax.
+  void head_and_argmax(int b, int qlen, bool greedy) {
+    const uint16_t* rows_in = x;
+    if (qlen > 1) {
+      gather_last_kernel<<<blocks_for(int64_t(b) * H / 8), 256, 0, stream>>>(x, last, d_qlens, b, qlen, H);
+      ck(hipGetLastError());
+      rows_in = last;
+    }
+    ck(tia::layernorm_f16(rows_in, lnf_g, lnf_b, norm, b, H, 1e-5f, stream));
+    tia::Epilogue e;
+    e.kind = tia::EPI_F32;
+    e.y = logits;
+    e.ldy = V;
+    gemm(norm, b, head, e);
+    if (greedy) {
+      argmax_kernel<<<b, 256, 0, stream>>>(logits, d_next, V);
+      ck(hipGetLastError());
+    }
+  }
+
+  void count_forward(bool head_used, bool greedy) {
+    ++trace.forward_calls;
+    ++trace.embedding;
+    for (int l = 0; l < L; ++l) {
+      trace.layernorm += 2;
+      if (quantized) trace.gemm_int8 += 4;
+      else trace.gemm_fp16 += 4;
+      ++trace.kv_scatter_gather;
+      ++trace.attention;
+      trace.residual += 2;
+      ++trace.gelu;
+    }
+    ++trace.layernorm;  // ln_f
+    if (head_used) {
+      ++trace.lm_head;
+      if (quantized) ++trace.gemm_int8;
+      else ++trace.gemm_fp16;
+    }
+    if (greedy) ++trace.argmax;
+  }
+
+  void upload_meta(int b, int qlen) {
+    const size_t rows = size_t(opt.max_batch) * opt.capacity;
+    ck(hipMemcpyAsync(d_ids, h_ids, size_t(b) * qlen * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+    ck(hipMemcpyAsync(d_slots, h_slots, 3 * size_t(opt.max_batch) * sizeof(int32_t), hipMemcpyHostToDevice,
+                      stream));
+    (void)rows;
+  }
+
+  void decode_step_graph(int b) {
+    auto it = decode_graphs.find(b);
+    if (it == decode_graphs.end()) {
+      hipGraph_t graph = nullptr;
+      ck(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+      try {
+        layers(b, 1);
+        head_and_argmax(b, 1, true);
+      } catch (...) {
+        hipGraph_t dropped = nullptr;
+        (void)hipStreamEndCapture(stream, &dropped);
+        if (dropped) (void)hipGraphDestroy(dropped);
+        throw;
+      }
+      ck(hipStreamEndCapture(stream, &graph));
+      hipGraphExec_t exec = nullptr;
+      const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      ck(e);
+      it = decode_graphs.emplace(b, exec).first;
+    }
+    ck(hipGraphLaunch(it->second, stream));
+  }
+
+  // reference runtime.cu:157-168
+  void forward(const int32_t* s, const int32_t* tokens, const int32_t* lens, int b, int stride, float* out,
+               int32_t* greedy, bool internal = false) {
+    check();
+    if (!s || !tokens || !lens || b < 1 || b > opt.max_batch || stride < 1 || stride > opt.capacity)
+      throw Invalid("invalid batch/host pointers/stride");
+    std::set<int32_t> unique;
+    int qlen = 0;
+    for (int i = 0; i < b; ++i) {
+      if (s[i] < 0 || s[i] >= opt.cache_slots + (internal ? 1 : 0) || !unique.insert(s[i]).second || lens[i] < 1 ||
+          lens[i] > stride || lengths[s[i]] + lens[i] > opt.capacity)
+        throw Invalid("duplicate/invalid slot, length or capacity");
+      qlen = std::max(qlen, lens[i]);
+      for (int j = 0; j < lens[i]; ++j)
+        if (tokens[int64_t(i) * stride + j] < 0 || tokens[int64_t(i) * stride + j] >= V)
+          throw Invalid("token ID outside the model vocabulary");
+    }
+    for (int i = 0; i < b; ++i) {
+      for (int j = 0; j < qlen; ++j) h_ids[int64_t(i) * qlen + j] = j < lens[i] ? tokens[int64_t(i) * stride + j] : 0;
+      h_slots[i] = s[i];
+      h_qlens[i] = lens[i];
+      h_offsets[i] = lengths[s[i]];
+    }
+    const bool need_head = out || greedy;
+    upload_meta(b, qlen);
+    if (qlen == 1 && greedy) {
+      decode_step_graph(b);
+    } else {
+      layers(b, qlen);
+      if (need_head) head_and_argmax(b, qlen, greedy != nullptr);
+    }
+    count_forward(need_head, greedy != nullptr);
+    if (out) ck(hipMemcpyAsync(out, logits, size_t(b) * V * sizeof(float), hipMemcpyDeviceToHost, stream));
+    if (greedy) ck(hipMemcpyAsync(h_next, d_next, size_t(b) * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    ck(hipStreamSynchronize(stream));
+    if (greedy) std::copy(h_next, h_next + b, greedy);
+    for (int i = 0; i < b; ++i) lengths[s[i]] += lens[i];
+  }
+
+  // reference runtime.cu:204-211
+  void score(const int32_t* tokens, const uint8_t* mask, int length, double* nll, uint64_t* count, double* positions) {
+    check();
+    if (!tokens || !mask || !nll || !count || length < 2 || length > opt.capacity || mask[0])
+      throw Invalid("invalid score window");
+    uint64_t targets = 0;
+    for (int i = 0; i < length; ++i) {
+      if (tokens[i] < 0 || tokens[i] >= V || mask[i] > 1) throw Invalid("invalid score token/mask");
+      targets += mask[i];
+    }
+    if (!targets) throw Invalid("no shifted targets selected");
+    const int slot = opt.cache_slots, q = length - 1;
+    lengths[slot] = 0;
+    std::copy(tokens, tokens + q, h_ids);
+    h_slots[0] = slot;
+    h_qlens[0] = q;
+    h_offsets[0] = 0;
+    upload_meta(1, q);
+    layers(1, q);
+    ck(tia::layernorm_f16(x, lnf_g, lnf_b, norm, q, H, 1e-5f, stream));
+    ++trace.forward_calls;
+    ++trace.embedding;
+    trace.layernorm += 2 * L + 1;
+    (quantized ? trace.gemm_int8 : trace.gemm_fp16) += 4 * L;
+    trace.kv_scatter_gather += L;
+    trace.attention += L;
+    trace.residual += 2 * L;
+    trace.gelu += L;
+    ck(hipMemcpyAsync(d_score_tokens, tokens, size_t(length) * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+    ck(hipMemcpyAsync(d_score_mask, mask, size_t(length), hipMemcpyHostToDevice, stream));
+    zero_f64_kernel<<<blocks_for(length), 256, 0, stream>>>(d_loss, length);
+    ck(hipGetLastError());
+    for (int row = 0; row < q; row += kScoreRows) {
+      const int rows = std::min(kScoreRows, q - row);
+      ++trace.lm_head;
+      (quantized ? trace.gemm_int8 : trace.gemm_fp16) += 1;
+      tia::Epilogue e;
+      e.kind = tia::EPI_F32;
+      e.y = logits;
+      e.ldy = V;
+      gemm(norm + int64_t(row) * H, rows, head, e);
+      ++trace.nll;
+      nll_kernel<<<rows, 256, 0, stream>>>(logits, d_score_tokens, d_score_mask, d_loss, row + 1, V);
+      ck(hipGetLastError());
+    }
+    sum_kernel<<<1, 256, 0, stream>>>(d_loss, d_loss_sum, length);
+    ck(hipGetLastError());
+    ck(hipMemcpyAsync(nll, d_loss_sum, sizeof(double), hipMemcpyDeviceToHost, stream));
+    if (positions) ck(hipMemcpyAsync(positions, d_loss, size_t(length) * sizeof(double), hipMemcpyDeviceToHost, stream));
+    ck(hipStreamSynchronize(stream));
+    if (!std::isfinite(*nll) || *nll < 0) throw GpuError("non-finite or negative NLL");
+    *count = targets;
+  }
+};
+
+namespace {
+template <class F>
+int api(ti_llm_model* m, F&& fn) {
+  error_text.clear();
+  try {
+    if (!m) throw Invalid("null model");
+    DeviceScope scope(m->opt.device);
+    m->check();
+    fn();
+    return TI_LLM_OK;
+  } catch (const Invalid& e) {
+    error_text = e.what();
+    return TI_LLM_INVALID;
+  } catch (const IOError& e) {
+    error_text = e.what();
+    return TI_LLM_IO;
+  } catch (const GpuError& e) {
+    if (m) m->poisoned = true;
+    error_text = e.what();
+    return TI_LLM_CUDA;
+  } catch (const std::exception& e) {
+    if (m) m->poisoned = true;
+    error_text = e.what();
+    return TI_LLM_INTERNAL;
+  } catch (...) {
+    if (m) m->poisoned = true;
+    error_text = "unknown native failure";
+    return TI_LLM_INTERNAL;
+  }
+}
+}  // namespace
+
+extern "C" int ti_llm_abi_version(void) { return 1; }
+extern "C" const char* ti_llm_last_error(void) { return error_text.c_str(); }
+
+extern "C" int ti_llm_create(const char* path, const ti_llm_options* o, ti_llm_model** out) {
+  error_text.clear();
+  if (out) *out = nullptr;
+  try {
+    if (!path || !o || !out || o->struct_size != sizeof(ti_llm_options) || o->device < 0 || o->max_batch < 1 ||
+        o->max_batch > 32 || o->cache_slots < o->max_batch || o->cache_slots > 1024 || o->capacity < 2 ||
+        o->capacity > 1024 || o->gemm_config < 0 || o->gemm_config > 11 || o->attention_config < 0 ||
+        o->attention_config > 1)
+      throw Invalid("invalid options/ABI size");
+    if (ti_v2_abi_version() != 2) throw Invalid("v2 kernel ABI required");
+    const tia::art::Artifact artifact = tia::art::load_artifact(path);
+    DeviceScope scope(o->device);
+    auto model = std::make_unique<ti_llm_model>();
+    model->opt = *o;
+    ck(hipStreamCreateWithFlags(&model->stream, hipStreamNonBlocking));
+    model->init(artifact);
+    *out = model.release();
+    return TI_LLM_OK;
+  } catch (const Invalid& e) {
+    error_text = e.what();
+    return TI_LLM_INVALID;
+  } catch (const IOError& e) {
+    error_text = e.what();
+    return TI_LLM_IO;
+  } catch (const GpuError& e) {
+    error_text = e.what();
+    return TI_LLM_CUDA;
+  } catch (const std::exception& e) {
+    error_text = e.what();
+    return TI_LLM_INTERNAL;
+  } catch (...) {
+    error_text = "unknown create failure";
+    return TI_LLM_INTERNAL;
+  }
+}
+
+extern "C" int ti_llm_destroy(ti_llm_model* m) {
+  error_text.clear();
+  if (!m) {
+    error_text = "null model";
+    return TI_LLM_INVALID;
+  }
+  delete m;
+  return TI_LLM_OK;
+}
+
+extern "C" int ti_llm_reset(ti_llm_model* m, int32_t slot) {
+  return api(m, [&] {
+    if (slot < 0 || slot >= m->opt.cache_slots) throw Invalid("invalid public slot");
+    m->lengths[slot] = 0;
+  });
+}
+
+extern "C" int ti_llm_lengths(ti_llm_model* m, int32_t* out, int32_t count) {
+  return api(m, [&] {
+    if (!out || count != m->opt.cache_slots) throw Invalid("wrong lengths output extent");
+    std::copy(m->lengths.begin(), m->lengths.begin() + count, out);
+  });
+}
+
+extern "C" int ti_llm_get_trace(ti_llm_model* m, ti_llm_trace* out) {
+  return api(m, [&] {
+    if (!out) throw Invalid("null trace output");
+    *out = m->trace;
+  });
+}
+
+extern "C" int ti_llm_forward_batch(ti_llm_model* m, const int32_t* slots, const int32_t* tokens,
+                                    const int32_t* lengths, int32_t batch, int32_t stride, float* out,
+                                    int32_t* next) {
+  return api(m, [&] { m->forward(slots, tokens, lengths, batch, stride, out, next); });
+}
+
+// reference runtime.cu:190-203
+extern "C" int ti_llm_greedy_batch(ti_llm_model* m, const int32_t* slots, const int32_t* prompts,
+                                   const int32_t* prompt_lengths, const int32_t* requested, int32_t batch,
+                                   int32_t stride, int32_t* output, int32_t out_stride, int32_t* output_lengths,
+                                   double* ttft, double* total) {
+  return api(m, [&] {
+    if (!slots || !prompts || !prompt_lengths || !requested || !output || batch < 1 || batch > m->opt.max_batch ||
+        stride < 1 || stride > m->opt.capacity || out_stride < 1 || out_stride > m->opt.capacity)
+      throw Invalid("invalid greedy arguments");
+    std::set<int> seen;
+    for (int i = 0; i < batch; ++i) {
+      if (slots[i] < 0 || slots[i] >= m->opt.cache_slots || !seen.insert(slots[i]).second || m->lengths[slots[i]] ||
+          prompt_lengths[i] < 1 || prompt_lengths[i] > stride || requested[i] < 1 || requested[i] > out_stride ||
+          requested[i] + prompt_lengths[i] > m->opt.capacity)
+        throw Invalid("greedy needs empty distinct slots and bounded positive lengths");
+      for (int j = 0; j < prompt_lengths[i]; ++j)
+        if (prompts[int64_t(i) * stride + j] < 0 || prompts[int64_t(i) * stride + j] >= m->V)
+          throw Invalid("invalid prompt token");
+    }
+    std::fill(output, output + int64_t(batch) * out_stride, -1);
+    if (output_lengths) std::fill(output_lengths, output_lengths + batch, 0);
+    const auto start = Clock::now();
+    std::vector<int32_t> next(batch);
+    m->forward(slots, prompts, prompt_lengths, batch, stride, nullptr, next.data());
+    const double first = ms_since(start);
+    std::vector<int> done(batch, 1);
+    for (int i = 0; i < batch; ++i) {
+      output[int64_t(i) * out_stride] = next[i];
+      if (ttft) ttft[i] = first;
+      if (total && requested[i] == 1) total[i] = first;
+    }
+    for (;;) {
+      std::vector<int32_t> active, ids, ones;
+      std::vector<int> owner;
+      for (int i = 0; i < batch; ++i)
+        if (done[i] < requested[i]) {
+          active.push_back(slots[i]);
+          ids.push_back(next[i]);
+          ones.push_back(1);
+          owner.push_back(i);
+        }
+      if (active.empty()) break;
+      std::vector<int32_t> generated(active.size());
+      m->forward(active.data(), ids.data(), ones.data(), int(active.size()), 1, nullptr, generated.data());
+      const double elapsed = ms_since(start);
+      for (size_t j = 0; j < owner.size(); ++j) {
+        const int i = owner[j];
+        next[i] = generated[j];
+        output[int64_t(i) * out_stride + done[i]] = next[i];
+        ++done[i];
+        if (total && done[i] == requested[i]) total[i] = elapsed;
+      }
+    }
+    if (output_lengths)
+      for (int i = 0; i < batch; ++i) output_lengths[i] = done[i];
+  });
+}
+
+extern "C" int ti_llm_score_window(ti_llm_model* m, const int32_t* tokens, const uint8_t* mask, int32_t length,
+                                   double* nll, uint64_t* count, double* positions) {
+  return api(m, [&] { m->score(tokens, mask, length, nll, count, positions); });
+}
+
+// Host-only self-test hooks for the artifact reader (no GPU needed): the
+// reference checks these with llm/tests/test_artifact.cpp:7-15.
+extern "C" int tia_llm_sha256_hex(const void* data, size_t n, char* out65) {
+  const std::string h = tia::art::Sha256::of(data, n);
+  std::memcpy(out65, h.c_str(), 65);
+  return 0;
+}
+extern "C" int tia_llm_json_accepts(const char* text) {
+  try {
+    (void)tia::art::JsonReader(std::string(text)).parse();
+    return 1;
+  } catch (const Invalid&) {
+    return 0;
+  }
+}
