@@ -86,9 +86,12 @@ def build(verbose: bool = True) -> None:
     if (CSRC / "ikernels.cpp").exists():
         import pybind11
         inc = sysconfig.get_paths()["include"]
-        _run([HIPCC, *HIP_FLAGS, "-shared", "-fopenmp", "-I", pybind11.get_include(), "-I", inc,
-              str(CSRC / "ikernels.cpp"), str(cpu_obj), "-o", str(PKG / ikernels_name()),
-              "-L", str(PKG), "-ltinyinfer_backend", "-lgomp", *rpath])
+        # Host-only translation unit (no kernels): libgomp's omp.h, linked to the backend.
+        _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-x", "c++", "-D__HIP_PLATFORM_AMD__",
+              "-I", str(ROCM / "include"), "-I", str(ROOT / "include"), "-I", pybind11.get_include(),
+              "-I", inc, "-isystem", "/usr/lib/gcc/x86_64-linux-gnu/11/include",
+              str(CSRC / "ikernels.cpp"), "-o", str(PKG / ikernels_name()),
+              "-L", str(PKG), "-ltinyinfer_backend", "-L", str(ROCM / "lib"), "-lamdhip64", "-lgomp", *rpath])
     if verbose:
         print("built:", ", ".join(sorted(p.name for p in PKG.glob("*.so"))))
 

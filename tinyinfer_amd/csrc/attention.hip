@@ -66,16 +66,27 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   float m = kNegInf, l = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int k0 = kw * 64; k0 < end; k0 += 64 * KW) {
+    // K and V of the whole 64-key tile are requested before any use: one memory
+    // round trip per tile.
+    half8_t kfr[NI], vfr[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int key = k0 + kg + KPI * i;
+      if (key < end) {
+        kfr[i] = load8(kb + int64_t(key) * D, p.vec);
+        vfr[i] = load8(vb + int64_t(key) * D, p.vec);
+      } else {
+        kfr[i] = half8_t{};
+        vfr[i] = half8_t{};
+      }
+    }
     float s[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + kg + KPI * i;
       float part = 0.f;
-      if (key < end) {
-        const half8_t kf = load8(kb + int64_t(key) * D, p.vec);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) part += float(qf[e]) * float(kf[e]);
-      }
+      for (int e = 0; e < 8; ++e) part += float(qf[e]) * float(kfr[i][e]);
 #pragma unroll
       for (int o = LPK / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
       s[i] = key < end ? part * p.scale : kNegInf;
@@ -95,11 +106,8 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
       const int key = k0 + kg + KPI * i;
       const float pr = key < end ? __expf(s[i] - nm) : 0.f;
       psum += pr;
-      if (key < end) {
-        const half8_t vf = load8(vb + int64_t(key) * D, p.vec);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += pr * float(vf[e]);
-      }
+      for (int e = 0; e < 8; ++e) acc[e] += pr * float(vfr[i][e]);
     }
 #pragma unroll
     for (int o = LPK; o < 64; o <<= 1) psum += __shfl_xor(psum, o, 64);
@@ -169,6 +177,7 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
     if (tiles >= 12) hipLaunchKernelGGL((attention_kernel<D, 1, 16>), grid, dim3(1024), 0, stream, p);
     else if (tiles >= 6) hipLaunchKernelGGL((attention_kernel<D, 1, 8>), grid, dim3(512), 0, stream, p);
     else if (tiles >= 3) hipLaunchKernelGGL((attention_kernel<D, 1, 4>), grid, dim3(256), 0, stream, p);
+    else if (tiles == 2) hipLaunchKernelGGL((attention_kernel<D, 1, 2>), grid, dim3(128), 0, stream, p);
     else hipLaunchKernelGGL((attention_kernel<D, 1, 1>), grid, dim3(64), 0, stream, p);
   } else {
     dim3 grid = blocks_per;

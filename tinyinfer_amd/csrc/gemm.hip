@@ -81,8 +81,9 @@ struct SkinnyParams {
   int64_t ldw;         // row stride of W in elements (>= n)
   int ntile;           // ceil(N / 64)
   int steps;           // ceil(K / 32)
-  int steps_per_block; // K steps owned by one workgroup (a multiple of 4)
+  int steps_per_block; // K steps owned by one workgroup (its waves take every 4th)
   int splits;
+  bool defer;          // always leave fp32 partials (even for one split), no epilogue
   Epilogue epi;
   float* partials;     // [splits][M][N]
 };
@@ -243,7 +244,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) 
     const int row = e >> 6, cc = e & 63, n = n0 + cc;
     if (row < p.m && n < p.n) {
       const float s = red[0][row][cc] + red[1][row][cc] + red[2][row][cc] + red[3][row][cc];
-      if (p.splits == 1) apply_epilogue(p.epi, row, n, s);
+      if (p.splits == 1 && !p.defer) apply_epilogue(p.epi, row, n, s);
       else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
     }
   }
@@ -452,30 +453,31 @@ __global__ __launch_bounds__(256) void legacy_f32_kernel(const float* a, const f
 // ---------------------------------------------------------------------------
 template <bool INT8, int MT>
 hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch* s,
-                         hipStream_t stream) {
+                         hipStream_t stream, int* deferred) {
   SkinnyParams p{};
   p.a = g.a; p.lda = g.lda; p.w = g.w; p.scales = g.scales;
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.ldw = g.ldw > 0 ? g.ldw : g.n;
   p.ntile = (g.n + 63) / 64;
   p.steps = (g.k + 31) / 32;
-  // Choose the number of K splits: aim for ~2 workgroups per CU, at least 4
-  // steps (one per wave) per workgroup, and fp32 partial traffic (splits * M * N
-  // * 4 bytes) at most a quarter of the weight bytes.
+  // Number of K splits: aim for ~2 workgroups per CU (a 2.4 MB GEMV is
+  // latency-bound, so every CU should have loads in flight), with the fp32
+  // partials (splits * M * N * 4 bytes, L2/MALL traffic) at most twice the
+  // weight bytes and within the scratch.
   int splits = 1;
   if (s && s->partials) {
     const int target = (2 * 256 + p.ntile - 1) / p.ntile;
-    const int max_by_steps = (p.steps + 3) / 4;
-    const int max_by_traffic = std::max(1, g.k / (16 * std::max(1, g.m)));
-    splits = std::max(1, std::min(target, std::min(max_by_steps, max_by_traffic)));
+    const int max_by_traffic = std::max(1, g.k / (2 * std::max(1, g.m)));
+    splits = std::max(1, std::min(target, std::min(p.steps, max_by_traffic)));
     while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
   }
-  int spb = (p.steps + splits - 1) / splits;
-  spb = (spb + 3) / 4 * 4;
+  const int spb = (p.steps + splits - 1) / splits;
   splits = (p.steps + spb - 1) / spb;
   p.steps_per_block = spb;
   p.splits = splits;
+  p.defer = deferred != nullptr;
   p.partials = s ? s->partials : nullptr;
+  if (p.defer && (!p.partials || size_t(splits) * g.m * g.n > s->partial_floats)) return hipErrorInvalidValue;
   const dim3 grid(unsigned(p.ntile) * unsigned(splits));
 #define TIA_SKINNY(WV, AV) hipLaunchKernelGGL((skinny_kernel<INT8, MT, WV, AV>), grid, dim3(kSkinnyThreads), 0, stream, p)
   if (wvec && avec) TIA_SKINNY(true, true);
@@ -483,6 +485,10 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   else if (avec) TIA_SKINNY(false, true);
   else TIA_SKINNY(false, false);
 #undef TIA_SKINNY
+  if (p.defer) {
+    *deferred = splits;
+    return hipGetLastError();
+  }
   if (splits > 1) {
     const int64_t total = int64_t(g.m) * g.n;
     const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 4096));
@@ -510,7 +516,8 @@ hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, hipStream_t str
 
 }  // namespace
 
-hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream) {
+hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  if (deferred) *deferred = 0;
   if (g.m <= 0 || g.n <= 0 || g.k <= 0) return hipErrorInvalidValue;
   const uintptr_t wp = reinterpret_cast<uintptr_t>(g.w), ap = reinterpret_cast<uintptr_t>(g.a);
   // Whole 4-column groups may be loaded when rows are 4-aligned and the row
@@ -519,10 +526,10 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream) {
   const bool wvec = ldw % 4 == 0 && ldw >= (int64_t(g.n) + 3) / 4 * 4 &&
                     (g.w_int8 ? wp % 4 == 0 : wp % 8 == 0);
   const bool avec = (g.lda % 8 == 0) && (ap % 16 == 0);
-  if (g.m <= 16) return g.w_int8 ? launch_skinny<true, 1>(g, wvec, avec, s, stream)
-                                 : launch_skinny<false, 1>(g, wvec, avec, s, stream);
-  if (g.m <= 32) return g.w_int8 ? launch_skinny<true, 2>(g, wvec, avec, s, stream)
-                                 : launch_skinny<false, 2>(g, wvec, avec, s, stream);
+  if (g.m <= 16) return g.w_int8 ? launch_skinny<true, 1>(g, wvec, avec, s, stream, deferred)
+                                 : launch_skinny<false, 1>(g, wvec, avec, s, stream, deferred);
+  if (g.m <= 32) return g.w_int8 ? launch_skinny<true, 2>(g, wvec, avec, s, stream, deferred)
+                                 : launch_skinny<false, 2>(g, wvec, avec, s, stream, deferred);
   return g.w_int8 ? launch_tiled<true>(g, wvec, avec, stream) : launch_tiled<false>(g, wvec, avec, stream);
 }
 

@@ -56,7 +56,21 @@ struct GemmArgs {
   Epilogue epi;
 };
 
-hipError_t gemm(const GemmArgs& args, const Scratch* scratch, hipStream_t stream);
+// When `deferred` is non-null and the skinny (M <= 32) kernel runs, the epilogue
+// is skipped: the raw fp32 sums are left in scratch->partials as [splits][M][N]
+// and *deferred = splits (>= 1); the caller finishes them (e.g. with
+// splitk_residual_layernorm).  Otherwise *deferred = 0 and the epilogue ran.
+hipError_t gemm(const GemmArgs& args, const Scratch* scratch, hipStream_t stream,
+                int* deferred = nullptr);
+// Finishes a deferred GEMM whose N equals the row width `cols`, one wave per row:
+//   x[r][c]    = fp16_rn(x[r][c] + fp16_rn(sum_s partials[s][r][c] + bias[c]))
+//   norm[r][:] = LayerNorm(x[r][:]; gamma, beta, eps)   (fp16 out)
+// i.e. the residual add of reference llm/src/runtime.cu:149/153 followed by the
+// next ln (cols <= 2048).
+hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows, int cols,
+                                     const uint16_t* bias, uint16_t* x, const uint16_t* gamma,
+                                     const uint16_t* beta, uint16_t* norm, float eps,
+                                     hipStream_t stream);
 // Per-(device, stream) scratch owned by the library, created on the first call
 // on that stream (never under graph capture).  Returns nullptr and sets *err if
 // it cannot be created.

@@ -3,13 +3,15 @@
 // Semantics follow reference llm/src/runtime.cu:86-211 (validation rules,
 // absolute positions, greedy loop, poisoning, internal scoring slot, trace
 // counters); the execution plan is MI355X-native:
-//  * per layer five launches: LN1 -> c_attn GEMM whose epilogue also writes K/V
-//    into the slot cache (no split/scatter/gather/pack kernels) -> attention
-//    reading the [slot][layer][head][pos][64] cache in place and writing merged
-//    heads -> c_proj GEMM + residual (in place) -> LN2 -> c_fc GEMM + GELU ->
-//    mlp.c_proj GEMM + residual (in place);
-//  * ln_f runs on the last row of each request only, the lm_head GEMM writes
-//    fp32 logits, a block-per-row argmax picks the lowest id on ties;
+//  * the embedding kernel also computes layer 0's LN1; per layer: c_attn GEMM
+//    whose epilogue also writes K/V into the slot cache (no split/scatter/
+//    gather/pack kernels) -> attention reading the [slot][layer][head][pos][64]
+//    cache in place and writing merged heads -> c_proj GEMM -> one kernel that
+//    reduces its split-K partials, adds bias and residual (in place) and applies
+//    LN2 -> c_fc GEMM with fused bias + GELU -> mlp.c_proj GEMM -> the same
+//    reduce + residual kernel applying the next layer's LN1 (ln_f after the last);
+//  * the lm_head GEMM writes fp32 logits of each request's last row (padded row
+//    pitch), a block-per-row argmax picks the lowest id on ties;
 //  * a decode step (every request appends one token) is captured once per
 //    batch size into a hipGraph whose kernels read all lengths, offsets and slots
 //    from device memory, so later steps are one graph launch between a pinned
@@ -62,29 +64,6 @@ struct DeviceScope {
 };
 
 // ---------------------------------------------------------------- kernels
-// x[row] = fp16(wte[id] + wpe[offset + t]) for t < qlens[b], else 0
-// (reference runtime.cu:25-30); 8 halves per thread.
-__global__ void embed_kernel(const int32_t* ids, const int32_t* qlens, const int32_t* offsets,
-                             const uint16_t* wte, const uint16_t* wpe, uint16_t* x, int rows, int qlen,
-                             int hidden) {
-  const int per_row = hidden / 8;
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= int64_t(rows) * per_row) return;
-  const int row = int(i / per_row), c = int(i % per_row) * 8;
-  const int b = row / qlen, t = row - b * qlen;
-  tia::half8_t out;
-  if (t < qlens[b]) {
-    const tia::half8_t e = *reinterpret_cast<const tia::half8_t*>(wte + int64_t(ids[row]) * hidden + c);
-    const tia::half8_t p = *reinterpret_cast<const tia::half8_t*>(wpe + int64_t(offsets[b] + t) * hidden + c);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) out[k] = tia::f16(float(e[k]) + float(p[k]));
-  } else {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) out[k] = tia::f16(0.f);
-  }
-  *reinterpret_cast<tia::half8_t*>(x + int64_t(row) * hidden + c) = out;
-}
-
 // out[b] = x[b * qlen + qlens[b] - 1] (reference runtime.cu:56-58).
 __global__ void gather_last_kernel(const uint16_t* x, uint16_t* out, const int32_t* qlens, int batch,
                                    int qlen, int hidden) {
@@ -96,20 +75,90 @@ __global__ void gather_last_kernel(const uint16_t* x, uint16_t* out, const int32
       *reinterpret_cast<const tia::half8_t*>(x + (int64_t(b) * qlen + qlens[b] - 1) * hidden + c);
 }
 
-// Greedy id per row: largest logit, lowest id on ties (reference runtime.cu:59-66).
-__global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int32_t* out, int vocab) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
-  const float* row = logits + int64_t(blockIdx.x) * vocab;
-  float best = -__builtin_huge_valf();
-  int idx = INT_MAX;
-  for (int j = threadIdx.x; j < vocab; j += 256) {
-    const float v = row[j];
-    if (v > best) {  // j increases, so equality keeps the lower id
-      best = v;
-      idx = j;
+// x[row] = fp16(wte[id] + wpe[offset + t]) for t < qlens[b], else 0 (reference
+// runtime.cu:25-30), fused with the first layer's LayerNorm of that row: one
+// wave per row, lane owns the 8-wide column groups lane + 64 i (hidden <= 2048).
+__global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const int32_t* qlens,
+                                                       const int32_t* offsets, const uint16_t* wte,
+                                                       const uint16_t* wpe, const uint16_t* g, const uint16_t* bt,
+                                                       uint16_t* x, uint16_t* norm, int rows, int qlen, int hidden) {
+  constexpr int NV = 4;
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int b = row / qlen, t = row - b * qlen, groups = hidden / 8;
+  const bool valid = t < qlens[b];
+  float v[NV][8];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int gi = lane + 64 * i;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[i][k] = 0.f;
+    if (gi < groups) {
+      if (valid) {
+        const tia::half8_t e = *reinterpret_cast<const tia::half8_t*>(wte + int64_t(ids[row]) * hidden + 8 * gi);
+        const tia::half8_t p =
+            *reinterpret_cast<const tia::half8_t*>(wpe + int64_t(offsets[b] + t) * hidden + 8 * gi);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[i][k] = float(tia::f16(float(e[k]) + float(p[k])));
+      }
+      tia::half8_t o;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        o[k] = tia::f16(v[i][k]);
+        s += v[i][k];
+      }
+      *reinterpret_cast<tia::half8_t*>(x + int64_t(row) * hidden + 8 * gi) = o;
     }
   }
+  const float mean = tia::wave_sum(s) / float(hidden);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < groups) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ss += (v[i][k] - mean) * (v[i][k] - mean);
+    }
+  const float inv = rsqrtf(tia::wave_sum(ss) / float(hidden) + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int gi = lane + 64 * i;
+    if (gi < groups) {
+      const tia::half8_t gg = *reinterpret_cast<const tia::half8_t*>(g + 8 * gi);
+      const tia::half8_t bb = *reinterpret_cast<const tia::half8_t*>(bt + 8 * gi);
+      tia::half8_t o;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] = tia::f16((v[i][k] - mean) * inv * float(gg[k]) + float(bb[k]));
+      *reinterpret_cast<tia::half8_t*>(norm + int64_t(row) * hidden + 8 * gi) = o;
+    }
+  }
+}
+
+// Greedy id per row: largest logit, lowest id on ties (reference runtime.cu:59-66).
+// One 1024-thread block per row, 16-byte loads over a row pitch `ld` (a multiple
+// of 4 floats).
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int32_t* out, int vocab, int64_t ld) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const float* row = logits + int64_t(blockIdx.x) * ld;
+  float best = -__builtin_huge_valf();
+  int idx = INT_MAX;
+  const int vec = vocab / 4;
+  for (int j4 = threadIdx.x; j4 < vec; j4 += 1024) {
+    const float4 v = *reinterpret_cast<const float4*>(row + 4 * j4);
+    const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (e[k] > best) {  // ids visited in increasing order: equality keeps the lower id
+        best = e[k];
+        idx = 4 * j4 + k;
+      }
+  }
+  for (int j = 4 * vec + threadIdx.x; j < vocab; j += 1024)
+    if (row[j] > best) {
+      best = row[j];
+      idx = j;
+    }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(best, o, 64);
@@ -125,7 +174,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int32_
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w)
+    for (int w = 1; w < 16; ++w)
       if (sv[w] > best || (sv[w] == best && si[w] < idx)) {
         best = sv[w];
         idx = si[w];
@@ -137,11 +186,11 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int32_
 // Shifted-target NLL of one row in fp64 (reference runtime.cu:67-76).
 __global__ __launch_bounds__(256) void nll_kernel(const float* logits, const int32_t* tokens,
                                                   const uint8_t* mask, double* loss, int first_position,
-                                                  int vocab) {
+                                                  int vocab, int64_t ld) {
   __shared__ float smax[4];
   __shared__ double ssum[4];
   const int row = blockIdx.x, pos = first_position + row;
-  const float* l = logits + int64_t(row) * vocab;
+  const float* l = logits + int64_t(row) * ld;
   float m = -__builtin_huge_valf();
   for (int j = threadIdx.x; j < vocab; j += 256) m = fmaxf(m, l[j]);
   m = tia::wave_max(m);
@@ -249,6 +298,7 @@ struct ti_llm_model {
     H = arch.hidden;
     V = arch.vocab;
     if (opt.capacity > arch.capacity) throw Invalid("capacity exceeds the model's position table");
+    if (H > 2048) throw Invalid("hidden size above 2048 is not supported by the fused row kernels");
     quantized = a.precision == "int8";
     const std::string lin = quantized ? "int8" : "float16";
     std::set<std::string> used;
@@ -316,7 +366,7 @@ struct ti_llm_model {
     const size_t cache = size_t(opt.cache_slots + 1) * L * NH * opt.capacity * kHeadDim;
     kc = alloc<uint16_t>(cache);
     vc = alloc<uint16_t>(cache);
-    logits = alloc<float>(size_t(std::max(opt.max_batch, kScoreRows)) * V);
+    logits = alloc<float>(size_t(std::max(opt.max_batch, kScoreRows)) * size_t(head.ldw));
     // Step metadata: ids[rows] | slots[B] | qlens[B] | offsets[B], mirrored in pinned host memory.
     meta_ints = rows + 3 * size_t(opt.max_batch);
     d_meta = alloc<int32_t>(meta_ints);
@@ -343,7 +393,7 @@ struct ti_llm_model {
   }
 
   // ---------------------------------------------------------------- launch helpers
-  void gemm(const uint16_t* a, int m, const Linear& w, tia::Epilogue epi) {
+  void gemm(const uint16_t* a, int m, const Linear& w, tia::Epilogue epi, int* deferred = nullptr) {
     tia::GemmArgs g;
     g.a = a;
     g.lda = w.k;
@@ -355,18 +405,36 @@ struct ti_llm_model {
     g.k = w.k;
     g.ldw = w.ldw;
     g.epi = epi;
-    ck(tia::gemm(g, &scratch, stream));
+    ck(tia::gemm(g, &scratch, stream, deferred));
+  }
+
+  // x += a @ w + bias (fp16 rounding points of reference runtime.cu:149/153), then
+  // norm = LayerNorm(x; g, beta).  Decode-sized GEMMs leave split-K partials that
+  // one fused kernel reduces, adds and normalizes.
+  void residual_ln(const uint16_t* a, int rows, const Linear& w, const uint16_t* g, const uint16_t* beta) {
+    tia::Epilogue r;
+    r.kind = tia::EPI_RESIDUAL;
+    r.bias = w.bias;
+    r.y = x;
+    r.ldy = H;
+    r.residual = x;
+    r.ldr = H;
+    int splits = 0;
+    gemm(a, rows, w, r, &splits);
+    if (splits > 0)
+      ck(tia::splitk_residual_layernorm(scratch.partials, splits, rows, H, w.bias, x, g, beta, norm, 1e-5f, stream));
+    else
+      ck(tia::layernorm_f16(x, g, beta, norm, rows, H, 1e-5f, stream));
   }
 
   // One pass of the transformer over rows [b, qlen] whose metadata is already on
-  // the device; leaves the residual stream in x.
+  // the device; leaves the residual stream in x and ln_f(x) of every row in norm.
   void layers(int b, int qlen) {
     const int rows = b * qlen;
-    embed_kernel<<<blocks_for(int64_t(rows) * H / 8), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, x,
-                                                                          rows, qlen, H);
+    embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, ln1_g[0],
+                                                             ln1_b[0], x, norm, rows, qlen, H);
     ck(hipGetLastError());
     for (int l = 0; l < L; ++l) {
-      ck(tia::layernorm_f16(x, ln1_g[l], ln1_b[l], norm, rows, H, 1e-5f, stream));
       tia::Epilogue e;
       e.kind = tia::EPI_QKV;
       e.bias = c_attn[l].bias;
@@ -412,42 +480,34 @@ struct ti_llm_model {
       at.causal = true;
       ck(tia::attention(at, stream));
 
-      tia::Epilogue r;
-      r.kind = tia::EPI_RESIDUAL;
-      r.bias = c_proj[l].bias;
-      r.y = x;
-      r.ldy = H;
-      r.residual = x;
-      r.ldr = H;
-      gemm(attn, rows, c_proj[l], r);
-      ck(tia::layernorm_f16(x, ln2_g[l], ln2_b[l], norm, rows, H, 1e-5f, stream));
+      residual_ln(attn, rows, c_proj[l], ln2_g[l], ln2_b[l]);
       tia::Epilogue gl;
       gl.kind = tia::EPI_GELU;
       gl.bias = c_fc[l].bias;
       gl.y = mlp;
       gl.ldy = 4 * H;
       gemm(norm, rows, c_fc[l], gl);
-      r.bias = c_proj2[l].bias;
-      gemm(mlp, rows, c_proj2[l], r);
+      const bool final_layer = l + 1 == L;
+      residual_ln(mlp, rows, c_proj2[l], final_layer ? lnf_g : ln1_g[l + 1], final_layer ? lnf_b : ln1_b[l + 1]);
     }
   }
 
-  // ln_f of each request's last row, fp32 logits without bias, argmax.
+  // Logits of each request's last row (norm already holds ln_f), fp32 without
+  // bias over the padded row pitch head.ldw, then the greedy argmax.
   void head_and_argmax(int b, int qlen, bool greedy) {
-    const uint16_t* rows_in = x;
+    const uint16_t* rows_in = norm;
     if (qlen > 1) {
-      gather_last_kernel<<<blocks_for(int64_t(b) * H / 8), 256, 0, stream>>>(x, last, d_qlens, b, qlen, H);
+      gather_last_kernel<<<blocks_for(int64_t(b) * H / 8), 256, 0, stream>>>(norm, last, d_qlens, b, qlen, H);
       ck(hipGetLastError());
       rows_in = last;
     }
-    ck(tia::layernorm_f16(rows_in, lnf_g, lnf_b, norm, b, H, 1e-5f, stream));
     tia::Epilogue e;
     e.kind = tia::EPI_F32;
     e.y = logits;
-    e.ldy = V;
-    gemm(norm, b, head, e);
+    e.ldy = head.ldw;
+    gemm(rows_in, b, head, e);
     if (greedy) {
-      argmax_kernel<<<b, 256, 0, stream>>>(logits, d_next, V);
+      argmax_kernel<<<b, 1024, 0, stream>>>(logits, d_next, V, head.ldw);
       ck(hipGetLastError());
     }
   }
@@ -537,7 +597,9 @@ struct ti_llm_model {
       if (need_head) head_and_argmax(b, qlen, greedy != nullptr);
     }
     count_forward(need_head, greedy != nullptr);
-    if (out) ck(hipMemcpyAsync(out, logits, size_t(b) * V * sizeof(float), hipMemcpyDeviceToHost, stream));
+    if (out)
+      ck(hipMemcpy2DAsync(out, size_t(V) * sizeof(float), logits, size_t(head.ldw) * sizeof(float),
+                          size_t(V) * sizeof(float), size_t(b), hipMemcpyDeviceToHost, stream));
     if (greedy) ck(hipMemcpyAsync(h_next, d_next, size_t(b) * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
     ck(hipStreamSynchronize(stream));
     if (greedy) std::copy(h_next, h_next + b, greedy);
@@ -562,8 +624,7 @@ struct ti_llm_model {
     h_qlens[0] = q;
     h_offsets[0] = 0;
     upload_meta(1, q);
-    layers(1, q);
-    ck(tia::layernorm_f16(x, lnf_g, lnf_b, norm, q, H, 1e-5f, stream));
+    layers(1, q);  // leaves ln_f of every row in norm
     ++trace.forward_calls;
     ++trace.embedding;
     trace.layernorm += 2 * L + 1;
@@ -583,10 +644,10 @@ struct ti_llm_model {
       tia::Epilogue e;
       e.kind = tia::EPI_F32;
       e.y = logits;
-      e.ldy = V;
+      e.ldy = head.ldw;
       gemm(norm + int64_t(row) * H, rows, head, e);
       ++trace.nll;
-      nll_kernel<<<rows, 256, 0, stream>>>(logits, d_score_tokens, d_score_mask, d_loss, row + 1, V);
+      nll_kernel<<<rows, 256, 0, stream>>>(logits, d_score_tokens, d_score_mask, d_loss, row + 1, V, head.ldw);
       ck(hipGetLastError());
     }
     sum_kernel<<<1, 256, 0, stream>>>(d_loss, d_loss_sum, length);

@@ -213,6 +213,50 @@ __global__ void gelu_kernel(const uint16_t* x, uint16_t* y, int64_t count, bool 
   }
 }
 
+// Deferred-GEMM finisher: split-K sum (in split order) + bias + residual, then
+// LayerNorm of the new row.  One wave per row, lane owns columns lane + 64 i.
+constexpr int kResLnMaxPerLane = 32;  // cols <= 2048
+__global__ __launch_bounds__(256) void splitk_residual_ln_kernel(const float* partials, int splits, int rows,
+                                                                 int cols, const uint16_t* bias, uint16_t* x,
+                                                                 const uint16_t* g, const uint16_t* b,
+                                                                 uint16_t* norm, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t plane = int64_t(rows) * cols, base = int64_t(row) * cols;
+  float v[kResLnMaxPerLane];
+#pragma unroll
+  for (int i = 0; i < kResLnMaxPerLane; ++i) v[i] = 0.f;
+  for (int sp = 0; sp < splits; ++sp) {
+    const float* p = partials + sp * plane + base;
+#pragma unroll
+    for (int i = 0; i < kResLnMaxPerLane; ++i)
+      if (lane + 64 * i < cols) v[i] += p[lane + 64 * i];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kResLnMaxPerLane; ++i) {
+    const int c = lane + 64 * i;
+    if (c < cols) {
+      const float h = rt16(v[i] + (bias ? h2f(bias[c]) : 0.f));
+      v[i] = rt16(h2f(x[base + c]) + h);
+      x[base + c] = f2h(v[i]);
+      s += v[i];
+    }
+  }
+  const float mean = wave_sum(s) / float(cols);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kResLnMaxPerLane; ++i)
+    if (lane + 64 * i < cols) ss += (v[i] - mean) * (v[i] - mean);
+  const float inv = rsqrtf(wave_sum(ss) / float(cols) + eps);
+#pragma unroll
+  for (int i = 0; i < kResLnMaxPerLane; ++i) {
+    const int c = lane + 64 * i;
+    if (c < cols) norm[base + c] = f2h((v[i] - mean) * inv * h2f(g[c]) + h2f(b[c]));
+  }
+}
+
 bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 template <typename T>
@@ -267,6 +311,14 @@ hipError_t layernorm_f32(const float* x, const float* g, const float* b, float* 
 }
 hipError_t softmax_f32(const float* x, float* y, int rows, int cols, hipStream_t st) {
   return softmax_dispatch<float>(x, y, rows, cols, st);
+}
+hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows, int cols,
+                                     const uint16_t* bias, uint16_t* x, const uint16_t* gamma,
+                                     const uint16_t* beta, uint16_t* norm, float eps, hipStream_t st) {
+  if (cols > 64 * kResLnMaxPerLane || splits < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(splitk_residual_ln_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, st, partials,
+                     splits, rows, cols, bias, x, gamma, beta, norm, eps);
+  return hipGetLastError();
 }
 hipError_t gelu_f16(const uint16_t* x, uint16_t* y, int64_t count, hipStream_t st) {
   const bool vec = al16(x) && al16(y);
