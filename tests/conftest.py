@@ -3,6 +3,15 @@ from pathlib import Path
 
 import pytest
 
+# torch-ROCm bundles its own libamdhip64.so.7, which shares its SONAME with the
+# ROCm runtime the tinyinfer libraries link; whichever loads first serves the
+# whole process.  Load torch's first so tests that use torch tensors and the
+# native libraries in one process run on one HIP runtime.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 ROOT = Path(__file__).resolve().parents[1]
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
