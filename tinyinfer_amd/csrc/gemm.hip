@@ -252,20 +252,28 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) 
 
 // Second pass of a split-K launch: C[m][n] = sum of the split partials in split
 // order, then the epilogue.  The kernel boundary orders it after every partial.
+// Each workgroup covers 64 consecutive outputs with 4 waves; wave w sums splits
+// w, w + 4, ... so all splits of an output are in flight at once, and wave 0
+// adds the four group sums in a fixed order.
 __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* partials, int splits, int m,
                                                               int n, Epilogue epi) {
-  const int64_t total = int64_t(m) * n, stride = total;
-  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int64_t total = int64_t(m) * n;
+  for (int64_t base = int64_t(blockIdx.x) * 64; base < total; base += int64_t(gridDim.x) * 64) {
+    const int64_t i = base + lane;
     float s = 0.f;
-    int sp = 0;
-    for (; sp + 4 <= splits; sp += 4) {
-      const float a0 = partials[i + sp * stride], a1 = partials[i + (sp + 1) * stride];
-      const float a2 = partials[i + (sp + 2) * stride], a3 = partials[i + (sp + 3) * stride];
-      s = (((s + a0) + a1) + a2) + a3;
+    if (i < total) {
+#pragma unroll 4
+      for (int sp = grp; sp < splits; sp += 4) s += partials[i + sp * total];
     }
-    for (; sp < splits; ++sp) s += partials[i + sp * stride];
-    const int row = int(i / n), col = int(i - int64_t(row) * n);
-    apply_epilogue(epi, row, col, s);
+    red[grp][lane] = s;
+    __syncthreads();
+    if (grp == 0 && i < total) {
+      const int row = int(i / n), col = int(i - int64_t(row) * n);
+      apply_epilogue(epi, row, col, ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]);
+    }
+    __syncthreads();
   }
 }
 
@@ -491,7 +499,7 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   }
   if (splits > 1) {
     const int64_t total = int64_t(g.m) * g.n;
-    const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 4096));
+    const unsigned blocks = unsigned(std::min<int64_t>((total + 63) / 64, 8192));
     hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m,
                        g.n, g.epi);
   }

@@ -213,25 +213,44 @@ __global__ void gelu_kernel(const uint16_t* x, uint16_t* y, int64_t count, bool 
   }
 }
 
-// Deferred-GEMM finisher: split-K sum (in split order) + bias + residual, then
-// LayerNorm of the new row.  One wave per row, lane owns columns lane + 64 i.
+// Deferred-GEMM finisher: split-K sum + bias + residual, then LayerNorm of the
+// new row.  One workgroup of G waves per row: wave w sums splits w, w + G, ...
+// for every column (all its loads independent, so the splits are fetched in
+// parallel rather than one memory round trip each), the G partial rows meet in
+// LDS and wave 0 adds them in group order, then does the residual and the
+// LayerNorm with lane owning columns lane + 64 i.
 constexpr int kResLnMaxPerLane = 32;  // cols <= 2048
-__global__ __launch_bounds__(256) void splitk_residual_ln_kernel(const float* partials, int splits, int rows,
-                                                                 int cols, const uint16_t* bias, uint16_t* x,
-                                                                 const uint16_t* g, const uint16_t* b,
-                                                                 uint16_t* norm, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+template <int G>
+__global__ __launch_bounds__(64 * G) void splitk_residual_ln_kernel(const float* partials, int splits, int rows,
+                                                                    int cols, const uint16_t* bias, uint16_t* x,
+                                                                    const uint16_t* g, const uint16_t* b,
+                                                                    uint16_t* norm, float eps) {
+  extern __shared__ float red[];  // [G][cols]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = blockIdx.x;
   const int64_t plane = int64_t(rows) * cols, base = int64_t(row) * cols;
   float v[kResLnMaxPerLane];
 #pragma unroll
   for (int i = 0; i < kResLnMaxPerLane; ++i) v[i] = 0.f;
-  for (int sp = 0; sp < splits; ++sp) {
+  for (int sp = wave; sp < splits; sp += G) {
     const float* p = partials + sp * plane + base;
 #pragma unroll
     for (int i = 0; i < kResLnMaxPerLane; ++i)
       if (lane + 64 * i < cols) v[i] += p[lane + 64 * i];
+  }
+#pragma unroll
+  for (int i = 0; i < kResLnMaxPerLane; ++i)
+    if (lane + 64 * i < cols) red[wave * cols + lane + 64 * i] = v[i];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int i = 0; i < kResLnMaxPerLane; ++i) {
+    const int c = lane + 64 * i;
+    if (c < cols) {
+      float t = red[c];
+      for (int w = 1; w < G; ++w) t += red[w * cols + c];
+      v[i] = t;
+    }
   }
   float s = 0.f;
 #pragma unroll
@@ -316,8 +335,13 @@ hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows
                                      const uint16_t* bias, uint16_t* x, const uint16_t* gamma,
                                      const uint16_t* beta, uint16_t* norm, float eps, hipStream_t st) {
   if (cols > 64 * kResLnMaxPerLane || splits < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(splitk_residual_ln_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, st, partials,
-                     splits, rows, cols, bias, x, gamma, beta, norm, eps);
+  // LDS holds G rows of partial sums: keep it within 64 KiB.
+  if (cols <= 1024)
+    hipLaunchKernelGGL((splitk_residual_ln_kernel<16>), dim3(unsigned(rows)), dim3(1024), 16 * cols * sizeof(float),
+                       st, partials, splits, rows, cols, bias, x, gamma, beta, norm, eps);
+  else
+    hipLaunchKernelGGL((splitk_residual_ln_kernel<8>), dim3(unsigned(rows)), dim3(512), 8 * cols * sizeof(float),
+                       st, partials, splits, rows, cols, bias, x, gamma, beta, norm, eps);
   return hipGetLastError();
 }
 hipError_t gelu_f16(const uint16_t* x, uint16_t* y, int64_t count, hipStream_t st) {
