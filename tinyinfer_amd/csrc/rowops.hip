@@ -215,50 +215,63 @@ __global__ void gelu_kernel(const uint16_t* x, uint16_t* y, int64_t count, bool 
 
 // Deferred-GEMM finisher: split-K sum + bias + residual, then LayerNorm of the
 // new row.  One workgroup of G waves per row: wave w sums splits w, w + G, ...
-// for every column (all its loads independent, so the splits are fetched in
-// parallel rather than one memory round trip each), the G partial rows meet in
-// LDS and wave 0 adds them in group order, then does the residual and the
-// LayerNorm with lane owning columns lane + 64 i.
+// for every column, the G partial rows meet in LDS and wave 0 adds them in
+// group order, then does the residual and the LayerNorm with lane owning
+// columns lane + 64 i.  NPL > 0 fixes cols = 64 * NPL so no load carries a
+// bounds predicate (predicated loads are issued one round trip at a time);
+// NPL = 0 is the predicated fallback for any cols <= 2048.
 constexpr int kResLnMaxPerLane = 32;  // cols <= 2048
-template <int G>
+template <int G, int NPL>
 __global__ __launch_bounds__(64 * G) void splitk_residual_ln_kernel(const float* partials, int splits, int rows,
                                                                     int cols, const uint16_t* bias, uint16_t* x,
                                                                     const uint16_t* g, const uint16_t* b,
                                                                     uint16_t* norm, float eps) {
+  constexpr int N = NPL > 0 ? NPL : kResLnMaxPerLane;
   extern __shared__ float red[];  // [G][cols]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x;
   const int64_t plane = int64_t(rows) * cols, base = int64_t(row) * cols;
-  float v[kResLnMaxPerLane];
+  auto on = [&](int i) { return NPL > 0 || lane + 64 * i < cols; };
+  // Operands that do not depend on the partials are requested first, in one batch.
+  // (A null bias reads gamma instead and is scaled to zero, so no load sits
+  // behind a per-element branch.)
+  float xv[N], bv[N], gv[N], btv[N];
+  if (wave == 0) {
+    const uint16_t* bp = bias ? bias : g;
+    const float bscale = bias ? 1.f : 0.f;
 #pragma unroll
-  for (int i = 0; i < kResLnMaxPerLane; ++i) v[i] = 0.f;
-  for (int sp = wave; sp < splits; sp += G) {
-    const float* p = partials + sp * plane + base;
-#pragma unroll
-    for (int i = 0; i < kResLnMaxPerLane; ++i)
-      if (lane + 64 * i < cols) v[i] += p[lane + 64 * i];
-  }
-#pragma unroll
-  for (int i = 0; i < kResLnMaxPerLane; ++i)
-    if (lane + 64 * i < cols) red[wave * cols + lane + 64 * i] = v[i];
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int i = 0; i < kResLnMaxPerLane; ++i) {
-    const int c = lane + 64 * i;
-    if (c < cols) {
-      float t = red[c];
-      for (int w = 1; w < G; ++w) t += red[w * cols + c];
-      v[i] = t;
+    for (int i = 0; i < N; ++i) {
+      const int c = on(i) ? lane + 64 * i : 0;
+      xv[i] = h2f(x[base + c]);
+      gv[i] = h2f(g[c]);
+      btv[i] = h2f(b[c]);
+      bv[i] = h2f(bp[c]) * bscale;
     }
   }
+  float v[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = 0.f;
+  for (int sp = wave; sp < splits; sp += G) {
+    const float* p = partials + sp * plane + base + lane;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (on(i)) v[i] += p[64 * i];
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    if (on(i)) red[wave * cols + lane + 64 * i] = v[i];
+  __syncthreads();
+  if (wave != 0) return;
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < kResLnMaxPerLane; ++i) {
+  for (int i = 0; i < N; ++i) {
     const int c = lane + 64 * i;
-    if (c < cols) {
-      const float h = rt16(v[i] + (bias ? h2f(bias[c]) : 0.f));
-      v[i] = rt16(h2f(x[base + c]) + h);
+    if (on(i)) {
+      float t = red[c];
+#pragma unroll
+      for (int w = 1; w < G; ++w) t += red[w * cols + c];
+      const float h = rt16(t + bv[i]);
+      v[i] = rt16(xv[i] + h);
       x[base + c] = f2h(v[i]);
       s += v[i];
     }
@@ -266,13 +279,13 @@ __global__ __launch_bounds__(64 * G) void splitk_residual_ln_kernel(const float*
   const float mean = wave_sum(s) / float(cols);
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < kResLnMaxPerLane; ++i)
-    if (lane + 64 * i < cols) ss += (v[i] - mean) * (v[i] - mean);
+  for (int i = 0; i < N; ++i)
+    if (on(i)) ss += (v[i] - mean) * (v[i] - mean);
   const float inv = rsqrtf(wave_sum(ss) / float(cols) + eps);
 #pragma unroll
-  for (int i = 0; i < kResLnMaxPerLane; ++i) {
+  for (int i = 0; i < N; ++i) {
     const int c = lane + 64 * i;
-    if (c < cols) norm[base + c] = f2h((v[i] - mean) * inv * h2f(g[c]) + h2f(b[c]));
+    if (on(i)) norm[base + c] = f2h((v[i] - mean) * inv * gv[i] + btv[i]);
   }
 }
 
@@ -336,12 +349,17 @@ hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows
                                      const uint16_t* beta, uint16_t* norm, float eps, hipStream_t st) {
   if (cols > 64 * kResLnMaxPerLane || splits < 1) return hipErrorInvalidValue;
   // LDS holds G rows of partial sums: keep it within 64 KiB.
-  if (cols <= 1024)
-    hipLaunchKernelGGL((splitk_residual_ln_kernel<16>), dim3(unsigned(rows)), dim3(1024), 16 * cols * sizeof(float),
-                       st, partials, splits, rows, cols, bias, x, gamma, beta, norm, eps);
-  else
-    hipLaunchKernelGGL((splitk_residual_ln_kernel<8>), dim3(unsigned(rows)), dim3(512), 8 * cols * sizeof(float),
-                       st, partials, splits, rows, cols, bias, x, gamma, beta, norm, eps);
+  const size_t lds16 = 16 * cols * sizeof(float), lds8 = 8 * cols * sizeof(float);
+#define TIA_RLN(G, NPL, LDS)                                                                              \
+  hipLaunchKernelGGL((splitk_residual_ln_kernel<G, NPL>), dim3(unsigned(rows)), dim3(64 * G), LDS, st, partials, \
+                     splits, rows, cols, bias, x, gamma, beta, norm, eps)
+  if (cols == 768) TIA_RLN(16, 12, lds16);
+  else if (cols == 1024) TIA_RLN(16, 16, lds16);
+  else if (cols == 1600) TIA_RLN(8, 25, lds8);
+  else if (cols == 2048) TIA_RLN(8, 32, lds8);
+  else if (cols <= 1024) TIA_RLN(16, 0, lds16);
+  else TIA_RLN(8, 0, lds8);
+#undef TIA_RLN
   return hipGetLastError();
 }
 hipError_t gelu_f16(const uint16_t* x, uint16_t* y, int64_t count, hipStream_t st) {
