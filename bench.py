@@ -8,10 +8,14 @@ achieved HBM GB/s".
   seeded prompt ids per request, 64 new tokens, rate B*(new-1)/(t_last-t_first)
   as reference llm/evaluate.py:195 defines it.  One "step" is one such greedy
   batch; batch 1 is reported beside it.
-* roofline: the W8A16 GEMV (skinny MFMA kernel, M=1, K=3072 -> N=768, fused
-  bias+GELU) replayed back-to-back from a HIP graph over >= 600 MiB of distinct
-  weight sets (beyond the 256 MiB Infinity Cache), timed with HIP events on the
-  launch stream; algorithmic bytes per launch 2MK + KN + 4N + 2N + 2MN.
+* roofline: the W8A16 GEMV (skinny MFMA kernel + split-K epilogue, M=1,
+  K=3072 -> N=768, fused bias+GELU) replayed back-to-back from a HIP graph over
+  >= 600 MiB of distinct weight sets (beyond the 256 MiB Infinity Cache), timed
+  with HIP events on the launch stream; algorithmic bytes 2MK + KN + 4N + 2N + 2MN.
+* kernels: the same graph-replay timing for every other row of the path at the
+  W8A16 GEMM M in {64, 512} (TFLOP/s vs 2.5 PF/s fp16 dense),
+  FP32 LayerNorm [4096,768], Softmax [4096,1024], LayerNorm->Softmax [4096,768]
+  (configs[2]) and decode attention B=32 H=12 D=64 L~U[128,1024].
 * cpu_baseline: the CPU restatement of the reference runtime (oracle/) decoding
   the same batch-32 workload for a bounded number of steps on this host.
 """
@@ -20,7 +24,6 @@ from __future__ import annotations
 import argparse
 import ctypes as C
 import json
-import os
 import sys
 import tempfile
 import time
@@ -32,6 +35,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+FP16_DENSE_TFLOPS = 2500.0
 ROTATE_BYTES = 640 << 20
 PROMPT, NEW = 32, 64
 
@@ -43,6 +47,10 @@ def parse():
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--skip-cpu", action="store_true")
+    p.add_argument("--part", default="all", choices=["all", "decode", "gemv", "kernels", "roofline", "copy"],
+                   help="run one part only (for profiler passes; 'roofline' = the dominant GEMV shape only, "
+                        "'copy' = a 512 MiB device copy used to calibrate the HBM byte counters); "
+                        "the driver's JSON line needs 'all'")
     return p.parse_args()
 
 
@@ -50,6 +58,7 @@ def gemv_bytes(m, k, n):
     return 2 * m * k + k * n + 4 * n + 2 * n + 2 * m * n
 
 
+# ---------------------------------------------------------------- decode
 def artifact_path():
     from tinyinfer_amd.artifact import GPT2_SMALL, write_synthetic
     d = Path(tempfile.gettempdir()) / "tinyinfer_amd_gpt2_small_seed42"
@@ -64,12 +73,6 @@ def prompts(batch):
     return [rng.integers(0, 50257, PROMPT).tolist() for _ in range(batch)]
 
 
-def decode_rate(res, batch):
-    t_first = min(res["ttft_ms"])
-    t_last = max(res["total_ms"])
-    return batch * (NEW - 1) / ((t_last - t_first) / 1e3), t_last
-
-
 def run_decode(model, batch, steps, warmup):
     ps = prompts(batch)
     for _ in range(warmup):
@@ -80,28 +83,73 @@ def run_decode(model, batch, steps, warmup):
     for _ in range(steps):
         model.reset_all()
         res = model.greedy(ps, NEW)
-        r, t_last = decode_rate(res, batch)
-        rates.append(r)
+        t_first, t_last = min(res["ttft_ms"]), max(res["total_ms"])
+        rates.append(batch * (NEW - 1) / ((t_last - t_first) / 1e3))
         totals.append(t_last)
-        ttfts.append(min(res["ttft_ms"]))
+        ttfts.append(t_first)
     elapsed = time.perf_counter() - t0
     return {"tokens_per_s": float(np.median(rates)), "samples": rates, "ms_per_step": elapsed / steps * 1e3,
-            "ttft_ms_p50": float(np.median(ttfts)), "total_ms_p50": float(np.median(totals)),
-            "tokens": res["tokens"]}
+            "ms_per_decode_token_step": float(np.median([(t - f) / (NEW - 1) for t, f in zip(totals, ttfts)])),
+            "ttft_ms_p50": float(np.median(ttfts)), "total_ms_p50": float(np.median(totals))}
 
 
-def run_gemv_roofline(reps=5):
-    import torch
+# ---------------------------------------------------------------- graph-replay timing
+class Replay:
+    """Captures a list of native launches (ctypes calls on one torch stream) in a
+    HIP graph and times back-to-back replays with HIP events on that stream."""
+
+    def __init__(self):
+        import torch
+        self.torch = torch
+        self.stream = torch.cuda.Stream()
+
+    def time_us(self, launches, reps=5):
+        t = self.torch
+        with t.cuda.stream(self.stream):
+            launches[0]()  # the first call on a stream creates the library's split-K scratch
+        t.cuda.synchronize()
+        graph = t.cuda.CUDAGraph()
+        with t.cuda.graph(graph, stream=self.stream):
+            for fn in launches:
+                fn()
+        with t.cuda.stream(self.stream):
+            graph.replay()
+            t.cuda.synchronize()
+            e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(self.stream)
+        t.cuda.synchronize()
+        del graph
+        return e0.elapsed_time(e1) * 1e3 / (reps * len(launches))
+
+
+def _lib():
     from tinyinfer_amd.native_ops import NativeOps
     ops = NativeOps()
-    fn = ops.lib.ti_amd_gemm_i8_fused
-    fn.argtypes = [C.c_void_p] * 6 + [C.c_int] * 4 + [C.c_size_t, C.c_int]
+    lib = ops.lib
+    v, i = C.c_void_p, C.c_int
+    lib.ti_amd_gemm_i8_fused.argtypes = [v] * 6 + [i] * 4 + [C.c_size_t, i]
+    lib.ti_amd_layernorm_f32.argtypes = [v, v, v, v, i, i, C.c_float, C.c_size_t, i]
+    lib.ti_amd_softmax_f32.argtypes = [v, v, i, i, C.c_size_t, i]
+    return ops, lib
+
+
+def _check(lib, st):
+    if st:
+        raise RuntimeError(lib.ti_v2_last_error().decode())
+
+
+def run_gemm(rp, shapes):
+    """W8A16 linear with fused bias+GELU over rotating weight sets."""
+    import torch
+    ops, lib = _lib()
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(20261101)
     out = {}
-    stream = torch.cuda.Stream()
-    for (m, k, n) in ((1, 3072, 768), (1, 768, 3072), (8, 3072, 768), (8, 768, 3072)):
+    for (m, k, n) in shapes:
         nsets = max(1, ROTATE_BYTES // (k * n))
         q = torch.randint(-127, 128, (nsets, k * n), dtype=torch.int8, device=dev, generator=g)
         scales = (torch.rand((nsets, n), device=dev, generator=g) * 9e-3 + 1e-3).half().float()
@@ -110,33 +158,98 @@ def run_gemv_roofline(reps=5):
         y = torch.empty((m, n), device=dev, dtype=torch.float16)
 
         def launch(i):
-            st = fn(a.data_ptr(), q[i].data_ptr(), scales[i].data_ptr(), bias[i].data_ptr(), y.data_ptr(), None,
-                    m, n, k, 1, stream.cuda_stream, 0)
-            if st:
-                raise RuntimeError(ops.lib.ti_v2_last_error().decode())
+            return lambda: _check(lib, lib.ti_amd_gemm_i8_fused(
+                a.data_ptr(), q[i].data_ptr(), scales[i].data_ptr(), bias[i].data_ptr(), y.data_ptr(), None,
+                m, n, k, 1, rp.stream.cuda_stream, 0))
 
-        with torch.cuda.stream(stream):
-            launch(0)  # creates the library's split-K scratch for this stream
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(nsets):
-                launch(i)
-        with torch.cuda.stream(stream):
-            graph.replay()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(reps):
-                graph.replay()
-            e1.record(stream)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * nsets)
-        out[f"M{m}_K{k}_N{n}"] = {"us_per_launch": us, "GBps": gemv_bytes(m, k, n) / us / 1e3,
+        us = rp.time_us([launch(i) for i in range(nsets)])
+        nbytes, flops = gemv_bytes(m, k, n), 2.0 * m * k * n
+        out[f"M{m}_K{k}_N{n}"] = {"us_per_launch": us, "GBps": nbytes / us / 1e3, "TFLOPs": flops / us / 1e6,
+                                  "hbm_frac": nbytes / us / 1e3 / HBM_PEAK_GBS,
+                                  "mfma_frac": flops / us / 1e6 / FP16_DENSE_TFLOPS,
                                   "weight_sets": int(nsets), "rotated_MiB": int(nsets * k * n >> 20)}
-        del graph, q, scales, bias
+        del q, scales, bias
         torch.cuda.empty_cache()
     return out
+
+
+def run_rowops(rp):
+    """FP32 LayerNorm [4096,768], Softmax [4096,1024], LN->Softmax [4096,768]."""
+    import torch
+    _, lib = _lib()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    res = {}
+    s = lambda: rp.stream.cuda_stream
+
+    rows, cols = 4096, 768
+    sets = ROTATE_BYTES // (2 * rows * cols * 4) + 1
+    x = torch.randn((sets, rows, cols), device=dev, generator=g)
+    y = torch.empty_like(x)
+    gam = 1 + 0.1 * torch.randn(cols, device=dev, generator=g)
+    bet = 0.1 * torch.randn(cols, device=dev, generator=g)
+    ln = lambda i: (lambda: _check(lib, lib.ti_amd_layernorm_f32(x[i].data_ptr(), gam.data_ptr(), bet.data_ptr(),
+                                                                  y[i].data_ptr(), rows, cols, 1e-5, s(), 0)))
+    us = rp.time_us([ln(i) for i in range(sets)])
+    nb = 2 * rows * cols * 4 + 2 * cols * 4
+    res["layernorm_f32_4096x768"] = {"us_per_launch": us, "GBps": nb / us / 1e3, "hbm_frac": nb / us / 1e3 / HBM_PEAK_GBS}
+    sm2 = lambda i: (lambda: _check(lib, lib.ti_amd_softmax_f32(y[i].data_ptr(), x[i].data_ptr(), rows, cols, s(), 0)))
+    pair = []
+    for i in range(sets):
+        pair += [ln(i), sm2(i)]
+    us2 = rp.time_us(pair) * 2
+    res["layernorm_softmax_f32_4096x768"] = {"us_per_pair": us2, "GBps_fused_ideal_bytes": nb / us2 / 1e3,
+                                             "hbm_frac": nb / us2 / 1e3 / HBM_PEAK_GBS,
+                                             "note": "two launches, as the reference's graph; bytes counted as the "
+                                                     "fused ideal 2*rows*cols*4"}
+    del x, y
+    torch.cuda.empty_cache()
+    rows, cols = 4096, 1024
+    sets = ROTATE_BYTES // (2 * rows * cols * 4) + 1
+    x = 3 * torch.randn((sets, rows, cols), device=dev, generator=g)
+    y = torch.empty_like(x)
+    sm = lambda i: (lambda: _check(lib, lib.ti_amd_softmax_f32(x[i].data_ptr(), y[i].data_ptr(), rows, cols, s(), 0)))
+    us = rp.time_us([sm(i) for i in range(sets)])
+    nb = 2 * rows * cols * 4
+    res["softmax_f32_4096x1024"] = {"us_per_launch": us, "GBps": nb / us / 1e3, "hbm_frac": nb / us / 1e3 / HBM_PEAK_GBS}
+    del x, y
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_decode_attention(rp):
+    """B=32, H=12, D=64, one query per request, L ~ U[128,1024],
+    Q, K, V ~ N(0,1)/8 fp16, packed [B,H,K,D] ABI layout."""
+    import torch
+    ops, lib = _lib()
+    dev = torch.device("cuda:0")
+    B, H, D, KMAX = 32, 12, 64, 1024
+    rng = np.random.default_rng(20261101)
+    L = rng.integers(128, KMAX + 1, B)
+    sets = ROTATE_BYTES // (2 * B * H * KMAX * D * 2) + 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    q = (torch.randn((sets, B, H, 1, D), device=dev, generator=g) / 8).half()
+    k = (torch.randn((sets, B, H, KMAX, D), device=dev, generator=g) / 8).half()
+    v = (torch.randn((sets, B, H, KMAX, D), device=dev, generator=g) / 8).half()
+    out = torch.empty((B, H, 1, D), device=dev, dtype=torch.float16)
+    ql = torch.ones(B, dtype=torch.int32, device=dev)
+    kl = torch.tensor(L, dtype=torch.int32, device=dev)
+    off = kl - 1
+    f = lib.ti_v2_attention_f16
+
+    def launch(i):
+        return lambda: _check(lib, f(q[i].data_ptr(), k[i].data_ptr(), v[i].data_ptr(), out.data_ptr(), ql.data_ptr(),
+                                     kl.data_ptr(), off.data_ptr(), B, H, 1, KMAX, D, 1, 0, rp.stream.cuda_stream, 0))
+
+    us = rp.time_us([launch(i) for i in range(sets)])
+    nb = int(L.sum()) * H * D * 2 * 2 + 2 * B * H * D * 2 + 12 * B
+    res = {"us_per_launch": us, "GBps": nb / us / 1e3, "hbm_frac": nb / us / 1e3 / HBM_PEAK_GBS,
+           "algorithmic_MB": nb / 1e6, "mean_L": float(L.mean()), "sets": int(sets)}
+    del q, k, v
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline_decode(manifest, seconds):
@@ -169,32 +282,51 @@ def main():
     import torch
     from tinyinfer_amd import LLM_LIB, require
     from tinyinfer_amd.runtime import NativeModel
-    manifest = artifact_path()
-    with NativeModel(require(LLM_LIB), manifest, max_batch=32, cache_slots=32, capacity=PROMPT + NEW) as model:
+
+    line = {}
+    if args.part in ("all", "decode"):
+        manifest = artifact_path()
+        with NativeModel(require(LLM_LIB), manifest, max_batch=32, cache_slots=32,
+                         capacity=PROMPT + NEW) as model:
+            b1 = run_decode(model, 1, max(2, args.steps // 2), 1)
+            b32 = run_decode(model, 32, args.steps, args.warmup)
         torch.cuda.synchronize()
-        b1 = run_decode(model, 1, max(2, args.steps // 2), 1)
+        line.update({
+            "metric": "GPT-2 INT8 decode tokens/sec (b=32; b=1 in decode_b1); W8A16 GEMV achieved HBM GB/s in roofline",
+            "value": b32["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": b32["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8 weights x fp16 activations, fp32 accumulate",
+            "data": "synthetic (random-init N(0,0.02) GPT-2 small, seed 42; seeded prompt ids)",
+            "config": {"workload": f"configs[0] GPT-2 small INT8 greedy, batch 32, prompt {PROMPT}, {NEW} new tokens",
+                       "global_batch": 32, "seq_len": PROMPT + NEW, "parallelism": "single GPU"},
+            "decode_b32": b32, "decode_b1": b1})
+    if args.part == "copy":
+        src = torch.ones(128 << 20, dtype=torch.float32, device="cuda")  # 512 MiB
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
         torch.cuda.synchronize()
-        b32 = run_decode(model, 32, args.steps, args.warmup)
-        torch.cuda.synchronize()
-    gemv = run_gemv_roofline()
-    dom = gemv["M1_K3072_N768"]
-    line = {
-        "metric": "GPT-2 INT8 decode tokens/sec (b=32; b=1 in decode_b1); W8A16 GEMV achieved HBM GB/s in roofline",
-        "value": b32["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": b32["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8 weights x fp16 activations, fp32 accumulate",
-        "data": "synthetic (random-init N(0,0.02) GPT-2 small, seed 42; seeded prompt ids)",
-        "config": {"workload": f"configs[0] GPT-2 small INT8 greedy, batch 32, prompt {PROMPT}, {NEW} new tokens",
-                   "global_batch": 32, "seq_len": PROMPT + NEW, "parallelism": "single GPU"},
-        "decode_b32": {k: v for k, v in b32.items() if k != "tokens"},
-        "decode_b1": {k: v for k, v in b1.items() if k != "tokens"},
-        "gemv": gemv,
-        "roofline": {"bound": "hbm", "kernel": "skinny_kernel<int8,MT=1> + split-K epilogue, M=1 K=3072 N=768",
-                     "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": None},
-    }
-    if not args.skip_cpu:
-        line["cpu_baseline"] = cpu_baseline_decode(manifest, args.cpu_seconds)
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "copies": 4}))
+        return
+    rp = Replay() if args.part in ("all", "gemv", "kernels", "roofline") else None
+    if args.part == "roofline":
+        print(json.dumps({"roofline_gemv": run_gemm(rp, ((1, 3072, 768),))}))
+        return
+    if args.part in ("all", "gemv"):
+        gemv = run_gemm(rp, ((1, 3072, 768), (1, 768, 3072), (8, 3072, 768), (8, 768, 3072)))
+        dom = gemv["M1_K3072_N768"]
+        line["gemv"] = gemv
+        line["roofline"] = {"bound": "hbm",
+                            "kernel": "skinny_kernel<int8,MT=1> + splitk_epilogue_kernel, M=1 K=3072 N=768",
+                            "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": None}
+    if args.part in ("all", "kernels"):
+        line["kernels"] = {"gemm_prefill": run_gemm(rp, ((64, 768, 3072), (64, 3072, 768), (512, 768, 3072),
+                                                         (512, 3072, 768))),
+                           "rowops_f32": run_rowops(rp), "decode_attention": run_decode_attention(rp)}
+    if args.part == "all" and not args.skip_cpu:
+        line["cpu_baseline"] = cpu_baseline_decode(artifact_path(), args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 

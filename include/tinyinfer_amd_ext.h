@@ -18,6 +18,15 @@ extern "C" {
 int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const float* scales,
                          const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m,
                          int n, int k, int epilogue, uintptr_t stream, int device);
+
+/* FP32 row LayerNorm / last-axis Softmax on a caller stream: the kernels behind
+ * ti_cuda_layernorm / ti_cuda_softmax (reference backend/runtime.cpp:10-12),
+ * with the v2 conventions (device pointers, stream, device check, status code
+ * instead of abort) so they can be ordered with other work or graph-captured.
+ * Validation as ti_v2_layernorm_f16 / ti_v2_softmax_f16 with 4-byte alignment. */
+int ti_amd_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
+                         int rows, int cols, float eps, uintptr_t stream, int device);
+int ti_amd_softmax_f32(const float* x, float* y, int rows, int cols, uintptr_t stream, int device);
 #ifdef __cplusplus
 }
 #endif

@@ -254,3 +254,21 @@ extern "C" int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const fl
   g.epi.ldr = n;
   return hip_status(tia::gemm(g, scratch, st));
 }
+
+extern "C" int ti_amd_layernorm_f32(const float* x, const float* g, const float* b, float* y, int rows, int cols,
+                                    float eps, uintptr_t stream, int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (!shape_fits({rows, cols}, 4) || !std::isfinite(eps) || eps <= 0.f || !aligned(x, 4) || !aligned(g, 4) ||
+      !aligned(b, 4) || !aligned(y, 4))
+    return fail(TI_V2_INVALID_ARGUMENT, "invalid LayerNorm arguments");
+  return hip_status(tia::layernorm_f32(x, g, b, y, rows, cols, eps, reinterpret_cast<hipStream_t>(stream)));
+}
+
+extern "C" int ti_amd_softmax_f32(const float* x, float* y, int rows, int cols, uintptr_t stream, int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (!shape_fits({rows, cols}, 4) || !aligned(x, 4) || !aligned(y, 4))
+    return fail(TI_V2_INVALID_ARGUMENT, "invalid softmax arguments");
+  return hip_status(tia::softmax_f32(x, y, rows, cols, reinterpret_cast<hipStream_t>(stream)));
+}
