@@ -58,6 +58,17 @@ def gemv_bytes(m, k, n):
     return 2 * m * k + k * n + 4 * n + 2 * n + 2 * m * n
 
 
+def pmc_traffic():
+    """HBM bytes per roofline GEMV launch measured by the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (copy-calibrated) recorded in profiles/; None if absent."""
+    path = ROOT / "profiles" / "w8a16_gemv_m1_k3072_n768_pmc.md"
+    if path.is_file():
+        for text in path.read_text().splitlines():
+            if text.startswith("traffic_bytes_per_launch:"):
+                return int(text.split(":")[1])
+    return None
+
+
 # ---------------------------------------------------------------- decode
 def artifact_path():
     from tinyinfer_amd.artifact import GPT2_SMALL, write_synthetic
@@ -320,7 +331,8 @@ def main():
         line["roofline"] = {"bound": "hbm",
                             "kernel": "skinny_kernel<int8,MT=1> + splitk_epilogue_kernel, M=1 K=3072 N=768",
                             "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": None}
+                            "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": pmc_traffic(),
+                            "algorithmic_bytes": gemv_bytes(1, 3072, 768)}
     if args.part in ("all", "kernels"):
         line["kernels"] = {"gemm_prefill": run_gemm(rp, ((64, 768, 3072), (64, 3072, 768), (512, 768, 3072),
                                                          (512, 3072, 768))),
