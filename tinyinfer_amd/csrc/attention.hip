@@ -30,17 +30,27 @@ struct AttnParams {
   bool vec;  // every pointer and stride allows 16-byte accesses
 };
 
-__device__ __forceinline__ half8_t load8(const uint16_t* p, bool vec) {
-  if (vec) return *reinterpret_cast<const half8_t*>(p);
+template <bool VEC>
+__device__ __forceinline__ half8_t load8(const uint16_t* p) {
+  if constexpr (VEC) return *reinterpret_cast<const half8_t*>(p);
   half8_t out;
 #pragma unroll
   for (int i = 0; i < 8; ++i) out[i] = __builtin_bit_cast(f16, p[i]);
   return out;
 }
 
-template <int D, int QW, int KW>
+// K and V fragments of one tile: NI wave-wide loads each of 64/LPK whole keys.
+template <int NI>
+struct KVTile {
+  half8_t k[NI], v[NI];
+};
+
+template <int D, int QW, int KW, bool VEC, bool FUSEDQKV = false>
 __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
-  constexpr int LPK = D / 8, KPI = 64 / LPK, NI = 64 / KPI;
+  // A tile is NI wave-wide loads: D=64 -> 32 keys, D=128 -> 16 keys.  Two tiles
+  // are kept in registers so the next tile's K and V are in flight while the
+  // current one is scored (one memory round trip per wave, not per tile).
+  constexpr int LPK = D / 8, KPI = 64 / LPK, NI = 4, TK = NI * KPI;
   const AttnArgs& a = p.a;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kg = lane / LPK, ds = lane % LPK;
@@ -61,32 +71,73 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   const uint16_t* vb = a.v + slot * a.kv_sb + int64_t(h) * a.kv_sh + 8 * ds;
 
   half8_t qf = {};
-  if (qi < q_valid) qf = load8(a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(qi) * a.q_sq + 8 * ds, p.vec);
+  if constexpr (FUSEDQKV) {
+    // Wave 0 finishes the deferred QKV GEMM for this (b, h): lane d sums the
+    // split-K partials of q, k and v (bias added, fp16 rounding as the QKV
+    // output), stores k and v into the cache at the new position, and shares q
+    // through LDS.  The barrier orders those stores before any tile load.
+    static_assert(D == 64 && QW == 1, "fused QKV decode is for 64-dim heads, one query");
+    __shared__ f16 sq[64];
+    if (wave == 0 && q_valid > 0) {
+      const int64_t plane = int64_t(a.batch) * 3 * a.hidden;
+      const float* pp = a.qkv_partials + int64_t(b) * 3 * a.hidden + h * 64 + lane;
+      const uint16_t* bq = a.qkv_bias + h * 64 + lane;
+      const float bqv = h2f(bq[0]), bkv = h2f(bq[a.hidden]), bvv = h2f(bq[2 * a.hidden]);
+      float sqv[4] = {0.f, 0.f, 0.f, 0.f}, skv[4] = {0.f, 0.f, 0.f, 0.f}, svv[4] = {0.f, 0.f, 0.f, 0.f};
+      int sp = 0;
+      for (; sp + 4 <= a.qkv_splits; sp += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float* ps = pp + int64_t(sp + u) * plane;
+          sqv[u] += ps[0];
+          skv[u] += ps[a.hidden];
+          svv[u] += ps[2 * a.hidden];
+        }
+      }
+      for (; sp < a.qkv_splits; ++sp) {
+        const float* ps = pp + int64_t(sp) * plane;
+        sqv[0] += ps[0];
+        skv[0] += ps[a.hidden];
+        svv[0] += ps[2 * a.hidden];
+      }
+      sq[lane] = f16(((sqv[0] + sqv[1]) + (sqv[2] + sqv[3])) + bqv);
+      const int64_t pos = a.offsets[b];
+      const int64_t at = slot * a.kv_sb + int64_t(h) * a.kv_sh + pos * D + lane;
+      const_cast<uint16_t*>(a.k)[at] = f2h(((skv[0] + skv[1]) + (skv[2] + skv[3])) + bkv);
+      const_cast<uint16_t*>(a.v)[at] = f2h(((svv[0] + svv[1]) + (svv[2] + svv[3])) + bvv);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[e] = sq[8 * ds + e];
+  } else {
+    if (qi < q_valid) qf = load8<VEC>(a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(qi) * a.q_sq + 8 * ds);
+  }
 
   float m = kNegInf, l = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int k0 = kw * 64; k0 < end; k0 += 64 * KW) {
-    // K and V of the whole 64-key tile are requested before any use: one memory
-    // round trip per tile.
-    half8_t kfr[NI], vfr[NI];
+
+  // Keys at or past `end` re-read key end-1 (valid, written data) instead of
+  // branching, so every load of a tile is unconditional and the compiler can
+  // wait for one tile while the next is still in flight; their scores are -inf
+  // and their probabilities 0 in `process`.
+  auto load_tile = [&](KVTile<NI>& t, int k0) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int key = k0 + kg + KPI * i;
-      if (key < end) {
-        kfr[i] = load8(kb + int64_t(key) * D, p.vec);
-        vfr[i] = load8(vb + int64_t(key) * D, p.vec);
-      } else {
-        kfr[i] = half8_t{};
-        vfr[i] = half8_t{};
-      }
+      const int key = min(k0 + kg + KPI * i, end - 1);
+      t.k[i] = load8<VEC>(kb + int64_t(key) * D);
+      t.v[i] = load8<VEC>(vb + int64_t(key) * D);
     }
+  };
+  // Online-softmax update with one tile (its first key k0 < end is visible, so
+  // the running maximum is finite afterwards).
+  auto process = [&](const KVTile<NI>& t, int k0) {
     float s[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + kg + KPI * i;
       float part = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part += float(qf[e]) * float(kfr[i][e]);
+      for (int e = 0; e < 8; ++e) part += float(qf[e]) * float(t.k[i][e]);
 #pragma unroll
       for (int o = LPK / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
       s[i] = key < end ? part * p.scale : kNegInf;
@@ -96,7 +147,7 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
     for (int i = 1; i < NI; ++i) tmax = fmaxf(tmax, s[i]);
 #pragma unroll
     for (int o = LPK; o < 64; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
-    const float nm = fmaxf(m, tmax);  // finite: key k0 + 0 < end is always visible here
+    const float nm = fmaxf(m, tmax);
     const float alpha = l == 0.f ? 0.f : __expf(m - nm);
     float psum = 0.f;
 #pragma unroll
@@ -107,12 +158,35 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
       const float pr = key < end ? __expf(s[i] - nm) : 0.f;
       psum += pr;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += pr * float(vfr[i][e]);
+      for (int e = 0; e < 8; ++e) acc[e] += pr * float(t.v[i][e]);
     }
 #pragma unroll
     for (int o = LPK; o < 64; o <<= 1) psum += __shfl_xor(psum, o, 64);
     l = l * alpha + psum;
     m = nm;
+  };
+
+  // Wave kw takes tiles kw, kw + KW, ...; tile loads for the next tile are
+  // issued before the current tile is processed (keys past `end` load nothing).
+  // The scheduling barriers keep the compiler from sinking the prefetch loads
+  // next to their uses (which would serialize them again).
+  constexpr int STEP = TK * KW;
+  int k0 = kw * TK;
+  if (k0 < end) {
+    KVTile<NI> ta, tb;
+    load_tile(ta, k0);
+    for (;;) {
+      load_tile(tb, k0 + STEP);
+      __builtin_amdgcn_sched_barrier(0);
+      process(ta, k0);
+      k0 += STEP;
+      if (k0 >= end) break;
+      load_tile(ta, k0 + STEP);
+      __builtin_amdgcn_sched_barrier(0);
+      process(tb, k0);
+      k0 += STEP;
+      if (k0 >= end) break;
+    }
   }
   // Sum the per-key-group partial accumulators: lanes with the same dim segment.
 #pragma unroll
@@ -158,31 +232,49 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   half8_t o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = f16(l > 0.f ? acc[e] * inv : 0.f);
-  if (p.vec) *reinterpret_cast<half8_t*>(op) = o;
+  if constexpr (VEC) *reinterpret_cast<half8_t*>(op) = o;
   else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) op[e] = __builtin_bit_cast(uint16_t, o[e]);
   }
 }
 
-template <int D>
+template <int D, bool VEC>
 hipError_t launch(const AttnParams& p, hipStream_t stream) {
   const AttnArgs& a = p.a;
   const dim3 blocks_per(1, unsigned(a.heads), unsigned(a.batch));
   if (a.q_len == 1) {
-    // Split keys across up to 16 waves so one (b, h) fills a CU.
-    const int tiles = (a.kv_len + 63) / 64;
+    // Decode: one workgroup per (b, h) whose KW waves split the keys.  Aim for
+    // ~2048 waves in total (every workgroup resident at once: 4-wave groups fit
+    // three per CU), never more waves than 32/16-key tiles.
+    const int tile_keys = D == 64 ? 32 : 16;
+    const int tiles = (a.kv_len + tile_keys - 1) / tile_keys;
+    const int64_t groups = int64_t(a.batch) * a.heads;
+    int kw = 1;
+    while (kw < 16 && kw * 2 <= tiles && groups * kw * 2 <= 2048) kw *= 2;
     dim3 grid = blocks_per;
     grid.x = 1;
-    if (tiles >= 12) hipLaunchKernelGGL((attention_kernel<D, 1, 16>), grid, dim3(1024), 0, stream, p);
-    else if (tiles >= 6) hipLaunchKernelGGL((attention_kernel<D, 1, 8>), grid, dim3(512), 0, stream, p);
-    else if (tiles >= 3) hipLaunchKernelGGL((attention_kernel<D, 1, 4>), grid, dim3(256), 0, stream, p);
-    else if (tiles == 2) hipLaunchKernelGGL((attention_kernel<D, 1, 2>), grid, dim3(128), 0, stream, p);
-    else hipLaunchKernelGGL((attention_kernel<D, 1, 1>), grid, dim3(64), 0, stream, p);
+    if (a.qkv_partials) {
+      if constexpr (D == 64 && VEC) {
+        if (kw >= 16) hipLaunchKernelGGL((attention_kernel<64, 1, 16, true, true>), grid, dim3(1024), 0, stream, p);
+        else if (kw == 8) hipLaunchKernelGGL((attention_kernel<64, 1, 8, true, true>), grid, dim3(512), 0, stream, p);
+        else if (kw == 4) hipLaunchKernelGGL((attention_kernel<64, 1, 4, true, true>), grid, dim3(256), 0, stream, p);
+        else if (kw == 2) hipLaunchKernelGGL((attention_kernel<64, 1, 2, true, true>), grid, dim3(128), 0, stream, p);
+        else hipLaunchKernelGGL((attention_kernel<64, 1, 1, true, true>), grid, dim3(64), 0, stream, p);
+        return hipGetLastError();
+      }
+      return hipErrorInvalidValue;
+    }
+    if (kw >= 16) hipLaunchKernelGGL((attention_kernel<D, 1, 16, VEC>), grid, dim3(1024), 0, stream, p);
+    else if (kw == 8) hipLaunchKernelGGL((attention_kernel<D, 1, 8, VEC>), grid, dim3(512), 0, stream, p);
+    else if (kw == 4) hipLaunchKernelGGL((attention_kernel<D, 1, 4, VEC>), grid, dim3(256), 0, stream, p);
+    else if (kw == 2) hipLaunchKernelGGL((attention_kernel<D, 1, 2, VEC>), grid, dim3(128), 0, stream, p);
+    else hipLaunchKernelGGL((attention_kernel<D, 1, 1, VEC>), grid, dim3(64), 0, stream, p);
   } else {
+    if (a.qkv_partials) return hipErrorInvalidValue;
     dim3 grid = blocks_per;
     grid.x = unsigned((a.q_len + 3) / 4);
-    hipLaunchKernelGGL((attention_kernel<D, 4, 1>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((attention_kernel<D, 4, 1, VEC>), grid, dim3(256), 0, stream, p);
   }
   return hipGetLastError();
 }
@@ -199,8 +291,8 @@ hipError_t attention(const AttnArgs& a, hipStream_t stream) {
   p.vec = al16(a.q) && al16(a.k) && al16(a.v) && al16(a.out) && a.q_sb % 8 == 0 && a.q_sh % 8 == 0 &&
           a.q_sq % 8 == 0 && a.kv_sb % 8 == 0 && a.kv_sh % 8 == 0 && a.o_sb % 8 == 0 &&
           a.o_sh % 8 == 0 && a.o_sq % 8 == 0;
-  if (a.head_dim == 64) return launch<64>(p, stream);
-  if (a.head_dim == 128) return launch<128>(p, stream);
+  if (a.head_dim == 64) return p.vec ? launch<64, true>(p, stream) : launch<64, false>(p, stream);
+  if (a.head_dim == 128) return p.vec ? launch<128, true>(p, stream) : launch<128, false>(p, stream);
   return hipErrorInvalidValue;
 }
 

@@ -101,6 +101,14 @@ struct AttnArgs {
   // kv_lengths[b] is ignored and offsets[b] + q_lengths[b] used instead when set
   // (the runtime's slot cache: the visible length follows from the offset).
   bool kv_from_offsets = false;
+  // Decode after a deferred QKV GEMM (q_len == 1, head_dim 64): q, k, v of the new
+  // token of request b are fp16_rn(sum of qkv_partials[s][b][part * hidden + h*64 + d]
+  // + qkv_bias[...]); the kernel stores k, v into the cache at position offsets[b]
+  // and attends with q.  q and out strides are then ignored for q.
+  const float* qkv_partials = nullptr;
+  int qkv_splits = 0;
+  const uint16_t* qkv_bias = nullptr;
+  int hidden = 0;
 };
 hipError_t attention(const AttnArgs& args, hipStream_t stream);
 

@@ -451,9 +451,18 @@ struct ti_llm_model {
       e.layer = l;
       e.layers = L;
       e.capacity = opt.capacity;
-      gemm(norm, rows, c_attn[l], e);
+      // Decode: the skinny GEMM leaves split-K partials and the attention kernel
+      // finishes q, k, v itself (one launch fewer per layer).
+      int qkv_splits = 0;
+      gemm(norm, rows, c_attn[l], e, qlen == 1 && c_attn[l].bias ? &qkv_splits : nullptr);
 
       tia::AttnArgs at;
+      if (qkv_splits > 0) {
+        at.qkv_partials = scratch.partials;
+        at.qkv_splits = qkv_splits;
+        at.qkv_bias = c_attn[l].bias;
+        at.hidden = H;
+      }
       const int64_t head_stride = int64_t(opt.capacity) * kHeadDim;
       at.q = qkv;
       at.q_sb = int64_t(qlen) * 3 * H;
