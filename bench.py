@@ -8,10 +8,13 @@ achieved HBM GB/s".
   seeded prompt ids per request, 64 new tokens, rate B*(new-1)/(t_last-t_first)
   as reference llm/evaluate.py:195 defines it.  One "step" is one such greedy
   batch; batch 1 is reported beside it.
-* roofline: the W8A16 GEMV (skinny MFMA kernel + split-K epilogue, M=1,
-  K=3072 -> N=768, fused bias+GELU) replayed back-to-back from a HIP graph over
-  >= 600 MiB of distinct weight sets (beyond the 256 MiB Infinity Cache), timed
-  with HIP events on the launch stream; algorithmic bytes 2MK + KN + 4N + 2N + 2MN.
+* roofline: the W8A16 decode GEMV over the runtime's panel-packed int8 weights
+  (one kernel, M=1, K=3072 -> N=768, fused bias+GELU) replayed back-to-back from
+  a HIP graph over >= 600 MiB of distinct weight sets (beyond the 256 MiB
+  Infinity Cache), timed with HIP events on the launch stream; algorithmic bytes
+  2MK + KN + 4N + 2N + 2MN.  gemv adds the other configs[1] M <= 8 shapes and
+  the lm_head shape (768 -> 50257); gemv_row_major_abi times the same sweep
+  through the row-major ABI kernel (skinny + split-K epilogue).
 * kernels: the same graph-replay timing for every other row of the path at the
   W8A16 GEMM M in {64, 512} (TFLOP/s vs 2.5 PF/s fp16 dense),
   FP32 LayerNorm [4096,768], Softmax [4096,1024], LayerNorm->Softmax [4096,768]
@@ -142,6 +145,10 @@ def _lib():
     lib = ops.lib
     v, i = C.c_void_p, C.c_int
     lib.ti_amd_gemm_i8_fused.argtypes = [v] * 6 + [i] * 4 + [C.c_size_t, i]
+    lib.ti_amd_gemm_w8p_fused.argtypes = [v] * 6 + [i] * 4 + [C.c_size_t, i]
+    lib.ti_amd_pack_w8.argtypes = [v, i, i, v, C.c_size_t, i]
+    lib.ti_amd_packed_w8_bytes.restype = C.c_int64
+    lib.ti_amd_packed_w8_bytes.argtypes = [i, i]
     lib.ti_amd_layernorm_f32.argtypes = [v, v, v, v, i, i, C.c_float, C.c_size_t, i]
     lib.ti_amd_softmax_f32.argtypes = [v, v, i, i, C.c_size_t, i]
     return ops, lib
@@ -152,8 +159,10 @@ def _check(lib, st):
         raise RuntimeError(lib.ti_v2_last_error().decode())
 
 
-def run_gemm(rp, shapes):
-    """W8A16 linear with fused bias+GELU over rotating weight sets."""
+def run_gemm(rp, shapes, packed=False):
+    """W8A16 linear with fused bias+GELU over rotating weight sets: row-major int8
+    weights through ti_amd_gemm_i8_fused, or (packed=True) the runtime's decode
+    layout through ti_amd_gemm_w8p_fused (weights packed once, outside the timing)."""
     import torch
     ops, lib = _lib()
     dev = torch.device("cuda:0")
@@ -161,15 +170,25 @@ def run_gemm(rp, shapes):
     g.manual_seed(20261101)
     out = {}
     for (m, k, n) in shapes:
-        nsets = max(1, ROTATE_BYTES // (k * n))
+        wbytes = int(lib.ti_amd_packed_w8_bytes(k, n)) if packed else k * n
+        nsets = max(1, ROTATE_BYTES // wbytes)
         q = torch.randint(-127, 128, (nsets, k * n), dtype=torch.int8, device=dev, generator=g)
         scales = (torch.rand((nsets, n), device=dev, generator=g) * 9e-3 + 1e-3).half().float()
         bias = (torch.randn((nsets, n), device=dev, generator=g) * 0.02).half()
         a = torch.randn((m, k), device=dev, generator=g).half()
         y = torch.empty((m, n), device=dev, dtype=torch.float16)
+        if packed:
+            w = torch.empty((nsets, wbytes), dtype=torch.uint8, device=dev)
+            for i in range(nsets):
+                _check(lib, lib.ti_amd_pack_w8(q[i].data_ptr(), k, n, w[i].data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream, 0))
+            torch.cuda.synchronize()
+            del q
+            q = w
+        entry = lib.ti_amd_gemm_w8p_fused if packed else lib.ti_amd_gemm_i8_fused
 
         def launch(i):
-            return lambda: _check(lib, lib.ti_amd_gemm_i8_fused(
+            return lambda: _check(lib, entry(
                 a.data_ptr(), q[i].data_ptr(), scales[i].data_ptr(), bias[i].data_ptr(), y.data_ptr(), None,
                 m, n, k, 1, rp.stream.cuda_stream, 0))
 
@@ -178,7 +197,7 @@ def run_gemm(rp, shapes):
         out[f"M{m}_K{k}_N{n}"] = {"us_per_launch": us, "GBps": nbytes / us / 1e3, "TFLOPs": flops / us / 1e6,
                                   "hbm_frac": nbytes / us / 1e3 / HBM_PEAK_GBS,
                                   "mfma_frac": flops / us / 1e6 / FP16_DENSE_TFLOPS,
-                                  "weight_sets": int(nsets), "rotated_MiB": int(nsets * k * n >> 20)}
+                                  "weight_sets": int(nsets), "rotated_MiB": int(nsets * wbytes >> 20)}
         del q, scales, bias
         torch.cuda.empty_cache()
     return out
@@ -322,14 +341,16 @@ def main():
         return
     rp = Replay() if args.part in ("all", "gemv", "kernels", "roofline") else None
     if args.part == "roofline":
-        print(json.dumps({"roofline_gemv": run_gemm(rp, ((1, 3072, 768),))}))
+        print(json.dumps({"roofline_gemv": run_gemm(rp, ((1, 3072, 768),), packed=True)}))
         return
     if args.part in ("all", "gemv"):
-        gemv = run_gemm(rp, ((1, 3072, 768), (1, 768, 3072), (8, 3072, 768), (8, 768, 3072)))
-        dom = gemv["M1_K3072_N768"]
+        sweep = ((1, 3072, 768), (1, 768, 3072), (8, 3072, 768), (8, 768, 3072))
+        gemv = run_gemm(rp, sweep + ((1, 768, 50257), (32, 768, 50257)), packed=True)
         line["gemv"] = gemv
+        line["gemv_row_major_abi"] = run_gemm(rp, sweep)
+        dom = gemv["M1_K3072_N768"]
         line["roofline"] = {"bound": "hbm",
-                            "kernel": "skinny_kernel<int8,MT=1> + splitk_epilogue_kernel, M=1 K=3072 N=768",
+                            "kernel": "gemv_packed_kernel<MT=1,W=16,CPW=4> (panel-packed int8), M=1 K=3072 N=768",
                             "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": pmc_traffic(),
                             "algorithmic_bytes": gemv_bytes(1, 3072, 768)}

@@ -19,6 +19,24 @@ int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const float* scales
                          const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m,
                          int n, int k, int epilogue, uintptr_t stream, int device);
 
+/* Panel-packed int8 weights for the decode GEMV (M <= 32).  The reference keeps
+ * q row-major [K,N] (reference kernels/src/cuda/tc/gemm.cu:21 reads
+ * q[r*n + c]); the runtime packs every linear once at load so that each wave
+ * load is one contiguous KiB already in MFMA B-operand order:
+ *   record (cb, kc) at byte (cb * ceil(K/64) + kc) * 1024, cb = column block of
+ *   16, kc = K chunk of 64; lane l's 16 bytes = column cb*16 + (l & 15), rows
+ *   kc*64 + 8*(l >> 4) + 0..7 then kc*64 + 32 + 8*(l >> 4) + 0..7; zero past K/N.
+ * ti_amd_packed_w8_bytes: size of the packed copy (0 for an invalid shape).
+ * ti_amd_pack_w8: device q int8 [K,N] -> packed (16-byte aligned), on `stream`.
+ * ti_amd_gemm_w8p_fused: ti_amd_gemm_i8_fused over packed weights; 1 <= M <= 32,
+ * K % 64 == 0, A and packed 16-byte aligned.  Same arithmetic:
+ * Y = epilogue(sum_k A[m,k] * fp16_rn(float(q[k,n]) * scales[n]) + bias[n]). */
+int64_t ti_amd_packed_w8_bytes(int k, int n);
+int ti_amd_pack_w8(const int8_t* q, int k, int n, void* packed, uintptr_t stream, int device);
+int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, const float* scales,
+                          const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m, int n,
+                          int k, int epilogue, uintptr_t stream, int device);
+
 /* FP32 row LayerNorm / last-axis Softmax on a caller stream: the kernels behind
  * ti_cuda_layernorm / ti_cuda_softmax (reference backend/runtime.cpp:10-12),
  * with the v2 conventions (device pointers, stream, device check, status code

@@ -154,6 +154,79 @@ def test_w8a16_sweep_fused_bias_gelu(ops, m, k, n):
     close(h(hbits(res)), expect.astype(np.float16).astype(np.float64))
 
 
+def _pack_gpu(lib, q_dev, k, n):
+    t = torch()
+    lib.ti_amd_packed_w8_bytes.restype = C.c_int64
+    lib.ti_amd_packed_w8_bytes.argtypes = [C.c_int, C.c_int]
+    lib.ti_amd_pack_w8.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_size_t, C.c_int]
+    size = lib.ti_amd_packed_w8_bytes(k, n)
+    out = t.empty(size, dtype=t.uint8, device="cuda")
+    st = lib.ti_amd_pack_w8(q_dev.data_ptr(), k, n, out.data_ptr(), t.cuda.current_stream().cuda_stream, 0)
+    assert st == 0, lib.ti_v2_last_error()
+    return out
+
+
+def _packed(lib, a, packed, s, bias, y, res, m, n, k, epi):
+    t = torch()
+    fn = lib.ti_amd_gemm_w8p_fused
+    fn.argtypes = [C.c_void_p] * 6 + [C.c_int] * 4 + [C.c_size_t, C.c_int]
+    ptr = lambda x: None if x is None else x.data_ptr()
+    st = fn(ptr(a), ptr(packed), ptr(s), ptr(bias), ptr(y), ptr(res), m, n, k, epi,
+            t.cuda.current_stream().cuda_stream, 0)
+    assert st == 0, lib.ti_v2_last_error()
+
+
+@pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (128, 100), (1600, 48)])
+def test_pack_w8_layout_bit_exact(ops, k, n):
+    """The device packer writes exactly the panel layout of the numpy restatement."""
+    from tests.test_packed_layout import pack_w8_numpy
+    rng = np.random.default_rng(k + n)
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    say("pack_w8", k, n)
+    got = host(_pack_gpu(ops.lib, dev(q), k, n))
+    assert np.array_equal(got.view(np.int8), pack_w8_numpy(q))
+
+
+@pytest.mark.parametrize("m", [1, 8, 17, 32])
+@pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (768, 2304), (128, 100), (64, 50257)])
+def test_packed_gemv_against_oracle(ops, m, k, n):
+    """Decode GEMV over panel-packed weights: bias, bias+GELU and in-place residual
+    epilogues against the oracle's fp32-accumulate linear."""
+    t = torch()
+    rng = np.random.default_rng(7 * m + k + n)
+    a = f16(rng.standard_normal((m, k)))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("packed gemv", m, k, n)
+    packed = _pack_gpu(ops.lib, dev(q), k, n)
+    ad, sd, bd = dev(a, t.float16), dev(s), dev(bias, t.float16)
+    y = t.empty((m, n), dtype=t.float16, device="cuda")
+    _packed(ops.lib, ad, packed, sd, bd, y, None, m, n, k, 0)
+    ref = oracle.linear(a, q=q, scales=s, bias_bits=bias)
+    close(h(hbits(y)), h(ref))
+    _packed(ops.lib, ad, packed, sd, bd, y, None, m, n, k, 1)
+    close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, bias_bits=bias, gelu=True)))
+    res = dev(f16(rng.standard_normal((m, n))), t.float16)
+    expect = (h(hbits(res)) + h(ref)).astype(np.float16).astype(np.float64)
+    _packed(ops.lib, ad, packed, sd, bd, res, res, m, n, k, 2)
+    close(h(hbits(res)), expect)
+
+
+def test_packed_gemv_rejects_unsupported_shapes(ops):
+    t = torch()
+    a = t.zeros((33, 64), dtype=t.float16, device="cuda")
+    q = t.zeros((64, 16), dtype=t.int8, device="cuda")
+    packed = _pack_gpu(ops.lib, q, 64, 16)
+    s = t.ones(16, dtype=t.float32, device="cuda")
+    y = t.empty((33, 16), dtype=t.float16, device="cuda")
+    fn = ops.lib.ti_amd_gemm_w8p_fused
+    fn.argtypes = [C.c_void_p] * 6 + [C.c_int] * 4 + [C.c_size_t, C.c_int]
+    say("packed gemv invalid")
+    assert fn(a.data_ptr(), packed.data_ptr(), s.data_ptr(), None, y.data_ptr(), None, 33, 16, 64, 0, 0, 0) == 1
+    assert fn(a.data_ptr(), packed.data_ptr(), s.data_ptr(), None, y.data_ptr(), None, 1, 16, 63, 0, 0, 0) == 1
+
+
 def test_legacy_fp32_gemm(ops):
     t = torch()
     rng = np.random.default_rng(4)

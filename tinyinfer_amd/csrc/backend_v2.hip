@@ -255,6 +255,50 @@ extern "C" int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const fl
   return hip_status(tia::gemm(g, scratch, st));
 }
 
+extern "C" int64_t ti_amd_packed_w8_bytes(int k, int n) {
+  if (!shape_fits({k, n}, 1)) return 0;
+  return int64_t(tia::packed_w8_bytes(k, n));
+}
+
+extern "C" int ti_amd_pack_w8(const int8_t* q, int k, int n, void* packed, uintptr_t stream, int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (!q || !aligned(packed, 16) || !shape_fits({k, n}, 1))
+    return fail(TI_V2_INVALID_ARGUMENT, "pack_w8 needs int8 q[K,N] and a 16-byte aligned output");
+  return hip_status(tia::pack_w8(q, n, k, n, packed, reinterpret_cast<hipStream_t>(stream)));
+}
+
+extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, const float* scales,
+                                     const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m,
+                                     int n, int k, int epilogue, uintptr_t stream, int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (!aligned(a, 16) || !aligned(packed, 16) || !aligned(scales, 4) || !aligned(y, 2) ||
+      (bias && !aligned(bias, 2)) || m < 1 || m > 32 || k % 64 != 0 || !shape_fits({m, k}, 2) ||
+      !shape_fits({k, n}, 1) || !shape_fits({m, n}, 2))
+    return fail(TI_V2_INVALID_ARGUMENT,
+                "packed GEMV needs 1 <= M <= 32, K % 64 == 0, 16-byte aligned A and packed weights");
+  if (epilogue < 0 || epilogue > 2 || (epilogue == 2 && !aligned(residual, 2)))
+    return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
+  tia::GemmArgs g;
+  g.a = a;
+  g.lda = k;
+  g.w = packed;
+  g.w_packed = packed;
+  g.w_int8 = true;
+  g.scales = scales;
+  g.m = m;
+  g.n = n;
+  g.k = k;
+  g.epi.kind = epilogue == 1 ? tia::EPI_GELU : (epilogue == 2 ? tia::EPI_RESIDUAL : tia::EPI_F16);
+  g.epi.bias = bias;
+  g.epi.y = y;
+  g.epi.ldy = n;
+  g.epi.residual = residual;
+  g.epi.ldr = n;
+  return hip_status(tia::gemm(g, nullptr, reinterpret_cast<hipStream_t>(stream)));
+}
+
 extern "C" int ti_amd_layernorm_f32(const float* x, const float* g, const float* b, float* y, int rows, int cols,
                                     float eps, uintptr_t stream, int device) {
   int status = begin(device);

@@ -1,7 +1,14 @@
 // W8A16 / FP16-weight linear layers for gfx950.
 //
-// Two kernels cover the M range of GPT-2 inference:
-//  * skinny (M <= 32, decode): every wave streams weight fragments straight from
+// Three kernels cover the M range of GPT-2 inference:
+//  * packed GEMV (M <= 32, int8 weights in the panel layout the runtime builds
+//    at load): a wave load is one contiguous KiB that is already two MFMA
+//    B operands per lane, so weights go HBM -> VGPR with 16-byte loads; all
+//    loads of a wave are in flight before its first wait, the waves of a
+//    workgroup split K and reduce through LDS, and the epilogue runs in the
+//    same kernel (K is split across workgroups only when the caller finishes
+//    the partials itself).
+//  * skinny (M <= 32, row-major weights of the ABI): every wave streams weight fragments straight from
 //    HBM into MFMA B-operand registers (no LDS for weights), dequantises them in
 //    registers as fp16_rn(float(q) * scale[n]) and runs v_mfma_f32_16x16x32_f16
 //    with A padded to 16/32 rows.  A lane loads one dword (4 consecutive output
@@ -28,27 +35,32 @@
 namespace tia {
 namespace {
 
-__device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc) {
+__device__ __forceinline__ float epilogue_bias(const Epilogue& e, int n) {
+  return e.bias ? h2f(e.bias[n]) : 0.f;
+}
+
+// `bias` is epilogue_bias(e, n) (callers may load it early); EPI_RAW_F32 ignores it.
+__device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias) {
   switch (e.kind) {
     case EPI_RAW_F32:
       static_cast<float*>(e.y)[int64_t(m) * e.ldy + n] = acc;
       return;
     case EPI_F32:
-      static_cast<float*>(e.y)[int64_t(m) * e.ldy + n] = acc + (e.bias ? h2f(e.bias[n]) : 0.f);
+      static_cast<float*>(e.y)[int64_t(m) * e.ldy + n] = acc + bias;
       return;
     case EPI_GELU: {
-      const float h = rt16(acc + (e.bias ? h2f(e.bias[n]) : 0.f));
+      const float h = rt16(acc + bias);
       static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(gelu_tanh(h));
       return;
     }
     case EPI_RESIDUAL: {
-      const float h = rt16(acc + (e.bias ? h2f(e.bias[n]) : 0.f));
+      const float h = rt16(acc + bias);
       const float r = h2f(e.residual[int64_t(m) * e.ldr + n]);
       static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(r + h);
       return;
     }
     case EPI_QKV: {
-      const uint16_t hv = f2h(acc + (e.bias ? h2f(e.bias[n]) : 0.f));
+      const uint16_t hv = f2h(acc + bias);
       static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = hv;
       if (n >= e.hidden) {
         const int b = m / e.qrows, t = m - b * e.qrows;
@@ -64,9 +76,13 @@ __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, 
       return;
     }
     default:  // EPI_F16
-      static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(acc + (e.bias ? h2f(e.bias[n]) : 0.f));
+      static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(acc + bias);
       return;
   }
+}
+
+__device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc) {
+  apply_epilogue(e, m, n, acc, e.kind == EPI_RAW_F32 ? 0.f : epilogue_bias(e, n));
 }
 
 // ---------------------------------------------------------------------------
@@ -274,6 +290,151 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* parti
       apply_epilogue(epi, row, col, ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]);
     }
     __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Panel-packed int8 weights and the decode GEMV over them (M <= 32)
+// ---------------------------------------------------------------------------
+// Panel layout: column block cb (16 columns), K chunk kc (64 rows) is one 1 KiB
+// record at ((cb * KC + kc) * 64 + lane) * 16 bytes; lane's 16 bytes are column
+// cb*16 + (lane & 15), rows kc*64 + 8*(lane >> 4) + r (bytes 0..7) and
+// kc*64 + 32 + 8*(lane >> 4) + r (bytes 8..15), r = 0..7: the B operands of two
+// consecutive v_mfma_f32_16x16x32_f16 steps.  Entries past K or N are 0.
+__global__ void pack_w8_kernel(const int8_t* q, int64_t ldq, int k, int n, int kc, int64_t total16,
+                               u32x4_t* out) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total16;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int lane = int(i & 63);
+    const int64_t rec = i >> 6;
+    const int chunk = int(rec % kc), cb = int(rec / kc);
+    const int col = cb * 16 + (lane & 15), g = lane >> 4;
+    uint32_t d[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int r = (w & 1) * 4 + b;
+        const int row = chunk * 64 + (w >> 1) * 32 + 8 * g + r;
+        const uint8_t byte = (row < k && col < n) ? uint8_t(q[int64_t(row) * ldq + col]) : uint8_t(0);
+        v |= uint32_t(byte) << (8 * b);
+      }
+      d[w] = v;
+    }
+    out[i] = u32x4_t{d[0], d[1], d[2], d[3]};
+  }
+}
+
+struct PackedParams {
+  const uint16_t* a;
+  int64_t lda;
+  const u32x4_t* w;     // panel-packed records
+  const float* scales;  // fp32 [N]
+  int m, n, k;
+  int nb, kc;           // column blocks, K chunks
+  int chunks_per_split, splits;
+  bool defer;
+  Epilogue epi;
+  float* partials;      // [splits][M][N]
+};
+
+// fp16_rn(float(q) * scale) of the 8 bytes in (lo, hi): one MFMA B operand.
+__device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scale) {
+  half8_t out;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[r] = f16(float(int8_t(lo >> (8 * r))) * scale);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[4 + r] = f16(float(int8_t(hi >> (8 * r))) * scale);
+  return out;
+}
+
+// One workgroup of W waves owns column block cb and the K chunks of one split;
+// wave w takes chunks w, w + W, ... and issues the loads of up to CPW of them
+// (weights and A) before the first MFMA, so a split is one memory round trip.
+// The W partial 16-column sums are reduced through LDS in wave order, then the
+// epilogue runs (or fp32 partials are stored for a split/deferred launch).
+// Loads use clamped chunk and row indices, never predicates (rows >= M are
+// computed from row M-1 and never stored).
+template <int MT, int W, int CPW>
+__global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
+  __shared__ float red[W][MT * 256];
+  // The wave index is uniform: chunk bounds below are scalar, so every load of a
+  // round is issued before the first wait.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nbk = gridDim.x, bid = blockIdx.x;
+  const int logical = (nbk % 8 == 0) ? (bid % 8) * (nbk / 8) + bid / 8 : bid;
+  const int cb = logical % p.nb, split = logical / p.nb;
+  const int c_begin = split * p.chunks_per_split;
+  const int c_end = min(p.kc, c_begin + p.chunks_per_split);
+  const int col = cb * 16 + j;
+  const float* scp = p.scales + min(col, p.n - 1);
+  const float colmask = col < p.n ? 1.f : 0.f;
+  // Every output this thread finishes is in column cb*16 + (threadIdx.x & 15):
+  // its bias is fetched now, not after the reduction.
+  const bool epi_now = p.splits == 1 && !p.defer;
+  const float bias_v = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias
+                           ? h2f(p.epi.bias[min(cb * 16 + int(threadIdx.x & 15), p.n - 1)])
+                           : 0.f;
+
+  const u32x4_t* wb = p.w + int64_t(cb) * p.kc * 64 + lane;
+  const uint16_t* arow[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) arow[t] = p.a + int64_t(min(16 * t + j, p.m - 1)) * p.lda + 8 * g;
+
+  float4_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = c_begin + wave; c0 < c_end; c0 += W * CPW) {
+    u32x4_t wf[CPW];
+    half8_t af[CPW][2][MT];
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const int c = min(c0 + i * W, c_end - 1);
+      wf[i] = __builtin_nontemporal_load(wb + int64_t(c) * 64);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          af[i][s][t] = *reinterpret_cast<const half8_t*>(arow[t] + c * 64 + 32 * s);
+    }
+    // The scale is loaded after the round's weights and A (and waited for with
+    // them); the scheduling barrier keeps every load of the round ahead of the
+    // first wait.
+    const float sc = *scp * colmask;
+    __builtin_amdgcn_sched_barrier(0);
+    // A chunk past the split's end re-read the last chunk; its scale is 0 so
+    // its B operands are +-0 and the MFMAs leave the sums unchanged.
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const float si = c0 + i * W < c_end ? sc : 0.f;
+      const half8_t b0 = dequant8(wf[i][0], wf[i][1], si);
+      const half8_t b1 = dequant8(wf[i][2], wf[i][3], si);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][0][t], b0, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][1][t], b1, acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // MFMA output: lane holds rows 4g + v of column j of each 16x16 block.
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave][(16 * t + 4 * g + v) * 16 + j] = acc[t][v];
+  __syncthreads();
+  const int rows = min(p.m, MT * 16);
+  for (int o = threadIdx.x; o < rows * 16; o += W * 64) {
+    const int row = o >> 4, n = cb * 16 + (o & 15);
+    if (n >= p.n) continue;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) s += red[w][o];
+    if (epi_now) apply_epilogue(p.epi, row, n, s, bias_v);
+    else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
   }
 }
 
@@ -506,6 +667,38 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   return hipGetLastError();
 }
 
+// Waves per workgroup W (4, 8 or 16) so that W * 4 chunks cover one split's K
+// range in one round where possible.  Without a caller that finishes partials,
+// one split: the epilogue runs in the same kernel.  A deferred launch may split
+// K further when there are few column blocks (more CUs with loads in flight),
+// keeping at least 4 chunks per split and the partials within the scratch.
+template <int MT>
+hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  PackedParams p{};
+  p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
+  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.nb = (g.n + 15) / 16;
+  p.kc = g.k / 64;
+  int splits = 1;
+  if (deferred && s && s->partials) {
+    splits = std::max(1, std::min((192 + p.nb - 1) / p.nb, p.kc / 4));
+    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
+  }
+  p.chunks_per_split = (p.kc + splits - 1) / splits;
+  splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
+  p.splits = splits;
+  p.defer = deferred != nullptr;
+  p.partials = s ? s->partials : nullptr;
+  if (p.defer && (!p.partials || size_t(splits) * g.m * g.n > s->partial_floats)) return hipErrorInvalidValue;
+  const dim3 grid(unsigned(p.nb) * unsigned(splits));
+  const int cps = p.chunks_per_split;
+  if (cps <= 16) hipLaunchKernelGGL((gemv_packed_kernel<MT, 4, 4>), grid, dim3(256), 0, stream, p);
+  else if (cps <= 32) hipLaunchKernelGGL((gemv_packed_kernel<MT, 8, 4>), grid, dim3(512), 0, stream, p);
+  else hipLaunchKernelGGL((gemv_packed_kernel<MT, 16, 4>), grid, dim3(1024), 0, stream, p);
+  if (deferred) *deferred = splits;
+  return hipGetLastError();
+}
+
 template <bool INT8>
 hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, hipStream_t stream) {
   TiledParams p{};
@@ -534,6 +727,9 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   const bool wvec = ldw % 4 == 0 && ldw >= (int64_t(g.n) + 3) / 4 * 4 &&
                     (g.w_int8 ? wp % 4 == 0 : wp % 8 == 0);
   const bool avec = (g.lda % 8 == 0) && (ap % 16 == 0);
+  if (g.w_int8 && g.w_packed && g.m <= 32 && g.k % 64 == 0 && avec &&
+      reinterpret_cast<uintptr_t>(g.w_packed) % 16 == 0)
+    return g.m <= 16 ? launch_packed<1>(g, s, stream, deferred) : launch_packed<2>(g, s, stream, deferred);
   if (g.m <= 16) return g.w_int8 ? launch_skinny<true, 1>(g, wvec, avec, s, stream, deferred)
                                  : launch_skinny<false, 1>(g, wvec, avec, s, stream, deferred);
   if (g.m <= 32) return g.w_int8 ? launch_skinny<true, 2>(g, wvec, avec, s, stream, deferred)
@@ -561,6 +757,21 @@ const Scratch* library_scratch(int device, hipStream_t stream, hipError_t* err) 
   }
   s.partial_floats = kScratchPartialFloats;
   return &(table[{device, stream}] = s);
+}
+
+size_t packed_w8_bytes(int k, int n) {
+  if (k <= 0 || n <= 0) return 0;
+  return size_t((n + 15) / 16) * size_t((k + 63) / 64) * 1024;
+}
+
+hipError_t pack_w8(const int8_t* q, int64_t ldq, int k, int n, void* out, hipStream_t stream) {
+  if (k <= 0 || n <= 0 || ldq < n) return hipErrorInvalidValue;
+  const int kc = (k + 63) / 64;
+  const int64_t total16 = int64_t(packed_w8_bytes(k, n) / 16);
+  const unsigned blocks = unsigned(std::min<int64_t>((total16 + 255) / 256, 16384));
+  hipLaunchKernelGGL(pack_w8_kernel, dim3(blocks), dim3(256), 0, stream, q, ldq, k, n, kc, total16,
+                     static_cast<u32x4_t*>(out));
+  return hipGetLastError();
 }
 
 hipError_t bias_epilogue(const float* ws, const uint16_t* bias, void* y, int64_t count, int n,

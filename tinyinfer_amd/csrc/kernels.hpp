@@ -53,8 +53,18 @@ struct GemmArgs {
   const float* scales = nullptr;  // fp32 [N] for int8 weights
   int m = 0, n = 0, k = 0;
   int64_t ldw = 0;                // row stride of W in elements; 0 means n
+  // Optional panel-packed copy of the int8 W (pack_w8).  When set, M <= 32,
+  // K % 64 == 0 and A allows 16-byte loads, the GEMV over the packed records runs.
+  const void* w_packed = nullptr;
   Epilogue epi;
 };
+
+// Panel-packed int8 weights: for column block cb (16 columns) and K chunk kc (64
+// rows), a 1 KiB record at (cb * ceil(K/64) + kc) * 1024 bytes holding, for lane
+// l = 0..63, column cb*16 + (l & 15) at rows kc*64 + 8*(l>>4) + 0..7 and
+// kc*64 + 32 + 8*(l>>4) + 0..7 (16 bytes); entries past K or N are zero.
+size_t packed_w8_bytes(int k, int n);
+hipError_t pack_w8(const int8_t* q, int64_t ldq, int k, int n, void* out, hipStream_t stream);
 
 // When `deferred` is non-null and the skinny (M <= 32) kernel runs, the epilogue
 // is skipped: the raw fp32 sums are left in scratch->partials as [splits][M][N]

@@ -238,6 +238,7 @@ struct ti_llm_model {
     const uint16_t* bias = nullptr;
     int k = 0, n = 0;
     int64_t ldw = 0;
+    const void* packed = nullptr;  // panel-packed int8 copy for the decode GEMV
   };
 
   ti_llm_options opt{};
@@ -355,6 +356,23 @@ struct ti_llm_model {
       if (quantized) head.scales = static_cast<const float*>(tensor("lm_head.weight.scales", {V}, "float32"));
     }
     if (used.size() != a.tensors.size()) throw Invalid("unexpected tensor(s) in artifact");
+    // Decode GEMVs read every int8 linear (and the head) from a panel-packed copy
+    // (one contiguous KiB per wave load, already in MFMA B-operand order); the
+    // row-major copy stays for the prefill GEMM.
+    if (quantized && H % 64 == 0) {
+      auto pack = [&](Linear& w) {
+        void* out = alloc<uint8_t>(tia::packed_w8_bytes(w.k, w.n));
+        ck(tia::pack_w8(static_cast<const int8_t*>(w.w), w.ldw, w.k, w.n, out, stream));
+        w.packed = out;
+      };
+      for (int l = 0; l < L; ++l) {
+        pack(c_attn[l]);
+        pack(c_proj[l]);
+        pack(c_fc[l]);
+        pack(c_proj2[l]);
+      }
+      pack(head);
+    }
 
     const size_t rows = size_t(opt.max_batch) * opt.capacity;
     x = alloc<uint16_t>(rows * H);
@@ -404,6 +422,7 @@ struct ti_llm_model {
     g.n = w.n;
     g.k = w.k;
     g.ldw = w.ldw;
+    g.w_packed = w.packed;
     g.epi = epi;
     ck(tia::gemm(g, &scratch, stream, deferred));
   }
