@@ -355,8 +355,9 @@ def main():
                             "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": pmc_traffic(),
                             "algorithmic_bytes": gemv_bytes(1, 3072, 768)}
     if args.part in ("all", "kernels"):
-        line["kernels"] = {"gemm_prefill": run_gemm(rp, ((64, 768, 3072), (64, 3072, 768), (512, 768, 3072),
-                                                         (512, 3072, 768))),
+        prefill = ((64, 768, 3072), (64, 3072, 768), (512, 768, 3072), (512, 3072, 768))
+        line["kernels"] = {"gemm_prefill": run_gemm(rp, prefill, packed=True),
+                           "gemm_prefill_row_major_abi": run_gemm(rp, prefill),
                            "rowops_f32": run_rowops(rp), "decode_attention": run_decode_attention(rp)}
     if args.part == "all" and not args.skip_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(artifact_path(), args.cpu_seconds)

@@ -28,8 +28,10 @@ int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const float* scales
  *   kc*64 + 8*(l >> 4) + 0..7 then kc*64 + 32 + 8*(l >> 4) + 0..7; zero past K/N.
  * ti_amd_packed_w8_bytes: size of the packed copy (0 for an invalid shape).
  * ti_amd_pack_w8: device q int8 [K,N] -> packed (16-byte aligned), on `stream`.
- * ti_amd_gemm_w8p_fused: ti_amd_gemm_i8_fused over packed weights; 1 <= M <= 32,
- * K % 64 == 0, A and packed 16-byte aligned.  Same arithmetic:
+ * ti_amd_gemm_w8p_fused: ti_amd_gemm_i8_fused over packed weights, K % 64 == 0,
+ * A and packed 16-byte aligned; M <= 32 runs the decode GEMV, M > 32 the
+ * multistage MFMA GEMM (64x64 tiles, operands streamed HBM -> LDS with
+ * global_load_lds).  Same arithmetic:
  * Y = epilogue(sum_k A[m,k] * fp16_rn(float(q[k,n]) * scales[n]) + bias[n]). */
 int64_t ti_amd_packed_w8_bytes(int k, int n);
 int ti_amd_pack_w8(const int8_t* q, int k, int n, void* packed, uintptr_t stream, int device);

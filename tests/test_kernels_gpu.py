@@ -213,6 +213,27 @@ def test_packed_gemv_against_oracle(ops, m, k, n):
     close(h(hbits(res)), expect)
 
 
+@pytest.mark.parametrize("m", [33, 64, 130, 512])
+@pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (128, 100), (64, 2000)])
+def test_packed_prefill_gemm_against_oracle(ops, m, k, n):
+    """Prefill (M > 32) GEMM over panel-packed weights: ragged row and column tiles,
+    bias and bias+GELU epilogues against the oracle; fp32-accumulate tolerance."""
+    t = torch()
+    rng = np.random.default_rng(11 * m + k + n)
+    a = f16(rng.standard_normal((m, k)))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("packed prefill gemm", m, k, n)
+    packed = _pack_gpu(ops.lib, dev(q), k, n)
+    ad, sd, bd = dev(a, t.float16), dev(s), dev(bias, t.float16)
+    y = t.empty((m, n), dtype=t.float16, device="cuda")
+    _packed(ops.lib, ad, packed, sd, bd, y, None, m, n, k, 0)
+    close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, bias_bits=bias)))
+    _packed(ops.lib, ad, packed, sd, None, y, None, m, n, k, 1)
+    close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, gelu=True)))
+
+
 def test_packed_gemv_rejects_unsupported_shapes(ops):
     t = torch()
     a = t.zeros((33, 64), dtype=t.float16, device="cuda")
@@ -223,8 +244,9 @@ def test_packed_gemv_rejects_unsupported_shapes(ops):
     fn = ops.lib.ti_amd_gemm_w8p_fused
     fn.argtypes = [C.c_void_p] * 6 + [C.c_int] * 4 + [C.c_size_t, C.c_int]
     say("packed gemv invalid")
-    assert fn(a.data_ptr(), packed.data_ptr(), s.data_ptr(), None, y.data_ptr(), None, 33, 16, 64, 0, 0, 0) == 1
     assert fn(a.data_ptr(), packed.data_ptr(), s.data_ptr(), None, y.data_ptr(), None, 1, 16, 63, 0, 0, 0) == 1
+    assert fn(a.data_ptr() + 2, packed.data_ptr(), s.data_ptr(), None, y.data_ptr(), None, 1, 16, 64, 0, 0, 0) == 1
+    assert fn(a.data_ptr(), packed.data_ptr(), s.data_ptr(), None, y.data_ptr(), None, 0, 16, 64, 0, 0, 0) == 1
 
 
 def test_legacy_fp32_gemm(ops):

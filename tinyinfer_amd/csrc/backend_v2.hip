@@ -274,12 +274,16 @@ extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, cons
   int status = begin(device);
   if (status) return status;
   if (!aligned(a, 16) || !aligned(packed, 16) || !aligned(scales, 4) || !aligned(y, 2) ||
-      (bias && !aligned(bias, 2)) || m < 1 || m > 32 || k % 64 != 0 || !shape_fits({m, k}, 2) ||
-      !shape_fits({k, n}, 1) || !shape_fits({m, n}, 2))
+      (bias && !aligned(bias, 2)) || k % 64 != 0 || !shape_fits({m, k}, 2) || !shape_fits({k, n}, 1) ||
+      !shape_fits({m, n}, 2) || (int64_t(m) + 63) / 64 * ((int64_t(n) + 63) / 64) > (int64_t(1) << 30))
     return fail(TI_V2_INVALID_ARGUMENT,
-                "packed GEMV needs 1 <= M <= 32, K % 64 == 0, 16-byte aligned A and packed weights");
+                "packed GEMM needs K % 64 == 0 and 16-byte aligned A and packed weights");
   if (epilogue < 0 || epilogue > 2 || (epilogue == 2 && !aligned(residual, 2)))
     return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err = hipSuccess;
+  const tia::Scratch* scratch = tia::library_scratch(device, st, &err);
+  if (!scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -296,7 +300,7 @@ extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, cons
   g.epi.ldy = n;
   g.epi.residual = residual;
   g.epi.ldr = n;
-  return hip_status(tia::gemm(g, nullptr, reinterpret_cast<hipStream_t>(stream)));
+  return hip_status(tia::gemm(g, scratch, st));
 }
 
 extern "C" int ti_amd_layernorm_f32(const float* x, const float* g, const float* b, float* y, int rows, int cols,

@@ -439,6 +439,172 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Multistage MFMA GEMM over panel-packed weights (prefill, M > 32)
+// ---------------------------------------------------------------------------
+// Tile BM x BN = (WM * MT * 16) x (WN * R * 16), 4 waves as WM x WN, K in chunks of
+// 64.  Every operand moves HBM/L2 -> LDS with global_load_lds_dwordx4 (no
+// registers), one 1 KiB wave instruction per A fragment (16 rows x 32 K, lanes
+// in MFMA A order) and per packed weight record (already in MFMA B order), so
+// each wave later reads its operands with conflict-free ds_read_b128 at
+// lane * 16.  S LDS stages: while chunk c is multiplied, chunks c+1 .. c+S-2
+// are in flight and c+S-1 is being issued.  Per chunk: wait for this wave's
+// loads of chunk c (vmcnt), barrier (everyone's loads of c landed and everyone
+// finished chunk c-1), issue chunk c+S-1 into the stage of c-1, compute c.
+using global_ptr = const void __attribute__((address_space(1)))*;
+using lds_ptr = void __attribute__((address_space(3)))*;
+
+struct PanelParams {
+  const uint16_t* a;
+  int64_t lda;
+  const u32x4_t* w;     // panel-packed records
+  const float* scales;  // fp32 [N]
+  int m, n, k;
+  int nb, kc;           // column blocks, K chunks
+  int tiles_n, tiles;   // tiles per row of tiles, tiles per split
+  int chunks_per_split, splits;
+  bool defer;
+  Epilogue epi;
+  float* partials;      // [splits][M][N] when splits > 1 or defer
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// Wait until at most `outstanding` chunks of this wave's loads (LPW each) are in
+// flight: vmcnt needs an immediate, so the uniform count selects one of MAX + 1.
+template <int LPW, int I, int MAX>
+__device__ __forceinline__ void wait_chunk(int outstanding) {
+  if constexpr (I >= MAX) {
+    wait_vmcnt<MAX * LPW>();
+  } else {
+    if (outstanding <= I) {
+      wait_vmcnt<I * LPW>();
+      return;
+    }
+    wait_chunk<LPW, I + 1, MAX>(outstanding);
+  }
+}
+
+template <int WM, int WN, int MT, int R, int S>
+__global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
+  constexpr int BM = WM * MT * 16, BN = WN * R * 16;
+  constexpr int NA = (BM / 16) * 2, NB = BN / 16, NL = NA + NB;
+  static_assert(NL % 4 == 0, "loads must split evenly over the waves");
+  constexpr int LPW = NL / 4;
+  constexpr int STAGE = NL * 1024;
+  static_assert(WM * WN == 4 && S >= 3 && (S - 2) * LPW < 64, "4 waves; in-flight loads within vmcnt");
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];  // S * STAGE bytes
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int wm = wave / WN, wn = wave % WN;
+  const int nbk = gridDim.x, bid = blockIdx.x;
+  const int logical = (nbk % 8 == 0) ? (bid % 8) * (nbk / 8) + bid / 8 : bid;
+  const int tile = logical % p.tiles, split = logical / p.tiles;
+  const int tn = tile % p.tiles_n, tm = tile / p.tiles_n;
+  const int m0 = tm * BM, cb0 = tn * NB;
+  const int c_begin = split * p.chunks_per_split;
+  const int kc = min(p.kc - c_begin, p.chunks_per_split);  // chunks of this split (>= 1)
+
+  // This wave's LPW loads per chunk: load id < NA is A fragment (t, s) = (id/2,
+  // id%2): lane (j, g) reads row m0 + 16t + j (clamped), k = 64c + 32s + 8g;
+  // otherwise packed record cb0 + id - NA (clamped): lane reads its 16 bytes.
+  const char* src[LPW];
+  int stride[LPW];
+#pragma unroll
+  for (int l = 0; l < LPW; ++l) {
+    const int id = wave * LPW + l;
+    if (id < NA) {
+      const int t = id >> 1, s = id & 1;
+      const int row = min(m0 + 16 * t + j, p.m - 1);
+      src[l] = reinterpret_cast<const char*>(p.a + int64_t(row) * p.lda + 64 * c_begin + 32 * s + 8 * g);
+      stride[l] = 128;
+    } else {
+      const int cb = min(cb0 + id - NA, p.nb - 1);
+      src[l] = reinterpret_cast<const char*>(p.w + (int64_t(cb) * p.kc + c_begin) * 64 + lane);
+      stride[l] = 1024;
+    }
+  }
+  auto issue = [&](int chunk, int stage) {
+#pragma unroll
+    for (int l = 0; l < LPW; ++l)
+      __builtin_amdgcn_global_load_lds((global_ptr)(src[l] + int64_t(chunk) * stride[l]),
+                                       (lds_ptr)(lds + stage * STAGE + (wave * LPW + l) * 1024), 16, 0, 0);
+  };
+
+  // The tile's BN fp32 scales reach LDS (past the stages) by the same DMA path
+  // (4-byte elements land at lane * 4), issued by wave 0 before its chunk-0
+  // loads, so the chunk-0 wait and barrier cover them: nothing loaded into a
+  // register is used in the loop (the compiler would otherwise wait for every
+  // prologue load up front).  The bias is loaded into registers now and used
+  // only after the loop; a null bias reads A's first element, scaled by 0.
+  static_assert(BN == 64, "one 64-lane scale load per tile");
+  const float* scale_lds = reinterpret_cast<const float*>(lds + S * STAGE);
+  if (wave == 0)
+    __builtin_amdgcn_global_load_lds((global_ptr)(p.scales + min(cb0 * 16 + lane, p.n - 1)),
+                                     (lds_ptr)(lds + S * STAGE), 4, 0, 0);
+  const bool has_bias = p.epi.kind != EPI_RAW_F32 && p.epi.bias;
+  const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
+  const float bmul = has_bias ? 1.f : 0.f;
+  float bias[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) bias[r] = h2f(bsrc[has_bias ? min((cb0 + wn * R + r) * 16 + j, p.n - 1) : 0]) * bmul;
+  float4_t acc[MT][R];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[t][r] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Prologue: chunks 0 .. S-2 (a split shorter than that re-reads its last chunk
+  // into stages it never uses; the waits below stay conservative).
+#pragma unroll
+  for (int c = 0; c < S - 1; ++c) issue(min(c, kc - 1), c);
+  for (int c = 0; c < kc; ++c) {
+    wait_chunk<LPW, 0, S - 2>(min(c + S - 2, kc - 1) - c);
+    __builtin_amdgcn_s_barrier();
+    if (c + S - 1 < kc) issue(c + S - 1, (c + S - 1) % S);
+    const uint8_t* st = lds + (c % S) * STAGE;
+    half8_t bq[R][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float sc = scale_lds[(wn * R + r) * 16 + j];
+      const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(st + (NA + wn * R + r) * 1024 + lane * 16);
+      bq[r][0] = dequant8(raw[0], raw[1], sc);
+      bq[r][1] = dequant8(raw[2], raw[3], sc);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const half8_t af = *reinterpret_cast<const half8_t*>(st + (((wm * MT + t) * 2 + s) * 1024) + lane * 16);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bq[r][s], acc[t][r], 0, 0, 0);
+      }
+  }
+  wait_vmcnt<0>();
+
+  // MFMA output: lane holds rows 4g + v of column j of each 16x16 block.
+  const bool epi_now = p.splits == 1 && !p.defer;
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int col = (cb0 + wn * R + r) * 16 + j;
+      if (col >= p.n) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + (wm * MT + t) * 16 + 4 * g + v;
+        if (row >= p.m) continue;
+        if (epi_now) apply_epilogue(p.epi, row, col, acc[t][r][v], bias[r]);
+        else p.partials[(int64_t(split) * p.m + row) * p.n + col] = acc[t][r][v];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Tiled kernel (M > 32)
 // ---------------------------------------------------------------------------
 struct TiledParams {
@@ -699,6 +865,57 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   return hipGetLastError();
 }
 
+// 64x64 tiles, S = 4 stages of 12 KiB (48 KiB of LDS: three workgroups per CU,
+// three chunks in flight each; six stages measured slower, since occupancy
+// matters more than depth here).  Fewer tiles than ~one per CU split K (at
+// least S - 1 chunks per split) when the caller lets partials go to scratch; a
+// split launch is finished by splitk_epilogue_kernel unless the caller defers it.
+template <int WM, int WN, int MT, int R, int S>
+hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  constexpr int BM = WM * MT * 16, BN = WN * R * 16;
+  constexpr int NL = (BM / 16) * 2 + BN / 16;
+  constexpr size_t kLds = size_t(S) * NL * 1024 + BN * 4;
+  static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&panel_gemm_kernel<WM, WN, MT, R, S>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds));
+  if (attr != hipSuccess) return attr;
+  PanelParams p{};
+  p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
+  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.nb = (g.n + 15) / 16;
+  p.kc = g.k / 64;
+  p.tiles_n = (g.n + BN - 1) / BN;
+  const int64_t tiles = int64_t(p.tiles_n) * ((g.m + BM - 1) / BM);
+  if (tiles > (int64_t(1) << 28)) return hipErrorInvalidValue;
+  p.tiles = int(tiles);
+  int splits = 1;
+  if (s && s->partials && tiles < 192) {
+    splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, p.kc / (S - 1))));
+    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
+  }
+  p.chunks_per_split = (p.kc + splits - 1) / splits;
+  splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
+  p.splits = splits;
+  p.defer = deferred != nullptr && splits > 1;
+  p.partials = s ? s->partials : nullptr;
+  hipLaunchKernelGGL((panel_gemm_kernel<WM, WN, MT, R, S>), dim3(unsigned(tiles * splits)), dim3(256), kLds,
+                     stream, p);
+  if (p.defer) {
+    *deferred = splits;
+    return hipGetLastError();
+  }
+  if (splits > 1) {
+    const int64_t total = int64_t(g.m) * g.n;
+    const unsigned blocks = unsigned(std::min<int64_t>((total + 63) / 64, 8192));
+    hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m, g.n,
+                       g.epi);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_panel(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  return launch_panel_cfg<1, 4, 4, 1, 4>(g, s, stream, deferred);
+}
+
 template <bool INT8>
 hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, hipStream_t stream) {
   TiledParams p{};
@@ -727,9 +944,11 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   const bool wvec = ldw % 4 == 0 && ldw >= (int64_t(g.n) + 3) / 4 * 4 &&
                     (g.w_int8 ? wp % 4 == 0 : wp % 8 == 0);
   const bool avec = (g.lda % 8 == 0) && (ap % 16 == 0);
-  if (g.w_int8 && g.w_packed && g.m <= 32 && g.k % 64 == 0 && avec &&
-      reinterpret_cast<uintptr_t>(g.w_packed) % 16 == 0)
-    return g.m <= 16 ? launch_packed<1>(g, s, stream, deferred) : launch_packed<2>(g, s, stream, deferred);
+  if (g.w_int8 && g.w_packed && g.k % 64 == 0 && avec && reinterpret_cast<uintptr_t>(g.w_packed) % 16 == 0) {
+    if (g.m <= 16) return launch_packed<1>(g, s, stream, deferred);
+    if (g.m <= 32) return launch_packed<2>(g, s, stream, deferred);
+    return launch_panel(g, s, stream, deferred);
+  }
   if (g.m <= 16) return g.w_int8 ? launch_skinny<true, 1>(g, wvec, avec, s, stream, deferred)
                                  : launch_skinny<false, 1>(g, wvec, avec, s, stream, deferred);
   if (g.m <= 32) return g.w_int8 ? launch_skinny<true, 2>(g, wvec, avec, s, stream, deferred)
