@@ -298,6 +298,29 @@ def test_decode_attention_config3(ops):
     close(h(hbits(out)), h(oracle.attention_f16(q, k, v, [1] * B, L, L - 1, True)))
 
 
+@pytest.mark.parametrize("d,nk", [(64, 1024), (64, 1500), (128, 512), (128, 1100)])
+@pytest.mark.parametrize("causal", [0, 1])
+def test_split_decode_attention_ragged(ops, d, nk, causal):
+    """Single-query attention over a long cache runs split over key chunks plus a
+    merge pass: ragged lengths including 0 and 1 visible keys, a request with no
+    query (its output row is zero), offsets that hide the tail when causal."""
+    t = torch()
+    rng = np.random.default_rng(d + nk + causal)
+    B, H = 6, 3
+    kl = [nk, 1, 0, nk - 37, 255, min(513, nk)]
+    ql = [1, 1, 1, 1, 0, 1]
+    off = [nk - 1, 0, 0, nk // 3, 0, 200]
+    q = f16(rng.standard_normal((B, H, 1, d)) * 0.5)
+    k = f16(rng.standard_normal((B, H, nk, d)) * 0.5)
+    v = f16(rng.standard_normal((B, H, nk, d)))
+    say("split decode attention", d, nk, causal)
+    out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
+                        kv_lengths=kl, query_offsets=off, causal=bool(causal))
+    got = h(hbits(out))
+    close(got, h(oracle.attention_f16(q, k, v, ql, kl, off, bool(causal))))
+    assert not got[2].any() and not got[4].any()
+
+
 @pytest.mark.parametrize("nq,nk", [(64, 64), (300, 300), (1, 2000), (3, 700)])
 def test_attention_prefill_and_long(ops, nq, nk):
     t = torch()

@@ -5,9 +5,10 @@
 //   (16 bytes) of one key, so a wave-wide load covers 64/LPK whole keys (128 or
 //   256 contiguous bytes each) and both K and V are read exactly once, fully
 //   coalesced, from either the packed [B,H,K,D] ABI layout or the runtime's
-//   [slot][layer][head][pos][64] cache.  The q.k dot finishes with a
-//   butterfly over the LPK lanes of a key group; probabilities never leave the
-//   lane that owns the key, so PV needs no broadcast.
+//   [slot][layer][head][pos][64] cache.  The q.k dot finishes with a DPP
+//   butterfly inside the LPK lanes of a key group; each key group keeps its
+//   own online-softmax state, so probabilities never leave the lanes that own
+//   the key (PV needs no broadcast) and the groups merge once per wave.
 // A workgroup serves QW queries with KW waves each: KW > 1 splits the keys of a
 // query across waves (decode, where one (b, h) row otherwise gives only
 // B*H waves) and merges their (m, l, acc) states through LDS.
@@ -27,12 +28,14 @@ constexpr float kNegInf = -__builtin_huge_valf();
 struct AttnParams {
   AttnArgs a;
   float scale;
-  bool vec;  // every pointer and stride allows 16-byte accesses
+  bool vec;       // every pointer and stride allows 16-byte accesses
+  float* parts;   // split decode: [B][H][chunks][2 + D] = (m, l, unnormalized acc)
+  int chunks;     // split decode: key chunks per (b, h)
 };
 
 template <bool VEC>
 __device__ __forceinline__ half8_t load8(const uint16_t* p) {
-  if constexpr (VEC) return *reinterpret_cast<const half8_t*>(p);
+  if constexpr (VEC) return __builtin_nontemporal_load(reinterpret_cast<const half8_t*>(p));
   half8_t out;
 #pragma unroll
   for (int i = 0; i < 8; ++i) out[i] = __builtin_bit_cast(f16, p[i]);
@@ -45,17 +48,21 @@ struct KVTile {
   half8_t k[NI], v[NI];
 };
 
-template <int D, int QW, int KW, bool VEC, bool FUSEDQKV = false>
+template <int D, int QW, int KW, bool VEC, bool FUSEDQKV = false, bool SPLIT = false>
 __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
-  // A tile is NI wave-wide loads: D=64 -> 32 keys, D=128 -> 16 keys.  Two tiles
-  // are kept in registers so the next tile's K and V are in flight while the
-  // current one is scored (one memory round trip per wave, not per tile).
+  // A tile is NI wave-wide loads: D=64 -> 32 keys, D=128 -> 16 keys; a wave
+  // loads two tiles at a time.
   constexpr int LPK = D / 8, KPI = 64 / LPK, NI = 4, TK = NI * KPI;
   const AttnArgs& a = p.a;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kg = lane / LPK, ds = lane % LPK;
   const int qslot = wave / KW, kw = wave % KW;
-  const int qi = blockIdx.x * QW + qslot, h = blockIdx.y, b = blockIdx.z;
+  // Split decode: grid (heads, batch, key chunks of 2 * KW tiles), one query; the
+  // chunk index varies slowest so every (b, h)'s first chunks are dispatched
+  // before any trailing (often empty) ones.
+  const int qi = SPLIT ? 0 : blockIdx.x * QW + qslot;
+  const int h = SPLIT ? blockIdx.x : blockIdx.y, b = SPLIT ? blockIdx.y : blockIdx.z;
+  const int chunk_id = SPLIT ? int(blockIdx.z) : 0;
 
   const int q_valid = max(0, min(a.q_len, a.q_lengths[b]));
   int end = 0;
@@ -66,6 +73,10 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
     const int64_t bound = a.causal ? off + qi + 1 : kvv;
     end = int(max<int64_t>(0, min<int64_t>(bound, kvv)));
   }
+  // Keys [kbeg, end) of this workgroup.
+  constexpr int CHUNK = 2 * KW * TK;
+  const int kbeg = chunk_id * CHUNK;
+  if constexpr (SPLIT) end = min(end, kbeg + CHUNK);
   const int64_t slot = a.kv_slot ? int64_t(a.kv_slot[b]) : int64_t(b);
   const uint16_t* kb = a.k + slot * a.kv_sb + int64_t(h) * a.kv_sh + 8 * ds;
   const uint16_t* vb = a.v + slot * a.kv_sb + int64_t(h) * a.kv_sh + 8 * ds;
@@ -109,9 +120,11 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < 8; ++e) qf[e] = sq[8 * ds + e];
-  } else {
-    if (qi < q_valid) qf = load8<VEC>(a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(qi) * a.q_sq + 8 * ds);
   }
+  // Unfused: q is re-read with each pair of tiles (an L2 hit after the first)
+  // rather than once up front, which would make the compiler wait for it
+  // before issuing any K/V load.
+  const uint16_t* qptr = a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(qi) * a.q_sq + 8 * ds;
 
   float m = kNegInf, l = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -128,9 +141,30 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
       t.v[i] = load8<VEC>(vb + int64_t(key) * D);
     }
   };
-  // Online-softmax update with one tile (its first key k0 < end is visible, so
-  // the running maximum is finite afterwards).
-  auto process = [&](const KVTile<NI>& t, int k0) {
+  // Online softmax per key group: the LPK lanes of a key group keep their own
+  // (m, l, acc) over the keys they own, so a tile needs no cross-group
+  // communication; the dot product of a key finishes with a DPP butterfly
+  // inside its group (row_mirror for 16 lanes, row_half_mirror, then two
+  // quad_perm steps: every lane of the group ends with the full sum).  The
+  // groups merge once, after the last tile.
+  auto dpp_add = [](float x, int ctrl_sel) {
+    int v = __builtin_bit_cast(int, x);
+    switch (ctrl_sel) {
+      case 0: v = __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false); break;  // row_mirror
+      case 1: v = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+      case 2: v = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); break;   // quad_perm [1,0,3,2]
+      default: v = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); break;  // quad_perm [2,3,0,1]
+    }
+    return x + __builtin_bit_cast(float, v);
+  };
+  auto group_sum = [&](float x) {
+    static_assert(LPK == 8 || LPK == 16, "key groups of 8 or 16 lanes");
+    if constexpr (LPK == 16) x = dpp_add(x, 0);
+    x = dpp_add(x, 1);
+    x = dpp_add(x, 2);
+    return dpp_add(x, 3);
+  };
+  auto process = [&](const KVTile<NI>& t, int k0, const half8_t& qf) {
     float s[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -138,61 +172,61 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
       float part = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) part += float(qf[e]) * float(t.k[i][e]);
-#pragma unroll
-      for (int o = LPK / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      part = group_sum(part);
       s[i] = key < end ? part * p.scale : kNegInf;
     }
     float tmax = s[0];
 #pragma unroll
     for (int i = 1; i < NI; ++i) tmax = fmaxf(tmax, s[i]);
-#pragma unroll
-    for (int o = LPK; o < 64; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
     const float nm = fmaxf(m, tmax);
     const float alpha = l == 0.f ? 0.f : __expf(m - nm);
-    float psum = 0.f;
+    l *= alpha;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + kg + KPI * i;
       const float pr = key < end ? __expf(s[i] - nm) : 0.f;
-      psum += pr;
+      l += pr;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += pr * float(t.v[i][e]);
     }
-#pragma unroll
-    for (int o = LPK; o < 64; o <<= 1) psum += __shfl_xor(psum, o, 64);
-    l = l * alpha + psum;
     m = nm;
   };
 
-  // Wave kw takes tiles kw, kw + KW, ...; tile loads for the next tile are
-  // issued before the current tile is processed (keys past `end` load nothing).
-  // The scheduling barriers keep the compiler from sinking the prefetch loads
-  // next to their uses (which would serialize them again).
+  // Wave kw takes tiles kw, kw + KW, ... in pairs: both tiles' loads are issued
+  // before the first is scored, so a pair costs one memory round trip.  (A
+  // loop that issues the next tile while scoring the current one gets a full
+  // vmcnt(0) at its header from the compiler, i.e. one round trip per tile.)
   constexpr int STEP = TK * KW;
-  int k0 = kw * TK;
-  if (k0 < end) {
+  for (int k0 = kbeg + kw * TK; k0 < end; k0 += 2 * STEP) {
+    half8_t qv = qf;
+    if constexpr (!FUSEDQKV) qv = load8<VEC>(qptr);
     KVTile<NI> ta, tb;
     load_tile(ta, k0);
-    for (;;) {
-      load_tile(tb, k0 + STEP);
-      __builtin_amdgcn_sched_barrier(0);
-      process(ta, k0);
-      k0 += STEP;
-      if (k0 >= end) break;
-      load_tile(ta, k0 + STEP);
-      __builtin_amdgcn_sched_barrier(0);
-      process(tb, k0);
-      k0 += STEP;
-      if (k0 >= end) break;
-    }
+    load_tile(tb, k0 + STEP);
+    __builtin_amdgcn_sched_barrier(0);  // every load of the pair ahead of the first use
+    process(ta, k0, qv);
+    if (k0 + STEP < end) process(tb, k0 + STEP, qv);
   }
-  // Sum the per-key-group partial accumulators: lanes with the same dim segment.
+  // Merge the key groups of this wave (lanes with the same dim segment): common
+  // maximum over groups that saw a key, rescale, then sum l and acc.
+  {
+    float gm = l > 0.f ? m : kNegInf;
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
+    for (int o = LPK; o < 64; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o, 64));
+    const float f = l > 0.f ? __expf(m - gm) : 0.f;
+    l *= f;
 #pragma unroll
-    for (int o = LPK; o < 64; o <<= 1) acc[e] += __shfl_xor(acc[e], o, 64);
+    for (int e = 0; e < 8; ++e) acc[e] *= f;
+#pragma unroll
+    for (int o = LPK; o < 64; o <<= 1) l += __shfl_xor(l, o, 64);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int o = LPK; o < 64; o <<= 1) acc[e] += __shfl_xor(acc[e], o, 64);
+    m = gm;
+  }
 
   if constexpr (KW > 1) {
     __shared__ float sm[QW][KW], sl[QW][KW];
@@ -223,8 +257,20 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
       }
     }
     l = tl;
+    m = gm;  // the split pass stores (m, l, acc) as one state
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = tacc[e];
+  }
+  if constexpr (SPLIT) {
+    if (kg != 0) return;
+    float* part = p.parts + ((int64_t(b) * a.heads + h) * p.chunks + chunk_id) * (2 + D);
+    if (lane == 0) {
+      part[0] = m;
+      part[1] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[2 + 8 * ds + e] = acc[e];
+    return;
   }
   if (qi >= a.q_len || kg != 0) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -237,6 +283,43 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) op[e] = __builtin_bit_cast(uint16_t, o[e]);
   }
+}
+
+// Second pass of the split decode: one wave per (b, h) merges the chunk states
+// (common maximum over chunks that saw a key, rescale, sum) and writes
+// fp16_rn(acc / l), or 0 when no key was visible.  Up to MAXC chunks are read
+// in one round of loads (clamped indices, unused ones weighted 0).
+template <int D, int MAXC>
+__global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
+  constexpr int DPL = D / 64;  // dims per lane
+  const AttnArgs& a = p.a;
+  const int lane = threadIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const float* base = p.parts + (int64_t(b) * a.heads + h) * p.chunks * (2 + D);
+  float cm[MAXC], cl[MAXC], ca[MAXC][DPL];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const float* part = base + min(c, p.chunks - 1) * (2 + D);
+    cm[c] = part[0];
+    cl[c] = c < p.chunks ? part[1] : 0.f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) ca[c][e] = part[2 + DPL * lane + e];
+  }
+  float gm = kNegInf;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c)
+    if (cl[c] > 0.f) gm = fmaxf(gm, cm[c]);
+  float l = 0.f, acc[DPL] = {};
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const float f = cl[c] > 0.f ? __expf(cm[c] - gm) : 0.f;
+    l += cl[c] * f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] += ca[c][e] * f;
+  }
+  uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + DPL * lane;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) op[e] = f2h(l > 0.f ? acc[e] * inv : 0.f);
 }
 
 template <int D, bool VEC>
@@ -254,6 +337,15 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
     while (kw < 16 && kw * 2 <= tiles && groups * kw * 2 <= 2048) kw *= 2;
     dim3 grid = blocks_per;
     grid.x = 1;
+    if (p.parts) {
+      // Long caches: 4-wave workgroups over chunks of 2 * 4 tiles (all of a
+      // wave's loads in flight at once), spread over every CU, then a merge.
+      const dim3 split_grid(unsigned(a.heads), unsigned(a.batch), unsigned(p.chunks));
+      hipLaunchKernelGGL((attention_kernel<D, 1, 4, VEC, false, true>), split_grid, dim3(256), 0, stream, p);
+      if (p.chunks <= 8) hipLaunchKernelGGL((attention_combine_kernel<D, 8>), grid, dim3(64), 0, stream, p);
+      else hipLaunchKernelGGL((attention_combine_kernel<D, 32>), grid, dim3(64), 0, stream, p);
+      return hipGetLastError();
+    }
     if (a.qkv_partials) {
       if constexpr (D == 64 && VEC) {
         if (kw >= 16) hipLaunchKernelGGL((attention_kernel<64, 1, 16, true, true>), grid, dim3(1024), 0, stream, p);
@@ -283,10 +375,21 @@ bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 }  // namespace
 
-hipError_t attention(const AttnArgs& a, hipStream_t stream) {
+hipError_t attention(const AttnArgs& a, hipStream_t stream, const Scratch* scratch) {
   if (a.batch <= 0 || a.heads <= 0 || a.q_len <= 0) return hipSuccess;
   AttnParams p{};
   p.a = a;
+  // Decode over a long cache (at least 4 chunks of 256/128 keys per (b, h)) and
+  // enough scratch for the chunk states: split the keys across workgroups.
+  if (scratch && scratch->partials && a.q_len == 1 && !a.qkv_partials && (a.head_dim == 64 || a.head_dim == 128)) {
+    const int chunk = a.head_dim == 64 ? 256 : 128;
+    const int chunks = (a.kv_len + chunk - 1) / chunk;
+    const size_t need = size_t(a.batch) * a.heads * chunks * (2 + a.head_dim);
+    if (chunks >= 4 && chunks <= 32 && need <= scratch->partial_floats) {
+      p.parts = scratch->partials;
+      p.chunks = chunks;
+    }
+  }
   p.scale = float(1.0 / __builtin_sqrt(double(a.head_dim)));
   p.vec = al16(a.q) && al16(a.k) && al16(a.v) && al16(a.out) && a.q_sb % 8 == 0 && a.q_sh % 8 == 0 &&
           a.q_sq % 8 == 0 && a.kv_sb % 8 == 0 && a.kv_sh % 8 == 0 && a.o_sb % 8 == 0 &&

@@ -193,7 +193,13 @@ extern "C" int ti_v2_attention_f16(const uint16_t* q, const uint16_t* k, const u
   a.kv_len = nk;
   a.head_dim = d;
   a.causal = causal != 0;
-  return hip_status(tia::attention(a, reinterpret_cast<hipStream_t>(stream)));
+  // The library's per-stream scratch lets a long single-query call split its
+  // keys across workgroups; without it (first call on a stream under graph
+  // capture) the one-pass kernel runs.
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t scratch_err = hipSuccess;
+  const tia::Scratch* scratch = tia::library_scratch(device, st, &scratch_err);
+  return hip_status(tia::attention(a, st, scratch));
 }
 
 extern "C" int ti_v2_layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,

@@ -120,7 +120,10 @@ struct AttnArgs {
   const uint16_t* qkv_bias = nullptr;
   int hidden = 0;
 };
-hipError_t attention(const AttnArgs& args, hipStream_t stream);
+// With a scratch, single-query attention over a long cache (kv_len >= 1024 for
+// head_dim 64, >= 512 for 128) splits the keys of each (b, h) across
+// workgroups and merges the chunk states in a second kernel.
+hipError_t attention(const AttnArgs& args, hipStream_t stream, const Scratch* scratch = nullptr);
 
 hipError_t layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
                          int rows, int cols, float eps, hipStream_t stream);
