@@ -19,6 +19,8 @@ achieved HBM GB/s".
   W8A16 GEMM M in {64, 512} (TFLOP/s vs 2.5 PF/s fp16 dense),
   FP32 LayerNorm [4096,768], Softmax [4096,1024], LayerNorm->Softmax [4096,768]
   (configs[2]) and decode attention B=32 H=12 D=64 L~U[128,1024].
+* limits: the machine limits those rows are read against (launch floor of an
+  empty kernel, pure streaming reads of the same sizes; libtinyinfer_diag.so).
 * cpu_baseline: the CPU restatement of the reference runtime (oracle/) decoding
   the same batch-32 workload for a bounded number of steps on this host.
 """
@@ -50,10 +52,12 @@ def parse():
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--skip-cpu", action="store_true")
-    p.add_argument("--part", default="all", choices=["all", "decode", "gemv", "kernels", "roofline", "copy"],
+    p.add_argument("--part", default="all",
+                   choices=["all", "decode", "gemv", "kernels", "roofline", "copy", "limits", "xl"],
                    help="run one part only (for profiler passes; 'roofline' = the dominant GEMV shape only, "
-                        "'copy' = a 512 MiB device copy used to calibrate the HBM byte counters); "
-                        "the driver's JSON line needs 'all'")
+                        "'copy' = a 512 MiB device copy used to calibrate the HBM byte counters, "
+                        "'xl' = configs[4] GPT-2 XL, not part of 'all': its synthetic artifact takes ~2 min "
+                        "to write); the driver's JSON line needs 'all'")
     return p.parse_args()
 
 
@@ -282,6 +286,91 @@ def run_decode_attention(rp):
     return res
 
 
+def run_xl(steps):
+    """GPT-2 XL INT8 (48 layers, d 1600, 25 heads, MLP 6400), random-init
+    N(0,0.02) seed 42; 64 requests with seeded prompt lengths U[128,512] (ids
+    U[0,50257)), prefill then 128 greedy tokens each.  The runtime ABI takes at
+    most 32 rows per call (reference max_batch), so the 64 requests run as two
+    batches of 32 in their own KV slots; decode tokens/s = 64 * 127 / (sum over the
+    two batches of t_last - t_first)."""
+    from tinyinfer_amd import LLM_LIB, require
+    from tinyinfer_amd.artifact import GPT2_XL, write_synthetic
+    from tinyinfer_amd.runtime import NativeModel
+    d = Path(tempfile.gettempdir()) / "tinyinfer_amd_gpt2_xl_seed42"
+    m = d / "manifest.json"
+    t0 = time.perf_counter()
+    if not m.exists():
+        def progress(name):
+            if name.endswith("mlp.c_proj.weight"):
+                print(f"[xl] artifact: wrote {name}", file=sys.stderr, flush=True)
+        write_synthetic(d, GPT2_XL, seed=42, progress=progress)
+    gen_s = time.perf_counter() - t0
+    rng = np.random.default_rng(42)
+    lens = rng.integers(128, 513, 64)
+    prompts = [rng.integers(0, 50257, int(n)).tolist() for n in lens]
+    new = 128
+    runs = []
+    with NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=64, capacity=640) as model:
+        for rep in range(max(1, steps) + 1):  # first repetition is warmup
+            model.reset_all()
+            decode_s, ttft = 0.0, []
+            t_run = time.perf_counter()
+            for half in (0, 1):
+                res = model.greedy(prompts[32 * half:32 * half + 32], new, slots=list(range(32 * half, 32 * half + 32)))
+                t_first, t_last = min(res["ttft_ms"]), max(res["total_ms"])
+                decode_s += (t_last - t_first) / 1e3
+                ttft.append(t_first)
+            if rep:
+                runs.append({"decode_tokens_per_s": 64 * (new - 1) / decode_s, "ttft_ms": ttft,
+                             "wall_s": time.perf_counter() - t_run})
+    rates = [r["decode_tokens_per_s"] for r in runs]
+    return {"decode_tokens_per_s": float(np.median(rates)), "samples": rates,
+            "ttft_ms_p50_per_batch": [float(np.median([r["ttft_ms"][i] for r in runs])) for i in (0, 1)],
+            "wall_s_per_run": float(np.median([r["wall_s"] for r in runs])),
+            "prompt_len_mean": float(lens.mean()), "requests": 64, "new_tokens": new,
+            "weights_bytes": int((d / "weights.bin").stat().st_size), "artifact_generation_s": gen_s,
+            "note": "two runtime batches of 32 (reference max_batch), KV slots 0..63, capacity 640"}
+
+
+def run_limits(rp):
+    """The machine limits the roofline figures are read against, measured with the
+    diagnostic kernels of libtinyinfer_diag.so: the per-launch floor of an empty
+    kernel replayed back to back from a graph, and pure 16-byte streaming reads of
+    the GEMV's size (2.25 MiB over 192 workgroups), the decode-attention size
+    (48 MiB over 768 workgroups), a long stream (512 MiB over 256 workgroups) and
+    one CU's ceiling (32 workgroups of 1024 threads, 256 KiB each), each over
+    rotating buffers (1 GiB)."""
+    import torch
+    from tinyinfer_amd import DIAG_LIB, require
+    lib = C.CDLL(str(require(DIAG_LIB)))
+    lib.tia_diag_empty.argtypes = [C.c_size_t]
+    lib.tia_diag_stream.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_size_t]
+    s = lambda: rp.stream.cuda_stream
+    res = {"empty_kernel_us_per_launch": rp.time_us([lambda: _check_diag(lib.tia_diag_empty(s()))] * 256)}
+    total = 1 << 30
+    src = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    out = torch.empty(1 << 22, dtype=torch.int32, device="cuda")
+    for name, per_wg, wgs, thr in (("stream_2.25MiB_192wg", 12 << 10, 192, 256),
+                                   ("stream_48MiB_768wg", 64 << 10, 768, 256),
+                                   ("stream_512MiB_256wg", 2 << 20, 256, 256),
+                                   ("one_cu_256KiB_32wg_1024thr", 256 << 10, 32, 1024)):
+        nbytes = per_wg * wgs
+        sets = max(1, min(64, total // nbytes))
+        launches = [(lambda off: lambda: _check_diag(lib.tia_diag_stream(
+            src.data_ptr() + off, out.data_ptr(), per_wg, wgs, thr, s())))(i * nbytes) for i in range(sets)]
+        us = rp.time_us(launches)
+        res[name] = {"us_per_launch": us, "GBps": nbytes / us / 1e3, "per_workgroup_GBps": per_wg / us / 1e3,
+                     "bytes": nbytes, "hbm_frac": nbytes / us / 1e3 / HBM_PEAK_GBS}
+    del src
+    torch.cuda.empty_cache()
+    return res
+
+
+def _check_diag(status):
+    if status:
+        raise RuntimeError("diagnostic launch failed")
+
+
 def cpu_baseline_decode(manifest, seconds):
     """The oracle's CPU GPT-2 (restating reference llm/src/runtime.cu) on the batch-32
     workload: one prefill of 32 x 32 tokens, then single-token steps until the time
@@ -331,6 +420,9 @@ def main():
             "config": {"workload": f"configs[0] GPT-2 small INT8 greedy, batch 32, prompt {PROMPT}, {NEW} new tokens",
                        "global_batch": 32, "seq_len": PROMPT + NEW, "parallelism": "single GPU"},
             "decode_b32": b32, "decode_b1": b1})
+    if args.part == "xl":
+        print(json.dumps({"xl": run_xl(args.steps)}), flush=True)
+        return
     if args.part == "copy":
         src = torch.ones(128 << 20, dtype=torch.float32, device="cuda")  # 512 MiB
         dst = torch.empty_like(src)
@@ -339,7 +431,10 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "copies": 4}))
         return
-    rp = Replay() if args.part in ("all", "gemv", "kernels", "roofline") else None
+    rp = Replay() if args.part in ("all", "gemv", "kernels", "roofline", "limits") else None
+    if args.part == "limits":
+        print(json.dumps({"limits": run_limits(rp)}))
+        return
     if args.part == "roofline":
         print(json.dumps({"roofline_gemv": run_gemm(rp, ((1, 3072, 768),), packed=True)}))
         return
@@ -359,6 +454,7 @@ def main():
         line["kernels"] = {"gemm_prefill": run_gemm(rp, prefill, packed=True),
                            "gemm_prefill_row_major_abi": run_gemm(rp, prefill),
                            "rowops_f32": run_rowops(rp), "decode_attention": run_decode_attention(rp)}
+        line["limits"] = run_limits(rp)
     if args.part == "all" and not args.skip_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(artifact_path(), args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -11,17 +11,18 @@ import pytest
 
 import oracle
 from tests.conftest import GOLDEN, ROOT
-from tinyinfer_amd import BACKEND_LIB, CODEC_LIB, LLM_LIB
+from tinyinfer_amd import BACKEND_LIB, CODEC_LIB, DIAG_LIB, LLM_LIB
 
 HEADERS = {"tinyinfer_backend_v2.h": BACKEND_LIB, "tinyinfer_backend.h": BACKEND_LIB,
            "tinyinfer_amd_ext.h": BACKEND_LIB,
-           "tinyinfer_host_codec.h": CODEC_LIB, "tinyinfer_llm.h": LLM_LIB}
+           "tinyinfer_host_codec.h": CODEC_LIB, "tinyinfer_llm.h": LLM_LIB,
+           "tinyinfer_amd_diag.h": DIAG_LIB}
 
 
 def declared(header):
     text = (ROOT / "include" / header).read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ti_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(tia?_[a-z0-9_]+)\s*\(", text)))
 
 
 @pytest.mark.parametrize("header", sorted(HEADERS))

@@ -1,0 +1,103 @@
+"""GPT-2 XL shapes through libtinyinfer_llm.so (BASELINE configs[4] architecture:
+hidden 1600, 25 heads x 64, MLP 6400, vocab 50257) on a 2-layer synthetic INT8
+artifact, against the CPU oracle (restating reference llm/src/runtime.cu).
+
+The two layers exercise every XL-specific shape of the path: K = 1600 and 6400
+(25 and 100 chunks of the packed GEMV/GEMM), N = 4800 / 1600 / 6400 / 50257,
+25-head attention over ragged prompts up to 300 tokens, and the fused
+residual+LayerNorm finisher at 1600 columns.  Tolerances as the small model:
+logits within atol 5e-2, greedy tokens identical or diverging only at
+near-ties (oracle logit gap within 5e-2), first divergence reported.
+"""
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+NEW_TOKENS = 16
+
+
+def say(*args):
+    print("[case]", *args, flush=True)
+
+
+@pytest.fixture(scope="module")
+def artifact(tmp_path_factory):
+    from tinyinfer_amd.artifact import GPT2_XL, write_synthetic
+    say("writing 2-layer GPT-2 XL-shaped synthetic artifact")
+    return write_synthetic(tmp_path_factory.mktemp("gpt2xl2"), dict(GPT2_XL, layers=2), seed=7)
+
+
+@pytest.fixture(scope="module")
+def model(artifact):
+    from tinyinfer_amd import LLM_LIB
+    from tinyinfer_amd.runtime import NativeModel
+    say("creating native XL-shaped model")
+    with NativeModel(LLM_LIB, artifact, max_batch=8, cache_slots=9, capacity=512) as m:
+        yield m
+
+
+@pytest.fixture(scope="module")
+def cpu_model(artifact):
+    from tinyinfer_amd.artifact import load_tensors
+    manifest, tensors = load_tensors(artifact)
+    m = oracle.Gpt2(tensors, manifest["architecture"], slots=9, capacity=512)
+    yield m
+    m.close()
+
+
+def logits_of(result):
+    return np.frombuffer(result["logits"], dtype=np.float32).reshape(result["shape"]).copy()
+
+
+def test_xl_logits_match_oracle(model, cpu_model):
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, 50257, n).tolist() for n in (300, 37, 1, 130)]
+    slots = [0, 1, 2, 3]
+    say("xl logits vs oracle")
+    model.reset_all()
+    gpu = logits_of(model.forward(slots, prompts))
+    for s in slots:
+        cpu_model.reset(s)
+    cpu, nxt = cpu_model.forward(slots, prompts)
+    err = np.abs(gpu - cpu)
+    print(f"prefill max |logit diff| {err.max():.3g}")
+    assert err.max() <= 5e-2
+    for _ in range(3):  # decode steps (captured graph path) on top of the prefill
+        step = [[int(t)] for t in nxt]
+        gpu2 = logits_of(model.forward(slots, step))
+        cpu2, nxt = cpu_model.forward(slots, step)
+        print(f"decode max |logit diff| {np.abs(gpu2 - cpu2).max():.3g}")
+        assert np.abs(gpu2 - cpu2).max() <= 5e-2
+    model.reset_all()
+
+
+def first_divergence(a, b):
+    for i, (x, y) in enumerate(zip(a, b)):
+        if x != y:
+            return i
+    return None if len(a) == len(b) else min(len(a), len(b))
+
+
+def test_xl_greedy_matches_oracle(model, cpu_model):
+    rng = np.random.default_rng(11)
+    prompts = [rng.integers(0, 50257, n).tolist() for n in (128, 200, 17, 64)]
+    say("xl greedy vs oracle")
+    model.reset_all()
+    gpu = model.greedy(prompts, NEW_TOKENS)["tokens"]
+    for s in range(len(prompts)):
+        cpu_model.reset(s)
+    cpu = cpu_model.greedy(list(range(len(prompts))), prompts, NEW_TOKENS)
+    diverged = {b: i for b, i in ((b, first_divergence(g, c)) for b, (g, c) in enumerate(zip(gpu, cpu)))
+                if i is not None}
+    margins = {}
+    for b, i in diverged.items():
+        cpu_model.reset(8)
+        lg, _ = cpu_model.forward([8], [prompts[b] + cpu[b][:i]])
+        margins[b] = float(lg[0][cpu[b][i]] - lg[0][gpu[b][i]])
+    print(f"xl greedy: {len(prompts) - len(diverged)}/{len(prompts)} identical over {NEW_TOKENS} tokens; "
+          f"first divergence index {diverged}; oracle logit gap at divergence {margins}")
+    assert all(0 <= m <= 5e-2 for m in margins.values()), margins
+    model.reset_all()

@@ -101,12 +101,13 @@ def _normal_f16(rng, shape, mean, std):
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std) + np.float32(mean)).astype(np.float16)
 
 
-def write_synthetic(dest, arch=None, seed=42, precision="int8", std=0.02):
+def write_synthetic(dest, arch=None, seed=42, precision="int8", std=0.02, progress=None):
     """Write a random-init GPT-2 artifact: every weight matrix, embedding and bias
     ~ N(0, std), LayerNorm gamma ~ N(1, std), beta ~ N(0, std) (numpy PCG64 from
     ``seed``), stored fp16; linears and the tied head INT8-quantized.  Returns the
     manifest path.  Quantized bytes must agree between the native codec and the
-    numpy quantizer, as the reference exporter requires (export_weights.py:146-151)."""
+    numpy quantizer, as the reference exporter requires (export_weights.py:146-151).
+    ``progress``, if given, is called with each tensor name as it is written."""
     arch = dict(GPT2_SMALL if arch is None else arch)
     dest = Path(dest)
     dest.mkdir(parents=True, exist_ok=True)
@@ -147,6 +148,8 @@ def write_synthetic(dest, arch=None, seed=42, precision="int8", std=0.02):
                 write(name + ".scales", "float32", [shape[1]], sc)
             else:
                 write(name, "float16", shape, vals.view(np.uint16))
+            if progress:
+                progress(name)
         head = np.ascontiguousarray(wte.T)  # [hidden, vocab]
         if precision == "int8":
             q, sc = codec.quantize(head.view(np.uint16))
