@@ -371,6 +371,41 @@ def _check_diag(status):
         raise RuntimeError("diagnostic launch failed")
 
 
+def run_prefill_attention(rp):
+    """Causal prefill attention through ti_v2_attention_f16 (MFMA kernel): the
+    reference's published online-attention case (B=1, H=4, Q=K=4096, D=64;
+    kernels/src/cuda/tc/README.md:75, 8.594944 ms on an RTX 3080) and a GPT-2
+    small prefill (B=32, H=12, Q=K=512, D=64).  flops = 4*B*H*D*(causal pairs)."""
+    import torch
+    _, lib = _lib()
+    f = lib.ti_v2_attention_f16
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    res = {}
+    for B, H, N, D in ((1, 4, 4096, 64), (32, 12, 512, 64)):
+        sets = 4
+        q = (torch.randn((sets, B, H, N, D), device=dev, generator=g) * 0.5).half()
+        k = (torch.randn((sets, B, H, N, D), device=dev, generator=g) * 0.5).half()
+        v = torch.randn((sets, B, H, N, D), device=dev, generator=g).half()
+        out = torch.empty((B, H, N, D), device=dev, dtype=torch.float16)
+        ql = torch.full((B,), N, dtype=torch.int32, device=dev)
+        off = torch.zeros(B, dtype=torch.int32, device=dev)
+
+        def launch(i):
+            return lambda: _check(lib, f(q[i].data_ptr(), k[i].data_ptr(), v[i].data_ptr(), out.data_ptr(),
+                                         ql.data_ptr(), ql.data_ptr(), off.data_ptr(), B, H, N, N, D, 1, 0,
+                                         rp.stream.cuda_stream, 0))
+
+        us = rp.time_us([launch(i) for i in range(sets)] * 4)
+        flops = 4.0 * B * H * D * (N * (N + 1) / 2)
+        res[f"B{B}_H{H}_Q{N}_K{N}_D{D}_causal"] = {"us_per_launch": us, "TFLOPs": flops / us / 1e6,
+                                                    "mfma_frac": flops / us / 1e6 / FP16_DENSE_TFLOPS}
+        del q, k, v
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline_decode(manifest, seconds):
     """The oracle's CPU GPT-2 (restating reference llm/src/runtime.cu) on the batch-32
     workload: one prefill of 32 x 32 tokens, then single-token steps until the time
@@ -453,7 +488,8 @@ def main():
         prefill = ((64, 768, 3072), (64, 3072, 768), (512, 768, 3072), (512, 3072, 768))
         line["kernels"] = {"gemm_prefill": run_gemm(rp, prefill, packed=True),
                            "gemm_prefill_row_major_abi": run_gemm(rp, prefill),
-                           "rowops_f32": run_rowops(rp), "decode_attention": run_decode_attention(rp)}
+                           "rowops_f32": run_rowops(rp), "decode_attention": run_decode_attention(rp),
+                           "prefill_attention": run_prefill_attention(rp)}
         line["limits"] = run_limits(rp)
     if args.part == "all" and not args.skip_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(artifact_path(), args.cpu_seconds)

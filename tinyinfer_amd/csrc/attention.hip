@@ -322,6 +322,183 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
   for (int e = 0; e < DPL; ++e) op[e] = f2h(l > 0.f ? acc[e] * inv : 0.f);
 }
 
+// Prefill (several queries per request) on MFMA, flash-attention style in the
+// transposed form, so that no operand ever moves between lanes:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = 16 keys x 32 dims of K (LDS),
+//                 B = Q^T (registers: lane (j, g) holds query j, dims 8g..8g+7);
+//                 lane (j, g) receives the scores of query j for keys 4g..4g+3;
+//   P^T = exp(S^T - m) rounded to fp16: exactly the B operand of
+//   O^T += V^T P^T  v_mfma_f32_16x16x16_f16, A = 16 dims x 16 keys of V^T (LDS,
+//                 V is staged transposed), lane (j, g) accumulates query j's
+//                 dims 16db + 4g + v.
+// So a query's running max, sum and rescale stay in the four lanes (j, g) that
+// hold it (two cross-lane steps per tile for max and sum).  A workgroup of 4
+// waves takes 64 queries (16 per wave) and walks 64-key tiles of K and V through
+// double-buffered LDS (the next tile's global loads are in flight during the
+// current tile's MFMAs), stopping at the last key any of its queries may see.
+// Numerics: scores, max, sum and accumulation in fp32 (exponentials in base 2
+// of the log2(e)-scaled scores), probabilities rounded to fp16 for the PV
+// product; rows with no visible key, and padded queries, are exactly zero.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
+  constexpr int BQ = 64, BT = 64, KP = D + 8, VP = BT + 8;
+  constexpr int SEGS = D / 8;                 // 16-byte pieces per key row
+  constexpr int PIECES = BT * SEGS / 256;     // per thread per tile (2 or 4)
+  __shared__ __attribute__((aligned(16))) f16 ks[2][BT][KP];
+  __shared__ __attribute__((aligned(16))) f16 vt[2][D][VP];
+  const AttnArgs& a = p.a;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y, b = blockIdx.z, q0 = blockIdx.x * BQ;
+
+  const int q_valid = max(0, min(a.q_len, a.q_lengths[b]));
+  const int64_t off = a.offsets ? int64_t(a.offsets[b]) : 0;
+  const int kvv = int(a.kv_from_offsets ? off + q_valid : max(0, min(a.kv_len, a.kv_lengths[b])));
+  const int my_q = q0 + 16 * wave + j;
+  const int last_q = min(q0 + BQ, q_valid) - 1;
+  const int key_end = last_q < q0 ? 0 : int(min<int64_t>(kvv, a.causal ? off + last_q + 1 : kvv));
+  const int ntiles = (key_end + BT - 1) / BT;
+  const int64_t slot = a.kv_slot ? int64_t(a.kv_slot[b]) : int64_t(b);
+  const uint16_t* kbase = a.k + slot * a.kv_sb + int64_t(h) * a.kv_sh;
+  const uint16_t* vbase = a.v + slot * a.kv_sb + int64_t(h) * a.kv_sh;
+  // Query my_q sees keys [0, my_end); every valid query of this wave sees at
+  // least [0, my_end_min) (its first query's range), so tiles below that need no mask.
+  const int my_end = my_q < q_valid ? int(min<int64_t>(kvv, a.causal ? off + my_q + 1 : kvv)) : 0;
+  const int wq0 = q0 + 16 * wave;
+  const int my_end_min = (wq0 + 15 < q_valid) ? int(min<int64_t>(kvv, a.causal ? off + wq0 + 1 : kvv)) : 0;
+
+  half8_t qf[D / 32];
+  {
+    const uint16_t* qp = a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(min(my_q, max(q_valid, 1) - 1)) * a.q_sq;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) {
+      qf[s] = *reinterpret_cast<const half8_t*>(qp + 32 * s + 8 * g);
+      if (my_q >= q_valid) qf[s] = half8_t{};
+    }
+  }
+
+  // Cooperative tile staging: piece r of thread t is key (t + 256 r) / SEGS,
+  // 8 dims at ((t + 256 r) % SEGS) * 8; keys past key_end re-read key_end - 1.
+  half8_t kr[PIECES], vr[PIECES];
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int r = 0; r < PIECES; ++r) {
+      const int piece = threadIdx.x + 256 * r, key = piece / SEGS, seg = piece % SEGS;
+      const int64_t kk = min(t * BT + key, key_end - 1);
+      kr[r] = *reinterpret_cast<const half8_t*>(kbase + kk * D + 8 * seg);
+      vr[r] = *reinterpret_cast<const half8_t*>(vbase + kk * D + 8 * seg);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < PIECES; ++r) {
+      const int piece = threadIdx.x + 256 * r, key = piece / SEGS, seg = piece % SEGS;
+      *reinterpret_cast<half8_t*>(&ks[buf][key][8 * seg]) = kr[r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[buf][8 * seg + e][key] = vr[r][e];
+    }
+  };
+
+  float m = kNegInf, l = 0.f;
+  float4_t acc[D / 16];
+#pragma unroll
+  for (int d = 0; d < D / 16; ++d) acc[d] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+  }
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load_tile(t + 1);
+    // This wave's queries see nothing of this tile: skip the math, keep the barriers.
+    const int wave_end = int(min<int64_t>(kvv, a.causal ? off + min(q0 + 16 * wave + 15, q_valid - 1) + 1 : kvv));
+    if (q0 + 16 * wave < q_valid && t * BT < wave_end) {
+      float4_t sc[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sc[kb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < D / 32; ++s) {
+          const half8_t kf = *reinterpret_cast<const half8_t*>(&ks[buf][16 * kb + j][32 * s + 8 * g]);
+          sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sc[kb], 0, 0, 0);
+        }
+      }
+      // Scores in base 2: x = s * D^-1/2 * log2(e), p = 2^(x - ref).  Keys past a
+      // query's end are masked only on tiles that reach some query's end (a
+      // wave-uniform test).  The reference ref is raised only when a score
+      // exceeds it by more than 8 (p <= 256 stays exact enough in fp16 and the
+      // sums are fp32), so acc and l are rescaled on few tiles, not every tile.
+      const float l2s = p.scale * 1.4426950408889634f;
+      float tmax = kNegInf;
+      if (t * BT + BT <= my_end_min) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            sc[kb][v] *= l2s;
+            tmax = fmaxf(tmax, sc[kb][v]);
+          }
+      } else {
+        const int lim = my_end - t * BT - 4 * g;  // key 16 kb + v of this lane is visible iff < lim
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            sc[kb][v] = 16 * kb + v < lim ? sc[kb][v] * l2s : kNegInf;
+            tmax = fmaxf(tmax, sc[kb][v]);
+          }
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const bool raise = tmax > m + 8.f;
+      if (__ballot(raise)) {
+        const float nref = raise ? tmax : m;
+        const float alpha = l == 0.f ? 0.f : __builtin_amdgcn_exp2f(m - nref);
+        l *= alpha;
+#pragma unroll
+        for (int d = 0; d < D / 16; ++d) acc[d] *= alpha;
+        m = nref;
+      }
+      const float base = m == kNegInf ? 0.f : m;  // -inf only while every key so far is masked
+      half4_t pt[4];
+      float psum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float pr = __builtin_amdgcn_exp2f(sc[kb][v] - base);
+          pt[kb][v] = f16(pr);
+          psum += pr;
+        }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      l += psum;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int d = 0; d < D / 16; ++d) {
+          const half4_t vf = *reinterpret_cast<const half4_t*>(&vt[buf][16 * d + j][16 * kb + 4 * g]);
+          acc[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pt[kb], acc[d], 0, 0, 0);
+        }
+    }
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (my_q >= a.q_len) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(my_q) * a.o_sq;
+#pragma unroll
+  for (int d = 0; d < D / 16; ++d) {
+    half4_t o;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) o[v] = f16(l > 0.f ? acc[d][v] * inv : 0.f);
+    *reinterpret_cast<half4_t*>(op + 16 * d + 4 * g) = o;
+  }
+}
+
 template <int D, bool VEC>
 hipError_t launch(const AttnParams& p, hipStream_t stream) {
   const AttnArgs& a = p.a;
@@ -365,8 +542,13 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
   } else {
     if (a.qkv_partials) return hipErrorInvalidValue;
     dim3 grid = blocks_per;
-    grid.x = unsigned((a.q_len + 3) / 4);
-    hipLaunchKernelGGL((attention_kernel<D, 4, 1, VEC>), grid, dim3(256), 0, stream, p);
+    if constexpr (VEC) {
+      grid.x = unsigned((a.q_len + 63) / 64);
+      hipLaunchKernelGGL((prefill_mfma_kernel<D>), grid, dim3(256), 0, stream, p);
+    } else {
+      grid.x = unsigned((a.q_len + 3) / 4);
+      hipLaunchKernelGGL((attention_kernel<D, 4, 1, VEC>), grid, dim3(256), 0, stream, p);
+    }
   }
   return hipGetLastError();
 }
