@@ -213,6 +213,23 @@ def test_packed_gemv_against_oracle(ops, m, k, n):
     close(h(hbits(res)), expect)
 
 
+@pytest.mark.parametrize("m,k,n", [(32, 1600, 8192), (24, 768, 50257), (32, 3072, 2048)])
+def test_packed_gemv_column_block_groups(ops, m, k, n):
+    """M in (16, 32] over a wide matrix: four column blocks share each A fragment,
+    including a split longer than one round of loads (K = 1600 -> 25 chunks)."""
+    t = torch()
+    rng = np.random.default_rng(m + k + n)
+    a = f16(rng.standard_normal((m, k)))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("packed gemv column groups", m, k, n)
+    packed = _pack_gpu(ops.lib, dev(q), k, n)
+    y = t.empty((m, n), dtype=t.float16, device="cuda")
+    _packed(ops.lib, dev(a, t.float16), packed, dev(s), dev(bias, t.float16), y, None, m, n, k, 1)
+    close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, bias_bits=bias, gelu=True)))
+
+
 @pytest.mark.parametrize("m", [33, 64, 130, 512])
 @pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (128, 100), (64, 2000)])
 def test_packed_prefill_gemm_against_oracle(ops, m, k, n):

@@ -349,73 +349,91 @@ __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scal
   return out;
 }
 
-// One workgroup of W waves owns column block cb and the K chunks of one split;
-// wave w takes chunks w, w + W, ... and issues the loads of up to CPW of them
-// (weights and A) before the first MFMA, so a split is one memory round trip.
-// The W partial 16-column sums are reduced through LDS in wave order, then the
-// epilogue runs (or fp32 partials are stored for a split/deferred launch).
-// Loads use clamped chunk and row indices, never predicates (rows >= M are
-// computed from row M-1 and never stored).
-template <int MT, int W, int CPW>
+// One workgroup of W waves owns CBG consecutive column blocks and the K chunks
+// of one split; wave w takes chunks w, w + W, ... and issues the loads of up to
+// CPW of them (CBG weight records and the A fragments of each chunk) before the
+// first MFMA, so a split is one memory round trip, and each A fragment feeds
+// CBG column blocks (at M = 32 the A rows would otherwise be re-read for every
+// 16 columns).  The W partial sums are reduced through LDS in wave order, then
+// the epilogue runs (or fp32 partials are stored for a split/deferred launch).
+// Loads use clamped chunk, row and column-block indices, never predicates
+// (rows >= M, blocks >= nb are computed from valid data and never stored).
+template <int MT, int W, int CPW, int CBG>
 __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
-  __shared__ float red[W][MT * 256];
+  __shared__ float red[W][CBG][MT * 256];
   // The wave index is uniform: chunk bounds below are scalar, so every load of a
   // round is issued before the first wait.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int nbk = gridDim.x, bid = blockIdx.x;
   const int logical = (nbk % 8 == 0) ? (bid % 8) * (nbk / 8) + bid / 8 : bid;
-  const int cb = logical % p.nb, split = logical / p.nb;
+  const int groups = (p.nb + CBG - 1) / CBG;
+  const int grp = logical % groups, split = logical / groups;
+  const int cb0 = grp * CBG;
   const int c_begin = split * p.chunks_per_split;
   const int c_end = min(p.kc, c_begin + p.chunks_per_split);
-  const int col = cb * 16 + j;
-  const float* scp = p.scales + min(col, p.n - 1);
-  const float colmask = col < p.n ? 1.f : 0.f;
-  // Every output this thread finishes is in column cb*16 + (threadIdx.x & 15):
-  // its bias is fetched now, not after the reduction.
   const bool epi_now = p.splits == 1 && !p.defer;
-  const float bias_v = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias
-                           ? h2f(p.epi.bias[min(cb * 16 + int(threadIdx.x & 15), p.n - 1)])
-                           : 0.f;
+  const bool has_bias = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias;
 
-  const u32x4_t* wb = p.w + int64_t(cb) * p.kc * 64 + lane;
+  const u32x4_t* wb[CBG];
+  const float* scp[CBG];
+  float colmask[CBG], bias_v[CBG];
+#pragma unroll
+  for (int r = 0; r < CBG; ++r) {
+    const int cb = min(cb0 + r, p.nb - 1), col = cb * 16 + j;
+    wb[r] = p.w + int64_t(cb) * p.kc * 64 + lane;
+    scp[r] = p.scales + min(col, p.n - 1);
+    colmask[r] = (cb0 + r < p.nb && col < p.n) ? 1.f : 0.f;
+    // Every output this thread finishes in block r is in column (cb0 + r) * 16 +
+    // (threadIdx.x & 15): its bias is fetched now, not after the reduction.
+    bias_v[r] = has_bias ? h2f(p.epi.bias[min((cb0 + r) * 16 + int(threadIdx.x & 15), p.n - 1)]) : 0.f;
+  }
   const uint16_t* arow[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) arow[t] = p.a + int64_t(min(16 * t + j, p.m - 1)) * p.lda + 8 * g;
 
-  float4_t acc[MT];
+  float4_t acc[MT][CBG];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < CBG; ++r) acc[t][r] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int c0 = c_begin + wave; c0 < c_end; c0 += W * CPW) {
-    u32x4_t wf[CPW];
+    u32x4_t wf[CPW][CBG];
     half8_t af[CPW][2][MT];
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
       const int c = min(c0 + i * W, c_end - 1);
-      wf[i] = __builtin_nontemporal_load(wb + int64_t(c) * 64);
+#pragma unroll
+      for (int r = 0; r < CBG; ++r) wf[i][r] = __builtin_nontemporal_load(wb[r] + int64_t(c) * 64);
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int t = 0; t < MT; ++t)
           af[i][s][t] = *reinterpret_cast<const half8_t*>(arow[t] + c * 64 + 32 * s);
     }
-    // The scale is loaded after the round's weights and A (and waited for with
-    // them); the scheduling barrier keeps every load of the round ahead of the
-    // first wait.
-    const float sc = *scp * colmask;
+    // The scales are loaded after the round's weights and A (and waited for
+    // with them); the scheduling barrier keeps every load of the round ahead of
+    // the first wait.
+    float sc[CBG];
+#pragma unroll
+    for (int r = 0; r < CBG; ++r) sc[r] = *scp[r] * colmask[r];
     __builtin_amdgcn_sched_barrier(0);
     // A chunk past the split's end re-read the last chunk; its scale is 0 so
     // its B operands are +-0 and the MFMAs leave the sums unchanged.
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
-      const float si = c0 + i * W < c_end ? sc : 0.f;
-      const half8_t b0 = dequant8(wf[i][0], wf[i][1], si);
-      const half8_t b1 = dequant8(wf[i][2], wf[i][3], si);
+      const bool live = c0 + i * W < c_end;
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][0][t], b0, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][1][t], b1, acc[t], 0, 0, 0);
+      for (int r = 0; r < CBG; ++r) {
+        const float si = live ? sc[r] : 0.f;
+        const half8_t b0 = dequant8(wf[i][r][0], wf[i][r][1], si);
+        const half8_t b1 = dequant8(wf[i][r][2], wf[i][r][3], si);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][0][t], b0, acc[t][r], 0, 0, 0);
+          acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][1][t], b1, acc[t][r], 0, 0, 0);
+        }
       }
     }
   }
@@ -424,16 +442,22 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[wave][(16 * t + 4 * g + v) * 16 + j] = acc[t][v];
+    for (int r = 0; r < CBG; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][r][(16 * t + 4 * g + v) * 16 + j] = acc[t][r][v];
   __syncthreads();
-  const int rows = min(p.m, MT * 16);
-  for (int o = threadIdx.x; o < rows * 16; o += W * 64) {
-    const int row = o >> 4, n = cb * 16 + (o & 15);
-    if (n >= p.n) continue;
+  const int rows = min(p.m, MT * 16), per_block = rows * 16;
+  for (int o = threadIdx.x; o < CBG * per_block; o += W * 64) {
+    const int r = o / per_block, rem = o - r * per_block;
+    const int row = rem >> 4, n = (cb0 + r) * 16 + (rem & 15);
+    if (cb0 + r >= p.nb || n >= p.n) continue;
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) s += red[w][o];
-    if (epi_now) apply_epilogue(p.epi, row, n, s, bias_v);
+    for (int w = 0; w < W; ++w) s += red[w][r][rem];
+    float bias = bias_v[0];
+#pragma unroll
+    for (int q = 1; q < CBG; ++q) bias = r == q ? bias_v[q] : bias;
+    if (epi_now) apply_epilogue(p.epi, row, n, s, bias);
     else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
   }
 }
@@ -833,21 +857,23 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   return hipGetLastError();
 }
 
-// Waves per workgroup W (4, 8 or 16) so that W * 4 chunks cover one split's K
-// range in one round where possible.  Without a caller that finishes partials,
-// one split: the epilogue runs in the same kernel.  A deferred launch may split
-// K further when there are few column blocks (more CUs with loads in flight),
-// keeping at least 4 chunks per split and the partials within the scratch.
-template <int MT>
-hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
-  PackedParams p{};
-  p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
-  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
-  p.nb = (g.n + 15) / 16;
-  p.kc = g.k / 64;
+// Launch shape of the packed GEMV.  M <= 16: one column block per workgroup
+// (A is one row, its re-reads are free).  M <= 32: four column blocks share
+// each A fragment when the matrix is wide enough to keep >= 128 workgroups
+// without splitting K (the LM head); for the narrower decode GEMVs that
+// measured no faster, and splitting K further to compensate only moved time
+// into the consumers of the partials.  Waves W in {4, 8, 16} so that W * CPW
+// chunks cover one split's K range in one round where possible.  A deferred
+// launch splits K to reach ~192 workgroups, keeping >= 4 chunks per split and
+// the partials within the scratch; otherwise one split and the epilogue runs
+// in the kernel.
+template <int MT, int CPW, int CBG>
+hipError_t launch_packed_cfg(PackedParams& p, const GemmArgs& g, const Scratch* s, hipStream_t stream,
+                             int* deferred) {
+  const int groups = (p.nb + CBG - 1) / CBG;
   int splits = 1;
   if (deferred && s && s->partials) {
-    splits = std::max(1, std::min((192 + p.nb - 1) / p.nb, p.kc / 4));
+    splits = std::max(1, std::min((192 + groups - 1) / groups, p.kc / 4));
     while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
   }
   p.chunks_per_split = (p.kc + splits - 1) / splits;
@@ -856,13 +882,31 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   p.defer = deferred != nullptr;
   p.partials = s ? s->partials : nullptr;
   if (p.defer && (!p.partials || size_t(splits) * g.m * g.n > s->partial_floats)) return hipErrorInvalidValue;
-  const dim3 grid(unsigned(p.nb) * unsigned(splits));
+  const dim3 grid(unsigned(groups) * unsigned(splits));
   const int cps = p.chunks_per_split;
-  if (cps <= 16) hipLaunchKernelGGL((gemv_packed_kernel<MT, 4, 4>), grid, dim3(256), 0, stream, p);
-  else if (cps <= 32) hipLaunchKernelGGL((gemv_packed_kernel<MT, 8, 4>), grid, dim3(512), 0, stream, p);
-  else hipLaunchKernelGGL((gemv_packed_kernel<MT, 16, 4>), grid, dim3(1024), 0, stream, p);
+  // Four-block groups hold 4x the weight registers: at most 8 waves (16 would
+  // exceed 128 VGPRs), with further rounds for longer splits.
+  if (cps <= 4 * CPW)
+    hipLaunchKernelGGL((gemv_packed_kernel<MT, 4, CPW, CBG>), grid, dim3(256), 0, stream, p);
+  else if (cps <= 8 * CPW || CBG > 1)
+    hipLaunchKernelGGL((gemv_packed_kernel<MT, 8, CPW, CBG>), grid, dim3(512), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemv_packed_kernel<MT, 16, CPW, 1>), grid, dim3(1024), 0, stream, p);
   if (deferred) *deferred = splits;
   return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  PackedParams p{};
+  p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
+  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.nb = (g.n + 15) / 16;
+  p.kc = g.k / 64;
+  if constexpr (MT == 2) {
+    if (!deferred && (p.nb + 3) / 4 >= 128) return launch_packed_cfg<2, 2, 4>(p, g, s, stream, deferred);
+  }
+  return launch_packed_cfg<MT, 4, 1>(p, g, s, stream, deferred);
 }
 
 // 64x64 tiles, S = 4 stages of 12 KiB (48 KiB of LDS: three workgroups per CU,
