@@ -230,8 +230,9 @@ def test_packed_gemv_column_block_groups(ops, m, k, n):
     close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, bias_bits=bias, gelu=True)))
 
 
-@pytest.mark.parametrize("m", [33, 64, 130, 512])
-@pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (128, 100), (64, 2000)])
+@pytest.mark.parametrize("m,k,n", [(33, 768, 3072), (64, 3072, 768), (130, 128, 100), (512, 64, 2000),
+                                   (512, 768, 3072), (512, 3072, 768), (2048, 768, 2304), (4100, 1600, 6400),
+                                   (2050, 64, 8200)])
 def test_packed_prefill_gemm_against_oracle(ops, m, k, n):
     """Prefill (M > 32) GEMM over panel-packed weights: ragged row and column tiles,
     bias and bias+GELU epilogues against the oracle; fp32-accumulate tolerance."""

@@ -565,17 +565,18 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
   // register is used in the loop (the compiler would otherwise wait for every
   // prologue load up front).  The bias is loaded into registers now and used
   // only after the loop; a null bias reads A's first element, scaled by 0.
-  static_assert(BN == 64, "one 64-lane scale load per tile");
+  static_assert(BN % 64 == 0 && BN / 64 <= 4, "one 64-lane scale load per 64 columns");
   const float* scale_lds = reinterpret_cast<const float*>(lds + S * STAGE);
-  if (wave == 0)
-    __builtin_amdgcn_global_load_lds((global_ptr)(p.scales + min(cb0 * 16 + lane, p.n - 1)),
-                                     (lds_ptr)(lds + S * STAGE), 4, 0, 0);
+  if (wave < BN / 64)
+    __builtin_amdgcn_global_load_lds((global_ptr)(p.scales + min(cb0 * 16 + 64 * wave + lane, p.n - 1)),
+                                     (lds_ptr)(lds + S * STAGE + 256 * wave), 4, 0, 0);
+  // The epilogue below gives thread t the outputs of tile column t % BN only:
+  // its bias is loaded now (used only after the loop).
+  static_assert(256 % BN == 0, "a thread's epilogue outputs share one column");
   const bool has_bias = p.epi.kind != EPI_RAW_F32 && p.epi.bias;
   const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
-  const float bmul = has_bias ? 1.f : 0.f;
-  float bias[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) bias[r] = h2f(bsrc[has_bias ? min((cb0 + wn * R + r) * 16 + j, p.n - 1) : 0]) * bmul;
+  const int my_col = cb0 * 16 + int(threadIdx.x % BN);
+  const float bias = h2f(bsrc[has_bias ? min(my_col, p.n - 1) : 0]) * (has_bias ? 1.f : 0.f);
   float4_t acc[MT][R];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
@@ -610,22 +611,32 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
   }
   wait_vmcnt<0>();
 
-  // MFMA output: lane holds rows 4g + v of column j of each 16x16 block.
-  const bool epi_now = p.splits == 1 && !p.defer;
+  // Epilogue through LDS (the stages are free once every wave is past the last
+  // chunk): the accumulators land in a [BM][BN+1] fp32 tile, then thread t
+  // finishes column t % BN of rows t / BN, t / BN + 256 / BN, ... with one
+  // epilogue call site and coalesced stores.
+  static_assert(BM * (BN + 1) * 4 <= S * STAGE, "fp32 tile fits the stages");
+  __syncthreads();
+  float* ctile = reinterpret_cast<float*>(lds);
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int col = (cb0 + wn * R + r) * 16 + j;
-      if (col >= p.n) continue;
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = m0 + (wm * MT + t) * 16 + 4 * g + v;
-        if (row >= p.m) continue;
-        if (epi_now) apply_epilogue(p.epi, row, col, acc[t][r][v], bias[r]);
-        else p.partials[(int64_t(split) * p.m + row) * p.n + col] = acc[t][r][v];
-      }
+      for (int v = 0; v < 4; ++v)
+        ctile[((wm * MT + t) * 16 + 4 * g + v) * (BN + 1) + (wn * R + r) * 16 + j] = acc[t][r][v];
+  __syncthreads();
+  const bool epi_now = p.splits == 1 && !p.defer;
+  const int cl = int(threadIdx.x % BN);
+  if (my_col < p.n) {
+    for (int rl = int(threadIdx.x / BN); rl < BM; rl += 256 / BN) {
+      const int row = m0 + rl;
+      if (row >= p.m) break;
+      const float val = ctile[rl * (BN + 1) + cl];
+      if (epi_now) apply_epilogue(p.epi, row, my_col, val, bias);
+      else p.partials[(int64_t(split) * p.m + row) * p.n + my_col] = val;
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -956,6 +967,9 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
   return hipGetLastError();
 }
 
+// (Tiles of 128 x 64 and 128 x 128 halve the LDS bytes and dequant work per
+// MFMA, but hold one or two 4-wave workgroups per CU and measured 1.3-2x slower
+// from M = 512 to 8192; the 64 x 64 tile keeps three per CU.)
 hipError_t launch_panel(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   return launch_panel_cfg<1, 4, 4, 1, 4>(g, s, stream, deferred);
 }
