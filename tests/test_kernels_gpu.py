@@ -267,6 +267,65 @@ def test_packed_gemv_rejects_unsupported_shapes(ops):
     assert fn(a.data_ptr(), packed.data_ptr(), s.data_ptr(), None, y.data_ptr(), None, 0, 16, 64, 0, 0, 0) == 1
 
 
+def _ln_packed(lib, a, g, b, eps, packed, s, bias, y, res, m, n, k, epi):
+    t = torch()
+    fn = lib.ti_amd_gemm_w8p_ln_fused
+    fn.argtypes = [C.c_void_p] * 3 + [C.c_float] + [C.c_void_p] * 5 + [C.c_int] * 4 + [C.c_size_t, C.c_int]
+    ptr = lambda x: None if x is None else x.data_ptr()
+    return fn(ptr(a), ptr(g), ptr(b), eps, ptr(packed), ptr(s), ptr(bias), ptr(y), ptr(res), m, n, k, epi,
+              t.cuda.current_stream().cuda_stream, 0)
+
+
+@pytest.mark.parametrize("m", [1, 7, 32])
+@pytest.mark.parametrize("k,n", [(768, 2304), (768, 3072), (768, 50257), (1600, 6400), (64, 100), (2048, 64)])
+def test_layernorm_prologue_gemv_against_oracle(ops, m, k, n):
+    """Decode GEMV with the LayerNorm of its A rows computed in the prologue:
+    epilogue(LN(A) @ W + bias) against the oracle's layernorm_f16 followed by its
+    linear.  Rows carry offsets up to 50 (the two-pass variance matters) and
+    the head shape at M = 32 takes the four-column-block variant."""
+    t = torch()
+    rng = np.random.default_rng(3 * m + k + n)
+    a = f16(rng.standard_normal((m, k)) * rng.uniform(0.5, 4, (m, 1)) + rng.uniform(-50, 50, (m, 1)))
+    gam = f16(1 + 0.2 * rng.standard_normal(k))
+    bet = f16(0.1 * rng.standard_normal(k))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("layernorm-prologue gemv", m, k, n)
+    packed = _pack_gpu(ops.lib, dev(q), k, n)
+    ad, gd, bd = dev(a, t.float16), dev(gam, t.float16), dev(bet, t.float16)
+    sd, biasd = dev(s), dev(bias, t.float16)
+    normed = oracle.layernorm_f16(a, gam, bet, 1e-5)
+    y = t.empty((m, n), dtype=t.float16, device="cuda")
+    assert _ln_packed(ops.lib, ad, gd, bd, 1e-5, packed, sd, biasd, y, None, m, n, k, 0) == 0, \
+        ops.lib.ti_v2_last_error()
+    ref = oracle.linear(normed, q=q, scales=s, bias_bits=bias)
+    close(h(hbits(y)), h(ref))
+    assert _ln_packed(ops.lib, ad, gd, bd, 1e-5, packed, sd, biasd, y, None, m, n, k, 1) == 0
+    close(h(hbits(y)), h(oracle.linear(normed, q=q, scales=s, bias_bits=bias, gelu=True)))
+    res = dev(f16(rng.standard_normal((m, n))), t.float16)
+    expect = (h(hbits(res)) + h(ref)).astype(np.float16).astype(np.float64)
+    assert _ln_packed(ops.lib, ad, gd, bd, 1e-5, packed, sd, biasd, res, res, m, n, k, 2) == 0
+    close(h(hbits(res)), expect)
+
+
+def test_layernorm_prologue_gemv_rejects_unsupported_shapes(ops):
+    t = torch()
+    a = t.zeros((33, 2112), dtype=t.float16, device="cuda")
+    g = t.ones(2112, dtype=t.float16, device="cuda")
+    q = t.zeros((2112, 16), dtype=t.int8, device="cuda")
+    packed = _pack_gpu(ops.lib, q, 2112, 16)
+    s = t.ones(16, dtype=t.float32, device="cuda")
+    y = t.empty((33, 16), dtype=t.float16, device="cuda")
+    say("layernorm-prologue gemv invalid")
+    args = lambda m, k, eps=1e-5: (ops.lib, a, g, g, eps, packed, s, None, y, None, m, 16, k, 0)
+    assert _ln_packed(*args(33, 64)) == 1        # M > 32
+    assert _ln_packed(*args(1, 2112)) == 1       # K / 64 > 32
+    assert _ln_packed(*args(1, 100)) == 1        # K % 64 != 0
+    assert _ln_packed(*args(1, 64, eps=0.0)) == 1
+    assert _ln_packed(*args(0, 64)) == 1
+
+
 def test_legacy_fp32_gemm(ops):
     t = torch()
     rng = np.random.default_rng(4)

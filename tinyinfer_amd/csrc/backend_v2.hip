@@ -309,6 +309,42 @@ extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, cons
   return hip_status(tia::gemm(g, scratch, st));
 }
 
+extern "C" int ti_amd_gemm_w8p_ln_fused(const uint16_t* a, const uint16_t* gamma, const uint16_t* beta, float eps,
+                                        const void* packed, const float* scales, const uint16_t* bias, uint16_t* y,
+                                        const uint16_t* residual, int m, int n, int k, int epilogue,
+                                        uintptr_t stream, int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (!tia::gemm_ln_supported(m, k, n) || !aligned(a, 16) || !aligned(gamma, 16) || !aligned(beta, 16) ||
+      !aligned(packed, 16) || !aligned(scales, 4) || !aligned(y, 2) || (bias && !aligned(bias, 2)) ||
+      !std::isfinite(eps) || eps <= 0.f || !shape_fits({m, n}, 2) || !shape_fits({k, n}, 1))
+    return fail(TI_V2_INVALID_ARGUMENT,
+                "LayerNorm-prologue GEMM needs 1 <= M <= 32, K % 64 == 0, K <= 2048, eps > 0 and 16-byte "
+                "aligned A, gamma, beta and packed weights");
+  if (epilogue < 0 || epilogue > 2 || (epilogue == 2 && !aligned(residual, 2)))
+    return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
+  tia::GemmArgs g;
+  g.a = a;
+  g.lda = k;
+  g.w = packed;
+  g.w_packed = packed;
+  g.w_int8 = true;
+  g.scales = scales;
+  g.m = m;
+  g.n = n;
+  g.k = k;
+  g.ln_gamma = gamma;
+  g.ln_beta = beta;
+  g.ln_eps = eps;
+  g.epi.kind = epilogue == 1 ? tia::EPI_GELU : (epilogue == 2 ? tia::EPI_RESIDUAL : tia::EPI_F16);
+  g.epi.bias = bias;
+  g.epi.y = y;
+  g.epi.ldy = n;
+  g.epi.residual = residual;
+  g.epi.ldr = n;
+  return hip_status(tia::gemm(g, nullptr, reinterpret_cast<hipStream_t>(stream)));
+}
+
 extern "C" int ti_amd_layernorm_f32(const float* x, const float* g, const float* b, float* y, int rows, int cols,
                                     float eps, uintptr_t stream, int device) {
   int status = begin(device);

@@ -337,7 +337,18 @@ struct PackedParams {
   bool defer;
   Epilogue epi;
   float* partials;      // [splits][M][N]
+  const uint16_t* ln_gamma;  // A = LayerNorm(a rows; gamma, beta, eps) when set
+  const uint16_t* ln_beta;
+  float ln_eps;
 };
+
+// Workgroup barrier that orders LDS accesses only: outstanding global loads
+// stay in flight across it (__syncthreads would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // fp16_rn(float(q) * scale) of the 8 bytes in (lo, hi): one MFMA B operand.
 __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scale) {
@@ -358,9 +369,13 @@ __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scal
 // the epilogue runs (or fp32 partials are stored for a split/deferred launch).
 // Loads use clamped chunk, row and column-block indices, never predicates
 // (rows >= M, blocks >= nb are computed from valid data and never stored).
-template <int MT, int W, int CPW, int CBG>
+// LNA: A is LayerNorm(a) over its K = hidden columns, computed from the loaded
+// fragments before the MFMAs; the launch then covers K in one round of one
+// split (W * CPW >= kc).
+template <int MT, int W, int CPW, int CBG, bool LNA = false>
 __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   __shared__ float red[W][CBG][MT * 256];
+  __shared__ float stat[LNA ? W : 1][MT * 16];  // per-wave LayerNorm partial sums
   // The wave index is uniform: chunk bounds below are scalar, so every load of a
   // round is issued before the first wait.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -377,7 +392,12 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 
   const u32x4_t* wb[CBG];
   const float* scp[CBG];
-  float colmask[CBG], bias_v[CBG];
+  float colmask[CBG];
+  uint16_t bias_raw[CBG];
+  // Unconditional load (of A's first element when there is no bias) whose value
+  // is converted only in the epilogue: a conditional load here would be waited
+  // for at once, before the weight loads are issued.
+  const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
 #pragma unroll
   for (int r = 0; r < CBG; ++r) {
     const int cb = min(cb0 + r, p.nb - 1), col = cb * 16 + j;
@@ -386,7 +406,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     colmask[r] = (cb0 + r < p.nb && col < p.n) ? 1.f : 0.f;
     // Every output this thread finishes in block r is in column (cb0 + r) * 16 +
     // (threadIdx.x & 15): its bias is fetched now, not after the reduction.
-    bias_v[r] = has_bias ? h2f(p.epi.bias[min((cb0 + r) * 16 + int(threadIdx.x & 15), p.n - 1)]) : 0.f;
+    bias_raw[r] = bsrc[has_bias ? min((cb0 + r) * 16 + int(threadIdx.x & 15), p.n - 1) : 0];
   }
   const uint16_t* arow[MT];
 #pragma unroll
@@ -398,27 +418,107 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
     for (int r = 0; r < CBG; ++r) acc[t][r] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int c0 = c_begin + wave; c0 < c_end; c0 += W * CPW) {
+  // One round: the loads of chunks c0, c0 + W, ... (CPW of them), then the MFMAs.
+  auto round = [&](int c0) {
     u32x4_t wf[CPW][CBG];
     half8_t af[CPW][2][MT];
-#pragma unroll
-    for (int i = 0; i < CPW; ++i) {
+    half8_t gam[CPW][2], bet[CPW][2];
+    auto load_w = [&](int i) {
       const int c = min(c0 + i * W, c_end - 1);
 #pragma unroll
       for (int r = 0; r < CBG; ++r) wf[i][r] = __builtin_nontemporal_load(wb[r] + int64_t(c) * 64);
+    };
+    auto load_a = [&](int i) {
+      const int c = min(c0 + i * W, c_end - 1);
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < 2; ++s) {
 #pragma unroll
         for (int t = 0; t < MT; ++t)
           af[i][s][t] = *reinterpret_cast<const half8_t*>(arow[t] + c * 64 + 32 * s);
+        if constexpr (LNA) {
+          gam[i][s] = *reinterpret_cast<const half8_t*>(p.ln_gamma + c * 64 + 32 * s + 8 * g);
+          bet[i][s] = *reinterpret_cast<const half8_t*>(p.ln_beta + c * 64 + 32 * s + 8 * g);
+        }
+      }
+    };
+    if constexpr (LNA) {
+      // A, gamma and beta first: the LayerNorm below needs only them (loads
+      // complete in order), so it runs while the weight records are in flight.
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) load_a(i);
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) load_w(i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) {
+        load_w(i);
+        load_a(i);
+      }
     }
     // The scales are loaded after the round's weights and A (and waited for
     // with them); the scheduling barrier keeps every load of the round ahead of
     // the first wait.
     float sc[CBG];
 #pragma unroll
-    for (int r = 0; r < CBG; ++r) sc[r] = *scp[r] * colmask[r];
+    for (int r = 0; r < CBG; ++r) sc[r] = *scp[r];
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (LNA) {
+      // LayerNorm of the A rows, as the row kernel computes it (two-pass fp32
+      // mean and variance over the K = hidden columns, rsqrt(var + eps),
+      // fp16_rn((x - mean) * inv * gamma + beta)); every chunk of K is in this
+      // workgroup's single round, spread over the waves and the 4 k-groups of
+      // a row's lanes.
+      float mean[MT], inv[MT];
+#pragma unroll
+      for (int pass = 0; pass < 2; ++pass) {
+        float part[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          part[t] = 0.f;
+#pragma unroll
+          for (int i = 0; i < CPW; ++i) {
+            float pc = 0.f;
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float x = float(af[i][s][t][e]);
+                pc += pass == 0 ? x : (x - mean[t]) * (x - mean[t]);
+              }
+            // A chunk past the end re-read the last one: it is not counted.
+            part[t] += c0 + i * W < c_end ? pc : 0.f;
+          }
+          part[t] += __shfl_xor(part[t], 16, 64);
+          part[t] += __shfl_xor(part[t], 32, 64);
+          // The 4 lanes of row j hold the same sum (branch-free store: the
+          // LayerNorm stays one basic block, so the scheduling barriers hold).
+          stat[wave][16 * t + j] = part[t];
+        }
+        lds_barrier();
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          float tot = 0.f;
+#pragma unroll
+          for (int w = 0; w < W; ++w) tot += stat[w][16 * t + j];
+          if (pass == 0) mean[t] = tot / float(p.k);
+          else inv[t] = rsqrtf(tot / float(p.k) + p.ln_eps);
+        }
+        lds_barrier();
+      }
+#pragma unroll
+      for (int i = 0; i < CPW; ++i)
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              af[i][s][t][e] = f16((float(af[i][s][t][e]) - mean[t]) * inv[t] * float(gam[i][s][e]) +
+                                   float(bet[i][s][e]));
+      // Keep the weight dequantization (which waits for the records) after the
+      // LayerNorm.
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // A chunk past the split's end re-read the last chunk; its scale is 0 so
     // its B operands are +-0 and the MFMAs leave the sums unchanged.
 #pragma unroll
@@ -426,7 +526,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
       const bool live = c0 + i * W < c_end;
 #pragma unroll
       for (int r = 0; r < CBG; ++r) {
-        const float si = live ? sc[r] : 0.f;
+        const float si = live ? sc[r] * colmask[r] : 0.f;
         const half8_t b0 = dequant8(wf[i][r][0], wf[i][r][1], si);
         const half8_t b1 = dequant8(wf[i][r][2], wf[i][r][3], si);
 #pragma unroll
@@ -436,6 +536,12 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
         }
       }
     }
+  };
+  if constexpr (LNA) {
+    // Every wave runs the single round (its barriers included), chunks or not.
+    round(c_begin + wave);
+  } else {
+    for (int c0 = c_begin + wave; c0 < c_end; c0 += W * CPW) round(c0);
   }
 
   // MFMA output: lane holds rows 4g + v of column j of each 16x16 block.
@@ -454,9 +560,10 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < W; ++w) s += red[w][r][rem];
-    float bias = bias_v[0];
+    uint16_t braw = bias_raw[0];
 #pragma unroll
-    for (int q = 1; q < CBG; ++q) bias = r == q ? bias_v[q] : bias;
+    for (int q = 1; q < CBG; ++q) braw = r == q ? bias_raw[q] : braw;
+    const float bias = has_bias ? h2f(braw) : 0.f;
     if (epi_now) apply_epilogue(p.epi, row, n, s, bias);
     else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
   }
@@ -907,6 +1014,34 @@ hipError_t launch_packed_cfg(PackedParams& p, const GemmArgs& g, const Scratch* 
   return hipGetLastError();
 }
 
+// LayerNorm prologue: one split whose K range one round covers.  A deferred
+// launch leaves its sums as partials [1][M][N].
+template <int MT, int W, int CPW, int CBG>
+hipError_t launch_packed_ln_cfg(PackedParams& p, const Scratch* s, hipStream_t stream, int* deferred) {
+  p.chunks_per_split = p.kc;
+  p.splits = 1;
+  p.defer = deferred != nullptr;
+  p.partials = s ? s->partials : nullptr;
+  if (p.defer && (!p.partials || size_t(p.m) * p.n > s->partial_floats)) return hipErrorInvalidValue;
+  const int groups = (p.nb + CBG - 1) / CBG;
+  hipLaunchKernelGGL((gemv_packed_kernel<MT, W, CPW, CBG, true>), dim3(unsigned(groups)), dim3(W * 64), 0,
+                     stream, p);
+  if (deferred) *deferred = 1;
+  return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_packed_ln(PackedParams& p, const Scratch* s, hipStream_t stream, int* deferred) {
+  if constexpr (MT == 2) {
+    if (!deferred && (p.nb + 3) / 4 >= 128 && p.kc <= 16)
+      return launch_packed_ln_cfg<2, 8, 2, 4>(p, s, stream, deferred);
+  }
+  if (p.kc <= 12) return launch_packed_ln_cfg<MT, 4, 3, 1>(p, s, stream, deferred);
+  if (p.kc <= 16) return launch_packed_ln_cfg<MT, 4, 4, 1>(p, s, stream, deferred);
+  if (p.kc <= kLnMaxChunks) return launch_packed_ln_cfg<MT, 8, 4, 1>(p, s, stream, deferred);
+  return hipErrorInvalidValue;
+}
+
 template <int MT>
 hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   PackedParams p{};
@@ -914,6 +1049,10 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.nb = (g.n + 15) / 16;
   p.kc = g.k / 64;
+  if (g.ln_gamma) {
+    p.ln_gamma = g.ln_gamma; p.ln_beta = g.ln_beta; p.ln_eps = g.ln_eps;
+    return launch_packed_ln<MT>(p, s, stream, deferred);
+  }
   if constexpr (MT == 2) {
     if (!deferred && (p.nb + 3) / 4 >= 128) return launch_packed_cfg<2, 2, 4>(p, g, s, stream, deferred);
   }
@@ -1002,6 +1141,12 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   const bool wvec = ldw % 4 == 0 && ldw >= (int64_t(g.n) + 3) / 4 * 4 &&
                     (g.w_int8 ? wp % 4 == 0 : wp % 8 == 0);
   const bool avec = (g.lda % 8 == 0) && (ap % 16 == 0);
+  if (g.ln_gamma) {
+    if (!gemm_ln_supported(g.m, g.k, g.n) || !g.w_int8 || !g.w_packed || !g.ln_beta || !avec ||
+        reinterpret_cast<uintptr_t>(g.w_packed) % 16 != 0 || reinterpret_cast<uintptr_t>(g.ln_gamma) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(g.ln_beta) % 16 != 0)
+      return hipErrorInvalidValue;
+  }
   if (g.w_int8 && g.w_packed && g.k % 64 == 0 && avec && reinterpret_cast<uintptr_t>(g.w_packed) % 16 == 0) {
     if (g.m <= 16) return launch_packed<1>(g, s, stream, deferred);
     if (g.m <= 32) return launch_packed<2>(g, s, stream, deferred);
@@ -1012,6 +1157,10 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   if (g.m <= 32) return g.w_int8 ? launch_skinny<true, 2>(g, wvec, avec, s, stream, deferred)
                                  : launch_skinny<false, 2>(g, wvec, avec, s, stream, deferred);
   return g.w_int8 ? launch_tiled<true>(g, wvec, avec, stream) : launch_tiled<false>(g, wvec, avec, stream);
+}
+
+bool gemm_ln_supported(int m, int k, int n) {
+  return m >= 1 && m <= 32 && n >= 1 && k >= 64 && k % 64 == 0 && k / 64 <= kLnMaxChunks;
 }
 
 const Scratch* library_scratch(int device, hipStream_t stream, hipError_t* err) {

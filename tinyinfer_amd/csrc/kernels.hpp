@@ -56,8 +56,17 @@ struct GemmArgs {
   // Optional panel-packed copy of the int8 W (pack_w8).  When set, M <= 32,
   // K % 64 == 0 and A allows 16-byte loads, the GEMV over the packed records runs.
   const void* w_packed = nullptr;
+  // Optional LayerNorm of the A rows (packed int8 W, M <= 32, gemm_ln_supported):
+  // the GEMM multiplies fp16_rn((a - mean) * rsqrt(var + eps) * gamma + beta),
+  // mean and var over the K columns of each row, as layernorm_f16 computes them.
+  const uint16_t* ln_gamma = nullptr;
+  const uint16_t* ln_beta = nullptr;
+  float ln_eps = 1e-5f;
   Epilogue epi;
 };
+// Largest K / 64 a LayerNorm-prologue GEMM takes (one round of 8 waves x 4 chunks).
+constexpr int kLnMaxChunks = 32;
+bool gemm_ln_supported(int m, int k, int n);
 
 // Panel-packed int8 weights: for column block cb (16 columns) and K chunk kc (64
 // rows), a 1 KiB record at (cb * ceil(K/64) + kc) * 1024 bytes holding, for lane

@@ -10,6 +10,12 @@
 //    reduces its split-K partials, adds bias and residual (in place) and applies
 //    LN2 -> c_fc GEMM with fused bias + GELU -> mlp.c_proj GEMM -> the same
 //    reduce + residual kernel applying the next layer's LN1 (ln_f after the last);
+//  * decode of up to 32 requests over packed int8 weights instead runs each
+//    LayerNorm in the prologue of the GEMV that consumes it (ln_1 in c_attn,
+//    ln_2 in c_fc, ln_f in the head) and each residual add in the epilogue of
+//    the GEMV that produces it: per layer c_attn (split-K partials) ->
+//    attention (finishes q/k/v) -> c_proj (+residual) -> c_fc (LN2, GELU) ->
+//    mlp.c_proj (+residual), five launches;
 //  * the lm_head GEMM writes fp32 logits of each request's last row (padded row
 //    pitch), a block-per-row argmax picks the lowest id on ties;
 //  * a decode step (every request appends one token) is captured once per
@@ -356,6 +362,25 @@ struct ti_llm_model {
       if (quantized) head.scales = static_cast<const float*>(tensor("lm_head.weight.scales", {V}, "float32"));
     }
     if (used.size() != a.tensors.size()) throw Invalid("unexpected tensor(s) in artifact");
+    // The LayerNorm parameters get 16-byte aligned copies (the GEMV prologue
+    // reads them 8 halves at a time; artifact offsets need not be aligned).
+    {
+      const size_t n = size_t(4 * L + 2);
+      uint16_t* ln = alloc<uint16_t>(n * size_t(H));
+      size_t i = 0;
+      auto place = [&](const uint16_t*& p) {
+        ck(hipMemcpy(ln + i * H, p, size_t(H) * sizeof(uint16_t), hipMemcpyDeviceToDevice));
+        p = ln + i++ * H;
+      };
+      place(lnf_g);
+      place(lnf_b);
+      for (int l = 0; l < L; ++l) {
+        place(ln1_g[l]);
+        place(ln1_b[l]);
+        place(ln2_g[l]);
+        place(ln2_b[l]);
+      }
+    }
     // Decode GEMVs read every int8 linear (and the head) from a panel-packed copy
     // (one contiguous KiB per wave load, already in MFMA B-operand order); the
     // row-major copy stays for the prefill GEMM.
@@ -411,7 +436,8 @@ struct ti_llm_model {
   }
 
   // ---------------------------------------------------------------- launch helpers
-  void gemm(const uint16_t* a, int m, const Linear& w, tia::Epilogue epi, int* deferred = nullptr) {
+  void gemm(const uint16_t* a, int m, const Linear& w, tia::Epilogue epi, int* deferred = nullptr,
+            const uint16_t* ln_g = nullptr, const uint16_t* ln_b = nullptr) {
     tia::GemmArgs g;
     g.a = a;
     g.lda = w.k;
@@ -423,6 +449,9 @@ struct ti_llm_model {
     g.k = w.k;
     g.ldw = w.ldw;
     g.w_packed = w.packed;
+    g.ln_gamma = ln_g;
+    g.ln_beta = ln_b;
+    g.ln_eps = 1e-5f;
     g.epi = epi;
     ck(tia::gemm(g, &scratch, stream, deferred));
   }
@@ -446,10 +475,33 @@ struct ti_llm_model {
       ck(tia::layernorm_f16(x, g, beta, norm, rows, H, 1e-5f, stream));
   }
 
+  // x += a @ w + bias in the GEMM's epilogue (no LayerNorm after it).
+  void residual(const uint16_t* a, int rows, const Linear& w) {
+    tia::Epilogue r;
+    r.kind = tia::EPI_RESIDUAL;
+    r.bias = w.bias;
+    r.y = x;
+    r.ldy = H;
+    r.residual = x;
+    r.ldr = H;
+    gemm(a, rows, w, r);
+  }
+
+  // Decode of up to 32 requests over packed weights: each LayerNorm runs in the
+  // prologue of the GEMV that consumes it (c_attn: ln_1, c_fc: ln_2, head: ln_f)
+  // and each residual add in the epilogue of the GEMV that produces it.
+  bool ln_fused(int b, int qlen) const {
+    return qlen == 1 && quantized && head.packed && c_attn[0].packed && tia::gemm_ln_supported(b, H, H);
+  }
+  bool head_ln = false;  // the last layers() pass left ln_f to the head GEMV
+
   // One pass of the transformer over rows [b, qlen] whose metadata is already on
-  // the device; leaves the residual stream in x and ln_f(x) of every row in norm.
+  // the device; leaves the residual stream in x and, unless ln_fused(b, qlen)
+  // (then the head applies ln_f itself), ln_f(x) of every row in norm.
   void layers(int b, int qlen) {
     const int rows = b * qlen;
+    const bool fuse = ln_fused(b, qlen);
+    head_ln = fuse;
     embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, ln1_g[0],
                                                              ln1_b[0], x, norm, rows, qlen, H);
     ck(hipGetLastError());
@@ -473,7 +525,9 @@ struct ti_llm_model {
       // Decode: the skinny GEMM leaves split-K partials and the attention kernel
       // finishes q, k, v itself (one launch fewer per layer).
       int qkv_splits = 0;
-      gemm(norm, rows, c_attn[l], e, qlen == 1 && c_attn[l].bias ? &qkv_splits : nullptr);
+      int* defer_qkv = qlen == 1 && c_attn[l].bias ? &qkv_splits : nullptr;
+      if (fuse) gemm(x, rows, c_attn[l], e, defer_qkv, ln1_g[l], ln1_b[l]);
+      else gemm(norm, rows, c_attn[l], e, defer_qkv);
 
       tia::AttnArgs at;
       if (qkv_splits > 0) {
@@ -508,20 +562,27 @@ struct ti_llm_model {
       at.causal = true;
       ck(tia::attention(at, stream));
 
-      residual_ln(attn, rows, c_proj[l], ln2_g[l], ln2_b[l]);
       tia::Epilogue gl;
       gl.kind = tia::EPI_GELU;
       gl.bias = c_fc[l].bias;
       gl.y = mlp;
       gl.ldy = 4 * H;
-      gemm(norm, rows, c_fc[l], gl);
+      if (fuse) {
+        residual(attn, rows, c_proj[l]);
+        gemm(x, rows, c_fc[l], gl, nullptr, ln2_g[l], ln2_b[l]);
+      } else {
+        residual_ln(attn, rows, c_proj[l], ln2_g[l], ln2_b[l]);
+        gemm(norm, rows, c_fc[l], gl);
+      }
       const bool final_layer = l + 1 == L;
-      residual_ln(mlp, rows, c_proj2[l], final_layer ? lnf_g : ln1_g[l + 1], final_layer ? lnf_b : ln1_b[l + 1]);
+      if (fuse) residual(mlp, rows, c_proj2[l]);
+      else residual_ln(mlp, rows, c_proj2[l], final_layer ? lnf_g : ln1_g[l + 1], final_layer ? lnf_b : ln1_b[l + 1]);
     }
   }
 
-  // Logits of each request's last row (norm already holds ln_f), fp32 without
-  // bias over the padded row pitch head.ldw, then the greedy argmax.
+  // Logits of each request's last row (ln_f of it from norm, or computed by the
+  // head GEMV from x after an ln_fused pass), fp32 without bias over the padded
+  // row pitch head.ldw, then the greedy argmax.
   void head_and_argmax(int b, int qlen, bool greedy) {
     const uint16_t* rows_in = norm;
     if (qlen > 1) {
@@ -533,7 +594,8 @@ struct ti_llm_model {
     e.kind = tia::EPI_F32;
     e.y = logits;
     e.ldy = head.ldw;
-    gemm(rows_in, b, head, e);
+    if (head_ln) gemm(x, b, head, e, nullptr, lnf_g, lnf_b);
+    else gemm(rows_in, b, head, e);
     if (greedy) {
       argmax_kernel<<<b, 1024, 0, stream>>>(logits, d_next, V, head.ldw);
       ck(hipGetLastError());
