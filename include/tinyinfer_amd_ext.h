@@ -41,12 +41,15 @@ int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, const float* sc
 
 /* ti_amd_gemm_w8p_ln_fused: the decode GEMV with the LayerNorm that precedes
  * every GPT-2 linear fed from the residual stream (reference
- * llm/src/runtime.cu:143 ln_1 -> c_attn, :150 ln_2 -> c_fc, :154 ln_f -> head)
- * computed in its prologue:
+ * llm/src/runtime.cu:143 ln_1 -> c_attn, :150 ln_2 -> c_fc) computed in its
+ * prologue:
  *   Y = epilogue(sum_k LN(A)[m,k] * fp16_rn(float(q[k,n]) * scales[n]) + bias[n]),
- *   LN(A)[m,:] = fp16_rn((A[m,:] - mean) * rsqrt(var + eps) * gamma + beta),
- * mean and var (population) in fp32 over the K columns of row m, as
- * ti_v2_layernorm_f16.  1 <= M <= 32, K % 64 == 0, K <= 2048; A, gamma, beta
+ *   LN(A)[m,:] = fp16_rn((A[m,:] * inv - mean * inv) * gamma + beta),
+ *   inv = rsqrt(var + eps),
+ * mean and var (population, two passes) in fp32 over the K columns of row m,
+ * as ti_v2_layernorm_f16 up to fp32 rounding.  The runtime uses it for decode;
+ * a caller with many workgroups per row set (the LM head) is better served by
+ * one ti_v2_layernorm_f16 pass, since every workgroup normalizes all M rows.  1 <= M <= 32, K % 64 == 0, K <= 2048; A, gamma, beta
  * and packed 16-byte aligned; epilogues as ti_amd_gemm_i8_fused. */
 int ti_amd_gemm_w8p_ln_fused(const uint16_t* a, const uint16_t* gamma, const uint16_t* beta, float eps,
                              const void* packed, const float* scales, const uint16_t* bias, uint16_t* y,

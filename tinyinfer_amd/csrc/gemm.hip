@@ -40,7 +40,9 @@ __device__ __forceinline__ float epilogue_bias(const Epilogue& e, int n) {
 }
 
 // `bias` is epilogue_bias(e, n) (callers may load it early); EPI_RAW_F32 ignores it.
-__device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias) {
+// `resid` is residual[m][n] for EPI_RESIDUAL (likewise loaded by the caller).
+__device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias,
+                                               float resid) {
   switch (e.kind) {
     case EPI_RAW_F32:
       static_cast<float*>(e.y)[int64_t(m) * e.ldy + n] = acc;
@@ -55,8 +57,7 @@ __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, 
     }
     case EPI_RESIDUAL: {
       const float h = rt16(acc + bias);
-      const float r = h2f(e.residual[int64_t(m) * e.ldr + n]);
-      static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(r + h);
+      static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(resid + h);
       return;
     }
     case EPI_QKV: {
@@ -81,6 +82,9 @@ __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, 
   }
 }
 
+__device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias) {
+  apply_epilogue(e, m, n, acc, bias, e.kind == EPI_RESIDUAL ? h2f(e.residual[int64_t(m) * e.ldr + n]) : 0.f);
+}
 __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc) {
   apply_epilogue(e, m, n, acc, e.kind == EPI_RAW_F32 ? 0.f : epilogue_bias(e, n));
 }
@@ -376,6 +380,10 @@ template <int MT, int W, int CPW, int CBG, bool LNA = false>
 __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   __shared__ float red[W][CBG][MT * 256];
   __shared__ float stat[LNA ? W : 1][MT * 16];  // per-wave LayerNorm partial sums
+  // LayerNorm gamma (q < CPW) and beta (q >= CPW) of chunk q % CPW of each
+  // wave, 16 bytes at [wave][q * 8 + part]: one load per lane, not one per A
+  // fragment and lane group.
+  __shared__ half8_t gbl[LNA ? W : 1][LNA ? 16 * CPW : 1];
   // The wave index is uniform: chunk bounds below are scalar, so every load of a
   // round is issued before the first wait.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -412,6 +420,22 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
   for (int t = 0; t < MT; ++t) arow[t] = p.a + int64_t(min(16 * t + j, p.m - 1)) * p.lda + 8 * g;
 
+  // Outputs of this thread in the epilogue: o = threadIdx.x + it * W * 64 over
+  // CBG blocks of rows x 16.  Their residuals are loaded now, unconditionally
+  // (A's first element stands in), like the bias.
+  constexpr int kOutIters = (CBG * MT * 256 + W * 64 - 1) / (W * 64);
+  const int rows = min(p.m, MT * 16), per_block = rows * 16;
+  const bool has_res = epi_now && p.epi.kind == EPI_RESIDUAL;
+  const uint16_t* rsrc = has_res ? p.epi.residual : p.a;
+  uint16_t res_raw[kOutIters];
+#pragma unroll
+  for (int it = 0; it < kOutIters; ++it) {
+    const int o = threadIdx.x + it * W * 64, r = o / per_block, rem = o - r * per_block;
+    const int n = (cb0 + r) * 16 + (rem & 15);
+    const bool ok = has_res && o < CBG * per_block && cb0 + r < p.nb && n < p.n;
+    res_raw[it] = rsrc[ok ? int64_t(rem >> 4) * p.epi.ldr + n : 0];
+  }
+
   float4_t acc[MT][CBG];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
@@ -422,7 +446,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   auto round = [&](int c0) {
     u32x4_t wf[CPW][CBG];
     half8_t af[CPW][2][MT];
-    half8_t gam[CPW][2], bet[CPW][2];
+    half8_t gbv;
     auto load_w = [&](int i) {
       const int c = min(c0 + i * W, c_end - 1);
 #pragma unroll
@@ -435,15 +459,16 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
         for (int t = 0; t < MT; ++t)
           af[i][s][t] = *reinterpret_cast<const half8_t*>(arow[t] + c * 64 + 32 * s);
-        if constexpr (LNA) {
-          gam[i][s] = *reinterpret_cast<const half8_t*>(p.ln_gamma + c * 64 + 32 * s + 8 * g);
-          bet[i][s] = *reinterpret_cast<const half8_t*>(p.ln_beta + c * 64 + 32 * s + 8 * g);
-        }
       }
     };
+    // Lanes past 16 * CPW repeat the last (q, part) pair: same address, same
+    // LDS slot, same value.
+    const int gb_q = min(lane >> 3, 2 * CPW - 1), gb_slot = gb_q * 8 + (lane & 7);
     if constexpr (LNA) {
-      // A, gamma and beta first: the LayerNorm below needs only them (loads
+      // gamma/beta and A first: the LayerNorm below needs only them (loads
       // complete in order), so it runs while the weight records are in flight.
+      const int c = min(c0 + (gb_q % CPW) * W, c_end - 1);
+      gbv = *reinterpret_cast<const half8_t*>((gb_q < CPW ? p.ln_gamma : p.ln_beta) + c * 64 + (lane & 7) * 8);
 #pragma unroll
       for (int i = 0; i < CPW; ++i) load_a(i);
 #pragma unroll
@@ -463,12 +488,20 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     for (int r = 0; r < CBG; ++r) sc[r] = *scp[r];
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (LNA) {
-      // LayerNorm of the A rows, as the row kernel computes it (two-pass fp32
-      // mean and variance over the K = hidden columns, rsqrt(var + eps),
-      // fp16_rn((x - mean) * inv * gamma + beta)); every chunk of K is in this
-      // workgroup's single round, spread over the waves and the 4 k-groups of
-      // a row's lanes.
-      float mean[MT], inv[MT];
+      // LayerNorm of the A rows over the K = hidden columns: two-pass fp32
+      // mean and variance as the row kernel (sum of x, then of (x - mean)^2),
+      // rsqrt(var + eps), fp16_rn((x * inv - mean * inv) * gamma + beta).  Every
+      // chunk of K is in this workgroup's single round, spread over the waves
+      // and the 4 k-groups of a row's lanes.  The first pass sums fp16 pairs
+      // with dot2 (exact products, fp32 sums) and the normalization reads x,
+      // gamma and beta as fp16 operands of mixed-precision fmas.
+      float mean[MT], inv[MT], shift[MT];
+      gbl[wave][gb_slot] = gbv;  // read after the barriers below
+      const half2_t ones = {f16(1.f), f16(1.f)};
+      // An opaque 1.0: fma(x, one, -mean) stays one mixed-precision fma (the
+      // compiler would turn a literal 1.0 into a conversion and a subtraction).
+      float one = 1.f;
+      asm volatile("" : "+v"(one));
 #pragma unroll
       for (int pass = 0; pass < 2; ++pass) {
         float part[MT];
@@ -481,9 +514,14 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
             for (int s = 0; s < 2; ++s)
 #pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                const float x = float(af[i][s][t][e]);
-                pc += pass == 0 ? x : (x - mean[t]) * (x - mean[t]);
+              for (int e = 0; e < 8; e += 2) {
+                if (pass == 0) {
+                  pc = __builtin_amdgcn_fdot2(half2_t{af[i][s][t][e], af[i][s][t][e + 1]}, ones, pc, false);
+                } else {
+                  const float d0 = fmaf(float(af[i][s][t][e]), one, -mean[t]);
+                  const float d1 = fmaf(float(af[i][s][t][e + 1]), one, -mean[t]);
+                  pc = fmaf(d1, d1, fmaf(d0, d0, pc));
+                }
               }
             // A chunk past the end re-read the last one: it is not counted.
             part[t] += c0 + i * W < c_end ? pc : 0.f;
@@ -506,15 +544,19 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
         lds_barrier();
       }
 #pragma unroll
+      for (int t = 0; t < MT; ++t) shift[t] = -mean[t] * inv[t];
+#pragma unroll
       for (int i = 0; i < CPW; ++i)
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < 2; ++s) {
+          const half8_t gam = gbl[wave][i * 8 + 4 * s + g], bet = gbl[wave][(CPW + i) * 8 + 4 * s + g];
 #pragma unroll
           for (int t = 0; t < MT; ++t)
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-              af[i][s][t][e] = f16((float(af[i][s][t][e]) - mean[t]) * inv[t] * float(gam[i][s][e]) +
-                                   float(bet[i][s][e]));
+              af[i][s][t][e] =
+                  f16(fmaf(fmaf(float(af[i][s][t][e]), inv[t], shift[t]), float(gam[e]), float(bet[e])));
+        }
       // Keep the weight dequantization (which waits for the records) after the
       // LayerNorm.
       __builtin_amdgcn_sched_barrier(0);
@@ -552,11 +594,16 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) red[wave][r][(16 * t + 4 * g + v) * 16 + j] = acc[t][r][v];
   __syncthreads();
-  const int rows = min(p.m, MT * 16), per_block = rows * 16;
-  for (int o = threadIdx.x; o < CBG * per_block; o += W * 64) {
-    const int r = o / per_block, rem = o - r * per_block;
+  // The epilogue recomputes its indices (an opaque copy of the thread index
+  // keeps the compiler from holding those of the residual loads live through
+  // the main loop).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+#pragma unroll
+  for (int it = 0; it < kOutIters; ++it) {
+    const int o = tid + it * W * 64, r = o / per_block, rem = o - r * per_block;
     const int row = rem >> 4, n = (cb0 + r) * 16 + (rem & 15);
-    if (cb0 + r >= p.nb || n >= p.n) continue;
+    if (o >= CBG * per_block || cb0 + r >= p.nb || n >= p.n) continue;
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < W; ++w) s += red[w][r][rem];
@@ -564,7 +611,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
     for (int q = 1; q < CBG; ++q) braw = r == q ? bias_raw[q] : braw;
     const float bias = has_bias ? h2f(braw) : 0.f;
-    if (epi_now) apply_epilogue(p.epi, row, n, s, bias);
+    if (epi_now) apply_epilogue(p.epi, row, n, s, bias, has_res ? h2f(res_raw[it]) : 0.f);
     else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
   }
 }
@@ -975,70 +1022,56 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   return hipGetLastError();
 }
 
-// Launch shape of the packed GEMV.  M <= 16: one column block per workgroup
-// (A is one row, its re-reads are free).  M <= 32: four column blocks share
-// each A fragment when the matrix is wide enough to keep >= 128 workgroups
-// without splitting K (the LM head); for the narrower decode GEMVs that
-// measured no faster, and splitting K further to compensate only moved time
-// into the consumers of the partials.  Waves W in {4, 8, 16} so that W * CPW
-// chunks cover one split's K range in one round where possible.  A deferred
-// launch splits K to reach ~192 workgroups, keeping >= 4 chunks per split and
-// the partials within the scratch; otherwise one split and the epilogue runs
-// in the kernel.
-template <int MT, int CPW, int CBG>
-hipError_t launch_packed_cfg(PackedParams& p, const GemmArgs& g, const Scratch* s, hipStream_t stream,
-                             int* deferred) {
-  const int groups = (p.nb + CBG - 1) / CBG;
-  int splits = 1;
-  if (deferred && s && s->partials) {
-    splits = std::max(1, std::min((192 + groups - 1) / groups, p.kc / 4));
-    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
+// Launch shape of the packed GEMV (timed on MI355X over the GPT-2 decode
+// shapes, M = 1 and 32, K = 768 / 3072, N = 768 .. 50257):
+//  * W waves x CPW chunks per wave cover a split's K range with the fewest dead
+//    slots (a dead slot re-reads a chunk): 12 chunks -> 4 x 3, 16 -> 4 x 4,
+//    24 -> 8 x 3, 32 -> 8 x 4, 48 -> 16 x 3 (M <= 16);
+//  * at M > 16 every 16-column block re-reads A (4 KiB per chunk against 1 KiB
+//    of weights), and more than 8 waves only queue more A requests on one CU:
+//    longer ranges take several rounds of 8 x 2;
+//  * at M > 16 two column blocks share each A fragment (CBG = 2) when that
+//    still leaves >= 512 workgroups (the LM head);
+//  * a deferred launch splits K to reach ~192 workgroups, keeping >= 4 chunks
+//    per split and the partials within the scratch; otherwise one split and
+//    the epilogue runs in the kernel;
+//  * a LayerNorm-prologue launch is one split covered by one round.
+struct GemvShape {
+  int w, cpw, cbg;
+};
+
+GemvShape gemv_shape(int mt, int chunks, bool one_round) {
+  if (chunks <= 12) return {4, 3, 1};
+  if (chunks <= 16) return {4, 4, 1};
+  if (one_round || mt == 1) {
+    if (chunks <= 24) return {8, 3, 1};
+    if (chunks <= 32) return {8, 4, 1};
+    if (mt == 1) return chunks <= 48 ? GemvShape{16, 3, 1} : GemvShape{16, 4, 1};
   }
-  p.chunks_per_split = (p.kc + splits - 1) / splits;
-  splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
-  p.splits = splits;
-  p.defer = deferred != nullptr;
-  p.partials = s ? s->partials : nullptr;
-  if (p.defer && (!p.partials || size_t(splits) * g.m * g.n > s->partial_floats)) return hipErrorInvalidValue;
-  const dim3 grid(unsigned(groups) * unsigned(splits));
-  const int cps = p.chunks_per_split;
-  // Four-block groups hold 4x the weight registers: at most 8 waves (16 would
-  // exceed 128 VGPRs), with further rounds for longer splits.
-  if (cps <= 4 * CPW)
-    hipLaunchKernelGGL((gemv_packed_kernel<MT, 4, CPW, CBG>), grid, dim3(256), 0, stream, p);
-  else if (cps <= 8 * CPW || CBG > 1)
-    hipLaunchKernelGGL((gemv_packed_kernel<MT, 8, CPW, CBG>), grid, dim3(512), 0, stream, p);
-  else
-    hipLaunchKernelGGL((gemv_packed_kernel<MT, 16, CPW, 1>), grid, dim3(1024), 0, stream, p);
-  if (deferred) *deferred = splits;
-  return hipGetLastError();
+  return {8, 2, 1};
 }
 
-// LayerNorm prologue: one split whose K range one round covers.  A deferred
-// launch leaves its sums as partials [1][M][N].
-template <int MT, int W, int CPW, int CBG>
-hipError_t launch_packed_ln_cfg(PackedParams& p, const Scratch* s, hipStream_t stream, int* deferred) {
-  p.chunks_per_split = p.kc;
-  p.splits = 1;
-  p.defer = deferred != nullptr;
-  p.partials = s ? s->partials : nullptr;
-  if (p.defer && (!p.partials || size_t(p.m) * p.n > s->partial_floats)) return hipErrorInvalidValue;
-  const int groups = (p.nb + CBG - 1) / CBG;
-  hipLaunchKernelGGL((gemv_packed_kernel<MT, W, CPW, CBG, true>), dim3(unsigned(groups)), dim3(W * 64), 0,
-                     stream, p);
-  if (deferred) *deferred = 1;
-  return hipGetLastError();
-}
-
-template <int MT>
-hipError_t launch_packed_ln(PackedParams& p, const Scratch* s, hipStream_t stream, int* deferred) {
+template <int MT, bool LNA>
+hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipStream_t st) {
+#define TIA_GEMV(W_, C_, B_)                                                                            \
+  if (sh.w == W_ && sh.cpw == C_ && sh.cbg == B_) {                                                     \
+    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
+    return hipGetLastError();                                                                           \
+  }
+  TIA_GEMV(4, 3, 1)
+  TIA_GEMV(4, 4, 1)
+  TIA_GEMV(8, 3, 1)
+  TIA_GEMV(8, 4, 1)
   if constexpr (MT == 2) {
-    if (!deferred && (p.nb + 3) / 4 >= 128 && p.kc <= 16)
-      return launch_packed_ln_cfg<2, 8, 2, 4>(p, s, stream, deferred);
+    TIA_GEMV(4, 3, 2)
+    TIA_GEMV(4, 4, 2)
   }
-  if (p.kc <= 12) return launch_packed_ln_cfg<MT, 4, 3, 1>(p, s, stream, deferred);
-  if (p.kc <= 16) return launch_packed_ln_cfg<MT, 4, 4, 1>(p, s, stream, deferred);
-  if (p.kc <= kLnMaxChunks) return launch_packed_ln_cfg<MT, 8, 4, 1>(p, s, stream, deferred);
+  if constexpr (MT == 1 && !LNA) {
+    TIA_GEMV(16, 3, 1)
+    TIA_GEMV(16, 4, 1)
+  }
+  if constexpr (MT == 2 && !LNA) TIA_GEMV(8, 2, 1)
+#undef TIA_GEMV
   return hipErrorInvalidValue;
 }
 
@@ -1049,14 +1082,28 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.nb = (g.n + 15) / 16;
   p.kc = g.k / 64;
-  if (g.ln_gamma) {
+  p.partials = s ? s->partials : nullptr;
+  p.defer = deferred != nullptr;
+  const bool ln = g.ln_gamma != nullptr;
+  if (ln) {
     p.ln_gamma = g.ln_gamma; p.ln_beta = g.ln_beta; p.ln_eps = g.ln_eps;
-    return launch_packed_ln<MT>(p, s, stream, deferred);
   }
-  if constexpr (MT == 2) {
-    if (!deferred && (p.nb + 3) / 4 >= 128) return launch_packed_cfg<2, 2, 4>(p, g, s, stream, deferred);
+  int splits = 1;
+  if (deferred && !ln && s && s->partials) {
+    const int groups = p.nb;
+    splits = std::max(1, std::min((192 + groups - 1) / groups, p.kc / 4));
+    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
   }
-  return launch_packed_cfg<MT, 4, 1>(p, g, s, stream, deferred);
+  p.chunks_per_split = (p.kc + splits - 1) / splits;
+  splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
+  p.splits = splits;
+  if (p.defer && (!p.partials || size_t(splits) * g.m * g.n > s->partial_floats)) return hipErrorInvalidValue;
+  GemvShape sh = gemv_shape(MT, p.chunks_per_split, ln);
+  if (ln && sh.w * sh.cpw < p.kc) return hipErrorInvalidValue;
+  if (MT == 2 && !p.defer && sh.w == 4 && (p.nb + 1) / 2 >= 512) sh.cbg = 2;
+  const int grid = (p.nb + sh.cbg - 1) / sh.cbg * splits;
+  if (deferred) *deferred = splits;
+  return ln ? launch_gemv_shape<MT, true>(p, sh, grid, stream) : launch_gemv_shape<MT, false>(p, sh, grid, stream);
 }
 
 // 64x64 tiles, S = 4 stages of 12 KiB (48 KiB of LDS: three workgroups per CU,

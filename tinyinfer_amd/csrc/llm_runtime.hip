@@ -10,12 +10,12 @@
 //    reduces its split-K partials, adds bias and residual (in place) and applies
 //    LN2 -> c_fc GEMM with fused bias + GELU -> mlp.c_proj GEMM -> the same
 //    reduce + residual kernel applying the next layer's LN1 (ln_f after the last);
-//  * decode of up to 32 requests over packed int8 weights instead runs each
-//    LayerNorm in the prologue of the GEMV that consumes it (ln_1 in c_attn,
-//    ln_2 in c_fc, ln_f in the head) and each residual add in the epilogue of
-//    the GEMV that produces it: per layer c_attn (split-K partials) ->
-//    attention (finishes q/k/v) -> c_proj (+residual) -> c_fc (LN2, GELU) ->
-//    mlp.c_proj (+residual), five launches;
+//  * decode of up to 32 requests over packed int8 weights instead runs ln_1
+//    and ln_2 in the prologue of the GEMV that consumes them (c_attn, c_fc)
+//    and each residual add in the epilogue of the GEMV that produces it: per
+//    layer c_attn (split-K partials) -> attention (finishes q/k/v) -> c_proj
+//    (+residual) -> c_fc (LN2, GELU) -> mlp.c_proj (+residual), five launches,
+//    and ln_f as a row kernel before the head;
 //  * the lm_head GEMM writes fp32 logits of each request's last row (padded row
 //    pitch), a block-per-row argmax picks the lowest id on ties;
 //  * a decode step (every request appends one token) is captured once per
@@ -490,18 +490,20 @@ struct ti_llm_model {
   // Decode of up to 32 requests over packed weights: each LayerNorm runs in the
   // prologue of the GEMV that consumes it (c_attn: ln_1, c_fc: ln_2, head: ln_f)
   // and each residual add in the epilogue of the GEMV that produces it.
+  // Up to hidden 1024 (16 K chunks, one round of 4 waves): at GPT-2 XL's 1600
+  // the prologue's per-workgroup LayerNorm and the unsplit c_proj launches
+  // measured slower than the split-K GEMVs and their reduce + residual + LN
+  // kernels.
   bool ln_fused(int b, int qlen) const {
-    return qlen == 1 && quantized && head.packed && c_attn[0].packed && tia::gemm_ln_supported(b, H, H);
+    return qlen == 1 && quantized && head.packed && c_attn[0].packed && H <= 1024 &&
+           tia::gemm_ln_supported(b, H, H);
   }
-  bool head_ln = false;  // the last layers() pass left ln_f to the head GEMV
 
   // One pass of the transformer over rows [b, qlen] whose metadata is already on
-  // the device; leaves the residual stream in x and, unless ln_fused(b, qlen)
-  // (then the head applies ln_f itself), ln_f(x) of every row in norm.
+  // the device; leaves the residual stream in x and ln_f(x) of every row in norm.
   void layers(int b, int qlen) {
     const int rows = b * qlen;
     const bool fuse = ln_fused(b, qlen);
-    head_ln = fuse;
     embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, ln1_g[0],
                                                              ln1_b[0], x, norm, rows, qlen, H);
     ck(hipGetLastError());
@@ -575,14 +577,19 @@ struct ti_llm_model {
         gemm(norm, rows, c_fc[l], gl);
       }
       const bool final_layer = l + 1 == L;
-      if (fuse) residual(mlp, rows, c_proj2[l]);
-      else residual_ln(mlp, rows, c_proj2[l], final_layer ? lnf_g : ln1_g[l + 1], final_layer ? lnf_b : ln1_b[l + 1]);
+      if (!fuse) {
+        residual_ln(mlp, rows, c_proj2[l], final_layer ? lnf_g : ln1_g[l + 1], final_layer ? lnf_b : ln1_b[l + 1]);
+        continue;
+      }
+      residual(mlp, rows, c_proj2[l]);
+      // ln_f as its own row kernel: in the head GEMV's prologue every one of its
+      // thousands of workgroups would normalize the same rows again.
+      if (final_layer) ck(tia::layernorm_f16(x, lnf_g, lnf_b, norm, rows, H, 1e-5f, stream));
     }
   }
 
-  // Logits of each request's last row (ln_f of it from norm, or computed by the
-  // head GEMV from x after an ln_fused pass), fp32 without bias over the padded
-  // row pitch head.ldw, then the greedy argmax.
+  // Logits of each request's last row (norm already holds ln_f), fp32 without
+  // bias over the padded row pitch head.ldw, then the greedy argmax.
   void head_and_argmax(int b, int qlen, bool greedy) {
     const uint16_t* rows_in = norm;
     if (qlen > 1) {
@@ -594,8 +601,7 @@ struct ti_llm_model {
     e.kind = tia::EPI_F32;
     e.y = logits;
     e.ldy = head.ldw;
-    if (head_ln) gemm(x, b, head, e, nullptr, lnf_g, lnf_b);
-    else gemm(rows_in, b, head, e);
+    gemm(rows_in, b, head, e);
     if (greedy) {
       argmax_kernel<<<b, 1024, 0, stream>>>(logits, d_next, V, head.ldw);
       ck(hipGetLastError());
