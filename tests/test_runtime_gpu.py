@@ -153,6 +153,35 @@ def test_logits_match_oracle(model, cpu_model):
     model.reset_all()
 
 
+def test_decode_b17_and_one_row_score_match_oracle(model, cpu_model):
+    """Decode of 17 requests (two 16-row MFMA tiles, the second mostly padding
+    rows of the fragment-packed activations) and a two-token score (a one-row
+    pass, whose ln_f output the head reads fragment-packed) against the oracle."""
+    ids = token_ids(17 * 3 + 2, seed=13)
+    prompts = [ids[3 * i:3 * i + 3] for i in range(17)]
+    slots = list(range(17))
+    say("decode b17 vs oracle")
+    model.reset_all()
+    model.forward(slots, prompts, return_logits=False, return_next=False)
+    for s in slots:
+        cpu_model.reset(s)
+    _, nxt = cpu_model.forward(slots, prompts)
+    step = [[int(t)] for t in nxt]
+    gpu = logits_of(model.forward(slots, step))
+    cpu, _ = cpu_model.forward(slots, step)
+    print(f"b17 decode max |logit diff| {np.abs(gpu - cpu).max():.3g}")
+    assert np.abs(gpu - cpu).max() <= 5e-2
+    say("two-token score vs oracle")
+    pair = ids[-2:]
+    sc = model.score(pair, [0, 1], positions=True)
+    cpu_model.reset(0)
+    lg = np.asarray(cpu_model.forward([0], [pair[:1]])[0][0], np.float64)
+    m = lg.max()
+    want = m + np.log(np.exp(lg - m).sum()) - lg[pair[1]]
+    assert abs(sc["position_nll"][1] - want) <= 5e-2
+    model.reset_all()
+
+
 def test_decode_graph_equals_eager(model):
     ids = token_ids(20, seed=9)
     say("graph vs eager")

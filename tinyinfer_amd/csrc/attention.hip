@@ -274,7 +274,8 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   }
   if (qi >= a.q_len || kg != 0) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(qi) * a.o_sq + 8 * ds;
+  uint16_t* op = a.out + (a.out_p32 ? p32_off(b * a.q_len + qi, h * D + 8 * ds)
+                                    : int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(qi) * a.o_sq + 8 * ds);
   half8_t o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = f16(l > 0.f ? acc[e] * inv : 0.f);
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
 #pragma unroll
     for (int e = 0; e < DPL; ++e) acc[e] += ca[c][e] * f;
   }
-  uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + DPL * lane;
+  uint16_t* op = a.out + (a.out_p32 ? p32_off(b, h * D + DPL * lane) : int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + DPL * lane);
   const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
   for (int e = 0; e < DPL; ++e) op[e] = f2h(l > 0.f ? acc[e] * inv : 0.f);
@@ -559,6 +560,9 @@ bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 hipError_t attention(const AttnArgs& a, hipStream_t stream, const Scratch* scratch) {
   if (a.batch <= 0 || a.heads <= 0 || a.q_len <= 0) return hipSuccess;
+  // P32 output: decode rows only (the MFMA prefill kernel writes row-major).
+  if (a.out_p32 && (a.q_len != 1 || a.batch > 32 || (a.heads * a.head_dim) % 64 != 0 || !al16(a.out)))
+    return hipErrorInvalidValue;
   AttnParams p{};
   p.a = a;
   // Decode over a long cache (at least 4 chunks of 256/128 keys per (b, h)) and

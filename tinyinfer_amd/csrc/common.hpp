@@ -14,6 +14,18 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Fragment-packed activations ("P32") for decode matrices of at most 32 rows
+// and K % 64 == 0: the 1 KiB MFMA A operand of rows 16t..16t+15, K columns
+// 64c + 32s .. +31 (lane j + 16g holding row 16t + j, columns +8g .. +8g+7) is
+// contiguous at element ((c * 2 + t) * 2 + s) * 512, so a wave loads it with
+// one fully used 16-byte-per-lane instruction (row-major A would touch 16 rows
+// with half-used cache lines per instruction).  A [32, K] matrix takes 32 * K
+// elements; 8 consecutive columns k..k+7 (k % 8 == 0) of a row are contiguous.
+__host__ __device__ __forceinline__ int64_t p32_off(int m, int k) {
+  return ((int64_t(k >> 6) * 2 + (m >> 4)) * 2 + ((k >> 5) & 1)) * 512 + ((m & 15) + 16 * ((k >> 3) & 3)) * 8 +
+         (k & 7);
+}
+
 // fp16 bits <-> fp32.  The conversion to fp16 is v_cvt_f16_f32, which rounds to
 // nearest-even under the default wave mode register.
 __device__ __forceinline__ float h2f(uint16_t bits) { return float(__builtin_bit_cast(f16, bits)); }

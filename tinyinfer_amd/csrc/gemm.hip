@@ -39,6 +39,15 @@ __device__ __forceinline__ float epilogue_bias(const Epilogue& e, int n) {
   return e.bias ? h2f(e.bias[n]) : 0.f;
 }
 
+// Element (m, n) of the fp16 output (and of the residual): row-major, or P32
+// fragment-packed.
+__device__ __forceinline__ int64_t y_off(const Epilogue& e, int m, int n) {
+  return e.p32 ? p32_off(m, n) : int64_t(m) * e.ldy + n;
+}
+__device__ __forceinline__ int64_t r_off(const Epilogue& e, int m, int n) {
+  return e.p32 ? p32_off(m, n) : int64_t(m) * e.ldr + n;
+}
+
 // `bias` is epilogue_bias(e, n) (callers may load it early); EPI_RAW_F32 ignores it.
 // `resid` is residual[m][n] for EPI_RESIDUAL (likewise loaded by the caller).
 __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias,
@@ -52,12 +61,12 @@ __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, 
       return;
     case EPI_GELU: {
       const float h = rt16(acc + bias);
-      static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(gelu_tanh(h));
+      static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(gelu_tanh(h));
       return;
     }
     case EPI_RESIDUAL: {
       const float h = rt16(acc + bias);
-      static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(resid + h);
+      static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(resid + h);
       return;
     }
     case EPI_QKV: {
@@ -77,13 +86,13 @@ __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, 
       return;
     }
     default:  // EPI_F16
-      static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = f2h(acc + bias);
+      static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(acc + bias);
       return;
   }
 }
 
 __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias) {
-  apply_epilogue(e, m, n, acc, bias, e.kind == EPI_RESIDUAL ? h2f(e.residual[int64_t(m) * e.ldr + n]) : 0.f);
+  apply_epilogue(e, m, n, acc, bias, e.kind == EPI_RESIDUAL ? h2f(e.residual[r_off(e, m, n)]) : 0.f);
 }
 __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc) {
   apply_epilogue(e, m, n, acc, e.kind == EPI_RAW_F32 ? 0.f : epilogue_bias(e, n));
@@ -375,8 +384,9 @@ __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scal
 // (rows >= M, blocks >= nb are computed from valid data and never stored).
 // LNA: A is LayerNorm(a) over its K = hidden columns, computed from the loaded
 // fragments before the MFMAs; the launch then covers K in one round of one
-// split (W * CPW >= kc).
-template <int MT, int W, int CPW, int CBG, bool LNA = false>
+// split (W * CPW >= kc).  PA: A is P32 fragment-packed (each A fragment one
+// contiguous KiB).
+template <int MT, int W, int CPW, int CBG, bool LNA = false, bool PA = false>
 __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   __shared__ float red[W][CBG][MT * 256];
   __shared__ float stat[LNA ? W : 1][MT * 16];  // per-wave LayerNorm partial sums
@@ -419,6 +429,11 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   const uint16_t* arow[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) arow[t] = p.a + int64_t(min(16 * t + j, p.m - 1)) * p.lda + 8 * g;
+  // PA: lane offset inside a fragment, rows past M clamped to row M - 1 like
+  // the row-major path (at M = 1 a fragment load then touches one cache line).
+  int pa_lane[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) pa_lane[t] = (min(16 * t + j, p.m - 1) - 16 * t + 16 * g) * 8;
 
   // Outputs of this thread in the epilogue: o = threadIdx.x + it * W * 64 over
   // CBG blocks of rows x 16.  Their residuals are loaded now, unconditionally
@@ -433,7 +448,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     const int o = threadIdx.x + it * W * 64, r = o / per_block, rem = o - r * per_block;
     const int n = (cb0 + r) * 16 + (rem & 15);
     const bool ok = has_res && o < CBG * per_block && cb0 + r < p.nb && n < p.n;
-    res_raw[it] = rsrc[ok ? int64_t(rem >> 4) * p.epi.ldr + n : 0];
+    res_raw[it] = rsrc[ok ? r_off(p.epi, rem >> 4, n) : 0];
   }
 
   float4_t acc[MT][CBG];
@@ -458,7 +473,8 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
       for (int s = 0; s < 2; ++s) {
 #pragma unroll
         for (int t = 0; t < MT; ++t)
-          af[i][s][t] = *reinterpret_cast<const half8_t*>(arow[t] + c * 64 + 32 * s);
+          af[i][s][t] = PA ? *reinterpret_cast<const half8_t*>(p.a + ((int64_t(c) * 2 + t) * 2 + s) * 512 + pa_lane[t])
+                           : *reinterpret_cast<const half8_t*>(arow[t] + c * 64 + 32 * s);
       }
     };
     // Lanes past 16 * CPW repeat the last (q, part) pair: same address, same
@@ -1051,11 +1067,11 @@ GemvShape gemv_shape(int mt, int chunks, bool one_round) {
   return {8, 2, 1};
 }
 
-template <int MT, bool LNA>
+template <int MT, bool LNA, bool PA>
 hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipStream_t st) {
 #define TIA_GEMV(W_, C_, B_)                                                                            \
   if (sh.w == W_ && sh.cpw == C_ && sh.cbg == B_) {                                                     \
-    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
+    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA, PA>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
     return hipGetLastError();                                                                           \
   }
   TIA_GEMV(4, 3, 1)
@@ -1103,7 +1119,11 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   if (MT == 2 && !p.defer && sh.w == 4 && (p.nb + 1) / 2 >= 512) sh.cbg = 2;
   const int grid = (p.nb + sh.cbg - 1) / sh.cbg * splits;
   if (deferred) *deferred = splits;
-  return ln ? launch_gemv_shape<MT, true>(p, sh, grid, stream) : launch_gemv_shape<MT, false>(p, sh, grid, stream);
+  if (g.a_p32)
+    return ln ? launch_gemv_shape<MT, true, true>(p, sh, grid, stream)
+              : launch_gemv_shape<MT, false, true>(p, sh, grid, stream);
+  return ln ? launch_gemv_shape<MT, true, false>(p, sh, grid, stream)
+            : launch_gemv_shape<MT, false, false>(p, sh, grid, stream);
 }
 
 // 64x64 tiles, S = 4 stages of 12 KiB (48 KiB of LDS: three workgroups per CU,
@@ -1187,7 +1207,15 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   const int64_t ldw = g.ldw > 0 ? g.ldw : g.n;
   const bool wvec = ldw % 4 == 0 && ldw >= (int64_t(g.n) + 3) / 4 * 4 &&
                     (g.w_int8 ? wp % 4 == 0 : wp % 8 == 0);
-  const bool avec = (g.lda % 8 == 0) && (ap % 16 == 0);
+  const bool avec = ((g.lda % 8 == 0) || g.a_p32) && (ap % 16 == 0);
+  if (g.a_p32 || g.epi.p32) {
+    // P32 operands exist only for the packed-weight decode GEMV.
+    const bool epi_ok = !g.epi.p32 || ((g.epi.kind == EPI_F16 || g.epi.kind == EPI_GELU ||
+                                        g.epi.kind == EPI_RESIDUAL) && g.n % 64 == 0 && !deferred);
+    if (g.m > 32 || g.k % 64 != 0 || !g.w_int8 || !g.w_packed || !epi_ok ||
+        reinterpret_cast<uintptr_t>(g.a) % 16 != 0 || reinterpret_cast<uintptr_t>(g.w_packed) % 16 != 0)
+      return hipErrorInvalidValue;
+  }
   if (g.ln_gamma) {
     if (!gemm_ln_supported(g.m, g.k, g.n) || !g.w_int8 || !g.w_packed || !g.ln_beta || !avec ||
         reinterpret_cast<uintptr_t>(g.w_packed) % 16 != 0 || reinterpret_cast<uintptr_t>(g.ln_gamma) % 16 != 0 ||

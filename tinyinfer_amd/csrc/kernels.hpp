@@ -35,6 +35,9 @@ struct Epilogue {
   const int32_t* offsets = nullptr;
   const int32_t* qlens = nullptr;
   int qrows = 1, hidden = 0, heads = 0, layer = 0, layers = 0, capacity = 0;
+  // EPI_F16 / EPI_GELU / EPI_RESIDUAL: y (and residual) are P32 fragment-packed
+  // (common.hpp p32_off) instead of row-major; ldy / ldr are ignored.
+  bool p32 = false;
 };
 
 // Split-K partial sums of the skinny (M <= 32) GEMM: [splits][M][N] fp32.
@@ -56,6 +59,8 @@ struct GemmArgs {
   // Optional panel-packed copy of the int8 W (pack_w8).  When set, M <= 32,
   // K % 64 == 0 and A allows 16-byte loads, the GEMV over the packed records runs.
   const void* w_packed = nullptr;
+  // A is P32 fragment-packed (M <= 32, packed W; lda ignored).
+  bool a_p32 = false;
   // Optional LayerNorm of the A rows (packed int8 W, M <= 32, gemm_ln_supported):
   // the GEMM multiplies fp16_rn((a - mean) * rsqrt(var + eps) * gamma + beta),
   // mean and var over the K columns of each row, as layernorm_f16 computes them.
@@ -128,6 +133,9 @@ struct AttnArgs {
   int qkv_splits = 0;
   const uint16_t* qkv_bias = nullptr;
   int hidden = 0;
+  // Output row b * q_len + qi, columns h * head_dim + d, written P32
+  // fragment-packed (rows < 32, heads * head_dim % 64 == 0); o_* ignored.
+  bool out_p32 = false;
 };
 // With a scratch, single-query attention over a long cache (kv_len >= 1024 for
 // head_dim 64, >= 512 for 128) splits the keys of each (b, h) across
@@ -136,6 +144,9 @@ hipError_t attention(const AttnArgs& args, hipStream_t stream, const Scratch* sc
 
 hipError_t layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
                          int rows, int cols, float eps, hipStream_t stream);
+// The same over P32 fragment-packed x and y (rows <= 32, cols % 64 == 0).
+hipError_t layernorm_f16_p32(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
+                             int rows, int cols, float eps, hipStream_t stream);
 hipError_t softmax_f16(const uint16_t* x, uint16_t* y, int rows, int cols, hipStream_t stream);
 hipError_t gelu_f16(const uint16_t* x, uint16_t* y, int64_t count, hipStream_t stream);
 hipError_t layernorm_f32(const float* x, const float* g, const float* b, float* y, int rows,

@@ -84,10 +84,12 @@ __global__ void gather_last_kernel(const uint16_t* x, uint16_t* out, const int32
 // x[row] = fp16(wte[id] + wpe[offset + t]) for t < qlens[b], else 0 (reference
 // runtime.cu:25-30), fused with the first layer's LayerNorm of that row: one
 // wave per row, lane owns the 8-wide column groups lane + 64 i (hidden <= 2048).
+// p32: x and norm are written P32 fragment-packed (rows <= 32, hidden % 64 == 0).
 __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const int32_t* qlens,
                                                        const int32_t* offsets, const uint16_t* wte,
                                                        const uint16_t* wpe, const uint16_t* g, const uint16_t* bt,
-                                                       uint16_t* x, uint16_t* norm, int rows, int qlen, int hidden) {
+                                                       uint16_t* x, uint16_t* norm, int rows, int qlen, int hidden,
+                                                       bool p32) {
   constexpr int NV = 4;
   const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -114,7 +116,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const
         o[k] = tia::f16(v[i][k]);
         s += v[i][k];
       }
-      *reinterpret_cast<tia::half8_t*>(x + int64_t(row) * hidden + 8 * gi) = o;
+      *reinterpret_cast<tia::half8_t*>(x + (p32 ? tia::p32_off(row, 8 * gi) : int64_t(row) * hidden + 8 * gi)) = o;
     }
   }
   const float mean = tia::wave_sum(s) / float(hidden);
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const
       tia::half8_t o;
 #pragma unroll
       for (int k = 0; k < 8; ++k) o[k] = tia::f16((v[i][k] - mean) * inv * float(gg[k]) + float(bb[k]));
-      *reinterpret_cast<tia::half8_t*>(norm + int64_t(row) * hidden + 8 * gi) = o;
+      *reinterpret_cast<tia::half8_t*>(norm + (p32 ? tia::p32_off(row, 8 * gi) : int64_t(row) * hidden + 8 * gi)) = o;
     }
   }
 }
@@ -399,7 +401,8 @@ struct ti_llm_model {
       pack(head);
     }
 
-    const size_t rows = size_t(opt.max_batch) * opt.capacity;
+    // At least 32 rows: decode keeps activations P32 fragment-packed (32 x K).
+    const size_t rows = std::max<size_t>(size_t(opt.max_batch) * opt.capacity, 32);
     x = alloc<uint16_t>(rows * H);
     norm = alloc<uint16_t>(rows * H);
     qkv = alloc<uint16_t>(rows * 3 * H);
@@ -437,7 +440,7 @@ struct ti_llm_model {
 
   // ---------------------------------------------------------------- launch helpers
   void gemm(const uint16_t* a, int m, const Linear& w, tia::Epilogue epi, int* deferred = nullptr,
-            const uint16_t* ln_g = nullptr, const uint16_t* ln_b = nullptr) {
+            const uint16_t* ln_g = nullptr, const uint16_t* ln_b = nullptr, bool a_p32 = false) {
     tia::GemmArgs g;
     g.a = a;
     g.lda = w.k;
@@ -449,6 +452,7 @@ struct ti_llm_model {
     g.k = w.k;
     g.ldw = w.ldw;
     g.w_packed = w.packed;
+    g.a_p32 = a_p32;
     g.ln_gamma = ln_g;
     g.ln_beta = ln_b;
     g.ln_eps = 1e-5f;
@@ -475,8 +479,9 @@ struct ti_llm_model {
       ck(tia::layernorm_f16(x, g, beta, norm, rows, H, 1e-5f, stream));
   }
 
-  // x += a @ w + bias in the GEMM's epilogue (no LayerNorm after it).
-  void residual(const uint16_t* a, int rows, const Linear& w) {
+  // x += a @ w + bias in the GEMM's epilogue (no LayerNorm after it); a and x
+  // P32 fragment-packed or row-major.
+  void residual_add(const uint16_t* a, int rows, const Linear& w, bool p32) {
     tia::Epilogue r;
     r.kind = tia::EPI_RESIDUAL;
     r.bias = w.bias;
@@ -484,7 +489,8 @@ struct ti_llm_model {
     r.ldy = H;
     r.residual = x;
     r.ldr = H;
-    gemm(a, rows, w, r);
+    r.p32 = p32;
+    gemm(a, rows, w, r, nullptr, nullptr, nullptr, p32);
   }
 
   // Decode of up to 32 requests over packed weights: each LayerNorm runs in the
@@ -499,13 +505,21 @@ struct ti_llm_model {
            tia::gemm_ln_supported(b, H, H);
   }
 
+  bool norm_p32 = false;  // the last layers() pass left x and norm P32-packed
+
   // One pass of the transformer over rows [b, qlen] whose metadata is already on
-  // the device; leaves the residual stream in x and ln_f(x) of every row in norm.
+  // the device; leaves the residual stream in x and ln_f(x) of every row in norm
+  // (both P32 fragment-packed after an ln_fused pass, row-major otherwise).
   void layers(int b, int qlen) {
     const int rows = b * qlen;
     const bool fuse = ln_fused(b, qlen);
+    // Fragment-packed activations from two rows up: a single row reads one
+    // cache line per A fragment either way, and its row-major output writes
+    // are contiguous.
+    const bool p32 = fuse && rows > 1;
+    norm_p32 = p32;
     embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, ln1_g[0],
-                                                             ln1_b[0], x, norm, rows, qlen, H);
+                                                             ln1_b[0], x, norm, rows, qlen, H, p32);
     ck(hipGetLastError());
     for (int l = 0; l < L; ++l) {
       tia::Epilogue e;
@@ -528,7 +542,7 @@ struct ti_llm_model {
       // finishes q, k, v itself (one launch fewer per layer).
       int qkv_splits = 0;
       int* defer_qkv = qlen == 1 && c_attn[l].bias ? &qkv_splits : nullptr;
-      if (fuse) gemm(x, rows, c_attn[l], e, defer_qkv, ln1_g[l], ln1_b[l]);
+      if (fuse) gemm(x, rows, c_attn[l], e, defer_qkv, ln1_g[l], ln1_b[l], p32);
       else gemm(norm, rows, c_attn[l], e, defer_qkv);
 
       tia::AttnArgs at;
@@ -562,6 +576,7 @@ struct ti_llm_model {
       at.kv_len = opt.capacity;
       at.head_dim = kHeadDim;
       at.causal = true;
+      at.out_p32 = p32;
       ck(tia::attention(at, stream));
 
       tia::Epilogue gl;
@@ -570,8 +585,9 @@ struct ti_llm_model {
       gl.y = mlp;
       gl.ldy = 4 * H;
       if (fuse) {
-        residual(attn, rows, c_proj[l]);
-        gemm(x, rows, c_fc[l], gl, nullptr, ln2_g[l], ln2_b[l]);
+        gl.p32 = p32;
+        residual_add(attn, rows, c_proj[l], p32);
+        gemm(x, rows, c_fc[l], gl, nullptr, ln2_g[l], ln2_b[l], p32);
       } else {
         residual_ln(attn, rows, c_proj[l], ln2_g[l], ln2_b[l]);
         gemm(norm, rows, c_fc[l], gl);
@@ -581,10 +597,12 @@ struct ti_llm_model {
         residual_ln(mlp, rows, c_proj2[l], final_layer ? lnf_g : ln1_g[l + 1], final_layer ? lnf_b : ln1_b[l + 1]);
         continue;
       }
-      residual(mlp, rows, c_proj2[l]);
+      residual_add(mlp, rows, c_proj2[l], p32);
       // ln_f as its own row kernel: in the head GEMV's prologue every one of its
       // thousands of workgroups would normalize the same rows again.
-      if (final_layer) ck(tia::layernorm_f16(x, lnf_g, lnf_b, norm, rows, H, 1e-5f, stream));
+      if (final_layer)
+        ck(p32 ? tia::layernorm_f16_p32(x, lnf_g, lnf_b, norm, rows, H, 1e-5f, stream)
+               : tia::layernorm_f16(x, lnf_g, lnf_b, norm, rows, H, 1e-5f, stream));
     }
   }
 
@@ -601,7 +619,7 @@ struct ti_llm_model {
     e.kind = tia::EPI_F32;
     e.y = logits;
     e.ldy = head.ldw;
-    gemm(rows_in, b, head, e);
+    gemm(rows_in, b, head, e, nullptr, nullptr, nullptr, norm_p32 && qlen == 1);
     if (greedy) {
       argmax_kernel<<<b, 1024, 0, stream>>>(logits, d_next, V, head.ldw);
       ck(hipGetLastError());
@@ -741,7 +759,8 @@ struct ti_llm_model {
       e.kind = tia::EPI_F32;
       e.y = logits;
       e.ldy = head.ldw;
-      gemm(norm + int64_t(row) * H, rows, head, e);
+      // (a one-token pass leaves norm P32-packed: then q == 1 and row == 0)
+      gemm(norm_p32 ? norm : norm + int64_t(row) * H, rows, head, e, nullptr, nullptr, nullptr, norm_p32);
       ++trace.nll;
       nll_kernel<<<rows, 256, 0, stream>>>(logits, d_score_tokens, d_score_mask, d_loss, row + 1, V, head.ldw);
       ck(hipGetLastError());

@@ -69,20 +69,20 @@ __device__ __forceinline__ void store_vec(T* p, const float* v) {
 }
 
 // One wave per row; lane l owns elements [VPL*l + 64*VPL*i, +VPL) for i < NV.
-template <typename T, int VPL, int NV>
+// P32: x and y are fragment-packed decode matrices (common.hpp p32_off; VPL 8).
+template <typename T, int VPL, int NV, bool P32 = false>
 __global__ __launch_bounds__(256) void layernorm_wave(const T* x, const T* g, const T* b, T* y,
                                                       int rows, int cols, float eps) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const T* xr = x + int64_t(row) * cols;
-  T* yr = y + int64_t(row) * cols;
+  auto at = [&](int c) { return P32 ? p32_off(row, c) : int64_t(row) * cols + c; };
   float v[NV][VPL];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = VPL * lane + 64 * VPL * i;
-    if (c < cols) load_vec<T, VPL>(xr + c, v[i]);
+    if (c < cols) load_vec<T, VPL>(x + at(c), v[i]);
     else {
 #pragma unroll
       for (int e = 0; e < VPL; ++e) v[i][e] = 0.f;
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void layernorm_wave(const T* x, const T* g, co
       load_vec<T, VPL>(b + c, bv);
 #pragma unroll
       for (int e = 0; e < VPL; ++e) o[e] = (v[i][e] - mean) * inv * gv[e] + bv[e];
-      store_vec<T, VPL>(yr + c, o);
+      store_vec<T, VPL>(y + at(c), o);
     }
   }
 }
@@ -333,6 +333,19 @@ hipError_t softmax_dispatch(const T* x, T* y, int rows, int cols, hipStream_t st
 hipError_t layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
                          int rows, int cols, float eps, hipStream_t st) {
   return layernorm_dispatch<uint16_t>(x, g, b, y, rows, cols, eps, st);
+}
+hipError_t layernorm_f16_p32(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y, int rows,
+                             int cols, float eps, hipStream_t st) {
+  if (rows < 1 || rows > 32 || cols % 64 != 0 || cols > 2048 || !al16(x) || !al16(g) || !al16(b) || !al16(y))
+    return hipErrorInvalidValue;
+  const dim3 grid(unsigned((rows + 3) / 4)), block(256);
+#define TIA_LNP(NV) \
+  hipLaunchKernelGGL((layernorm_wave<uint16_t, 8, NV, true>), grid, block, 0, st, x, g, b, y, rows, cols, eps)
+  if (cols <= 512) TIA_LNP(1);
+  else if (cols <= 1024) TIA_LNP(2);
+  else TIA_LNP(4);
+#undef TIA_LNP
+  return hipGetLastError();
 }
 hipError_t softmax_f16(const uint16_t* x, uint16_t* y, int rows, int cols, hipStream_t st) {
   return softmax_dispatch<uint16_t>(x, y, rows, cols, st);
