@@ -496,12 +496,9 @@ struct ti_llm_model {
   // Decode of up to 32 requests over packed weights: each LayerNorm runs in the
   // prologue of the GEMV that consumes it (c_attn: ln_1, c_fc: ln_2, head: ln_f)
   // and each residual add in the epilogue of the GEMV that produces it.
-  // Up to hidden 1024 (16 K chunks, one round of 4 waves): at GPT-2 XL's 1600
-  // the prologue's per-workgroup LayerNorm and the unsplit c_proj launches
-  // measured slower than the split-K GEMVs and their reduce + residual + LN
-  // kernels.
+  // (hidden <= 2048: one round of at most 8 waves x 4 chunks covers K.)
   bool ln_fused(int b, int qlen) const {
-    return qlen == 1 && quantized && head.packed && c_attn[0].packed && H <= 1024 &&
+    return qlen == 1 && quantized && head.packed && c_attn[0].packed &&
            tia::gemm_ln_supported(b, H, H);
   }
 
@@ -521,6 +518,19 @@ struct ti_llm_model {
     embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, ln1_g[0],
                                                              ln1_b[0], x, norm, rows, qlen, H, p32);
     ck(hipGetLastError());
+    // The LayerNorm before c_attn / c_fc: in the GEMV's prologue up to hidden
+    // 1024; above, every one of the GEMV's workgroups normalising all rows
+    // costs more VALU time than one row-kernel launch into norm (measured at
+    // GPT-2 XL's 1600).  Layer 0's ln_1 is already in norm (embedding kernel).
+    const bool ln_prologue = H <= 1024;
+    auto ln_then_gemm = [&](const Linear& w, const tia::Epilogue& epi, int* defer, const uint16_t* g,
+                            const uint16_t* beta, bool in_norm) {
+      if (ln_prologue) return gemm(x, rows, w, epi, defer, g, beta, p32);
+      if (!in_norm)
+        ck(p32 ? tia::layernorm_f16_p32(x, g, beta, norm, rows, H, 1e-5f, stream)
+               : tia::layernorm_f16(x, g, beta, norm, rows, H, 1e-5f, stream));
+      gemm(norm, rows, w, epi, defer, nullptr, nullptr, p32);
+    };
     for (int l = 0; l < L; ++l) {
       tia::Epilogue e;
       e.kind = tia::EPI_QKV;
@@ -542,7 +552,7 @@ struct ti_llm_model {
       // finishes q, k, v itself (one launch fewer per layer).
       int qkv_splits = 0;
       int* defer_qkv = qlen == 1 && c_attn[l].bias ? &qkv_splits : nullptr;
-      if (fuse) gemm(x, rows, c_attn[l], e, defer_qkv, ln1_g[l], ln1_b[l], p32);
+      if (fuse) ln_then_gemm(c_attn[l], e, defer_qkv, ln1_g[l], ln1_b[l], l == 0);
       else gemm(norm, rows, c_attn[l], e, defer_qkv);
 
       tia::AttnArgs at;
@@ -587,7 +597,7 @@ struct ti_llm_model {
       if (fuse) {
         gl.p32 = p32;
         residual_add(attn, rows, c_proj[l], p32);
-        gemm(x, rows, c_fc[l], gl, nullptr, ln2_g[l], ln2_b[l], p32);
+        ln_then_gemm(c_fc[l], gl, nullptr, ln2_g[l], ln2_b[l], false);
       } else {
         residual_ln(attn, rows, c_proj[l], ln2_g[l], ln2_b[l]);
         gemm(norm, rows, c_fc[l], gl);
