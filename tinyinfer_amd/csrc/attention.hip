@@ -505,21 +505,24 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
   const AttnArgs& a = p.a;
   const dim3 blocks_per(1, unsigned(a.heads), unsigned(a.batch));
   if (a.q_len == 1) {
-    // Decode: one workgroup per (b, h) whose KW waves split the keys.  Aim for
-    // ~2048 waves in total (every workgroup resident at once: 4-wave groups fit
-    // three per CU), never more waves than 32/16-key tiles.
+    // Decode: one workgroup per (b, h) whose KW waves split the keys.  Each
+    // wave keeps at least 4 tiles of 32/16 keys (two double-buffered rounds;
+    // fewer make the LDS merge of the waves cost more than the parallelism
+    // gains), and at most ~4096 waves in total (timed on GPT-2 small, 96 keys:
+    // KW 1; GPT-2 XL, 640 keys and 800 heads: KW 4).
     const int tile_keys = D == 64 ? 32 : 16;
     const int tiles = (a.kv_len + tile_keys - 1) / tile_keys;
     const int64_t groups = int64_t(a.batch) * a.heads;
     int kw = 1;
-    while (kw < 16 && kw * 2 <= tiles && groups * kw * 2 <= 2048) kw *= 2;
+    while (kw < 8 && kw * 2 * 4 <= tiles && groups * kw * 2 <= 4096) kw *= 2;
     dim3 grid = blocks_per;
     grid.x = 1;
     if (p.parts) {
-      // Long caches: 4-wave workgroups over chunks of 2 * 4 tiles (all of a
-      // wave's loads in flight at once), spread over every CU, then a merge.
+      // Long caches: 2-wave workgroups over chunks of 2 * 2 tiles (all of a
+      // wave's loads in flight at once; 4- and 8-wave chunks of 256 / 512 keys
+      // measured slower on configs[3]), spread over every CU, then a merge.
       const dim3 split_grid(unsigned(a.heads), unsigned(a.batch), unsigned(p.chunks));
-      hipLaunchKernelGGL((attention_kernel<D, 1, 4, VEC, false, true>), split_grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((attention_kernel<D, 1, 2, VEC, false, true>), split_grid, dim3(128), 0, stream, p);
       if (p.chunks <= 8) hipLaunchKernelGGL((attention_combine_kernel<D, 8>), grid, dim3(64), 0, stream, p);
       else hipLaunchKernelGGL((attention_combine_kernel<D, 32>), grid, dim3(64), 0, stream, p);
       return hipGetLastError();
@@ -565,10 +568,10 @@ hipError_t attention(const AttnArgs& a, hipStream_t stream, const Scratch* scrat
     return hipErrorInvalidValue;
   AttnParams p{};
   p.a = a;
-  // Decode over a long cache (at least 4 chunks of 256/128 keys per (b, h)) and
+  // Decode over a long cache (at least 4 chunks of 128/64 keys per (b, h)) and
   // enough scratch for the chunk states: split the keys across workgroups.
   if (scratch && scratch->partials && a.q_len == 1 && !a.qkv_partials && (a.head_dim == 64 || a.head_dim == 128)) {
-    const int chunk = a.head_dim == 64 ? 256 : 128;
+    const int chunk = a.head_dim == 64 ? 128 : 64;  // 2 waves x 2 tiles
     const int chunks = (a.kv_len + chunk - 1) / chunk;
     const size_t need = size_t(a.batch) * a.heads * chunks * (2 + a.head_dim);
     if (chunks >= 4 && chunks <= 32 && need <= scratch->partial_floats) {

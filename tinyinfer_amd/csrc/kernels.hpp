@@ -137,9 +137,9 @@ struct AttnArgs {
   // fragment-packed (rows < 32, heads * head_dim % 64 == 0); o_* ignored.
   bool out_p32 = false;
 };
-// With a scratch, single-query attention over a long cache (kv_len >= 1024 for
-// head_dim 64, >= 512 for 128) splits the keys of each (b, h) across
-// workgroups and merges the chunk states in a second kernel.
+// With a scratch, single-query attention over a long cache (kv_len 512 ..
+// 4096 for head_dim 64, 256 .. 2048 for 128) splits the keys of each (b, h)
+// across workgroups and merges the chunk states in a second kernel.
 hipError_t attention(const AttnArgs& args, hipStream_t stream, const Scratch* scratch = nullptr);
 
 hipError_t layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
