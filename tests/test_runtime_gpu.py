@@ -167,10 +167,14 @@ def test_decode_b17_and_one_row_score_match_oracle(model, cpu_model):
         cpu_model.reset(s)
     _, nxt = cpu_model.forward(slots, prompts)
     step = [[int(t)] for t in nxt]
-    gpu = logits_of(model.forward(slots, step))
+    res = model.forward(slots, step)
+    gpu = logits_of(res)
     cpu, _ = cpu_model.forward(slots, step)
     print(f"b17 decode max |logit diff| {np.abs(gpu - cpu).max():.3g}")
     assert np.abs(gpu - cpu).max() <= 5e-2
+    # the device's greedy pick (the head's per-workgroup partials) is the
+    # lowest-index maximum of the logits it returned
+    assert res["next_tokens"] == np.argmax(gpu, axis=1).tolist()
     say("two-token score vs oracle")
     pair = ids[-2:]
     sc = model.score(pair, [0, 1], positions=True)

@@ -25,6 +25,7 @@
 // Dequantisation mirrors reference kernels/src/cuda/tc/gemm.cu:21,24 and the
 // bias epilogue mirrors gemm.cu:73-80 / :118-124; accumulation is fp32.
 #include <algorithm>
+#include <climits>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -633,6 +634,154 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Wide decode GEMV (the LM head): M <= 32 rows of P32 activations against many
+// 16-column blocks.  The whole A (KC <= 16 chunks) is copied to LDS once per
+// workgroup and each of its W >= 8 waves streams whole column blocks (every K
+// chunk of a block in one round of loads; the waves of a CU overlap each
+// other's rounds).  A wave owns its blocks over the full K, so the
+// accumulators go straight to the epilogue (no reduction across waves), which
+// also keeps each row's running argmax for greedy decoding.  The split-K GEMV
+// instead re-reads all of A for every one or two column blocks (1571
+// workgroups x 48 KiB for the 38.6 MB GPT-2 head at M = 32).
+struct WideParams {
+  const uint16_t* a;    // P32 fragment-packed [32][K]
+  const u32x4_t* w;     // panel-packed records
+  const float* scales;  // fp32 [N]
+  int m, n, nb, per;    // rows, columns, column blocks, blocks per workgroup
+  Epilogue epi;
+  float* amax_v;        // when set: per (workgroup, row) best logit and its column
+  int32_t* amax_i;
+};
+
+// Largest value, lowest index on ties; NaN never wins (reference
+// llm/src/runtime.cu:59-66).
+__device__ __forceinline__ void amax_merge(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+template <int MT, int KC, int W>
+__global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
+  __shared__ half8_t a_lds[KC * 256];  // P32 fragments ((c * 2 + t) * 2 + s) * 64 + lane
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const half8_t* asrc = reinterpret_cast<const half8_t*>(p.a);
+  static_assert((KC * 256) % (W * 64) == 0, "A copy must divide evenly");
+  static_assert(W >= 8, "the blocks of a wave are not overlapped: at least 8 waves per workgroup");
+  constexpr int kACopy = KC * 256 / (W * 64);
+  const int cb_first = blockIdx.x * p.per + wave, cb_end = min(p.nb, (blockIdx.x + 1) * p.per);
+  const int count = cb_first < cb_end ? (cb_end - cb_first + W - 1) / W : 0;  // this wave's blocks
+  const bool has_bias = p.epi.kind != EPI_RAW_F32 && p.epi.bias;
+  // Running argmax of this lane's column over its rows 16t + 4g + v (columns
+  // arrive in increasing order, so a tie keeps the first).
+  float bv[MT * 4];
+  int bi[MT * 4];
+#pragma unroll
+  for (int r = 0; r < MT * 4; ++r) {
+    bv[r] = -__builtin_huge_valf();
+    bi[r] = INT_MAX;
+  }
+  const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
+
+  struct Block {
+    u32x4_t w[KC];
+    float scale;
+    uint16_t bias;
+  };
+  auto load = [&](Block& b, int i) {
+    const int cb = min(cb_first + W * i, p.nb - 1), col = min(cb * 16 + j, p.n - 1);
+#pragma unroll
+    for (int c = 0; c < KC; ++c) b.w[c] = __builtin_nontemporal_load(p.w + (int64_t(cb) * KC + c) * 64 + lane);
+    b.scale = p.scales[col];
+    b.bias = bsrc[has_bias ? col : 0];
+  };
+  auto compute = [&](const Block& b, int i) {
+    float4_t acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const half8_t b0 = dequant8(b.w[c][0], b.w[c][1], b.scale);
+      const half8_t b1 = dequant8(b.w[c][2], b.w[c][3], b.scale);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * 2 + t) * 2) * 64 + lane], b0, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * 2 + t) * 2 + 1) * 64 + lane], b1, acc[t], 0, 0, 0);
+      }
+      // One chunk's LDS reads and dequantisation at a time (hoisting all of
+      // them would hold every A fragment of the block in registers).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // EPI_F32 (fp32 logits + bias), the only epilogue this kernel is launched with.
+    const int col = (cb_first + W * i) * 16 + j;
+    if (col >= p.n) return;
+    const float bias = has_bias ? h2f(b.bias) : 0.f;
+    float* y = static_cast<float*>(p.epi.y);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * t + 4 * g + v;
+        const float val = acc[t][v] + bias;
+        if (row < p.m) y[int64_t(row) * p.epi.ldy + col] = val;
+        amax_merge(bv[t * 4 + v], bi[t * 4 + v], val, col);
+      }
+  };
+  Block x;
+  {
+    // A into LDS, then the wave's blocks one at a time (enough waves per CU
+    // to overlap them; issuing the first blocks' weight loads ahead of the A
+    // copy measured slower).
+#pragma unroll
+    for (int i = 0; i < kACopy; ++i) a_lds[i * W * 64 + threadIdx.x] = asrc[i * W * 64 + threadIdx.x];
+    __syncthreads();
+    for (int i = 0; i < count; ++i) {
+      load(x, i);
+      compute(x, i);
+    }
+    if (!p.amax_v) return;
+    // Argmax partials: across the 16 column lanes of each row, then across the
+    // waves through LDS; one (value, column) per row per workgroup.
+    __shared__ float sv[W][32];
+    __shared__ int si[W][32];
+#pragma unroll
+    for (int r = 0; r < MT * 4; ++r) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1)
+        amax_merge(bv[r], bi[r], __shfl_xor(bv[r], o, 64), __shfl_xor(bi[r], o, 64));
+      if (j == 0) {
+        sv[wave][16 * (r >> 2) + 4 * g + (r & 3)] = bv[r];
+        si[wave][16 * (r >> 2) + 4 * g + (r & 3)] = bi[r];
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < 32 && int(threadIdx.x) < p.m) {
+      float v = sv[0][threadIdx.x];
+      int i = si[0][threadIdx.x];
+#pragma unroll
+      for (int w = 1; w < W; ++w) amax_merge(v, i, sv[w][threadIdx.x], si[w][threadIdx.x]);
+      p.amax_v[blockIdx.x * 32 + threadIdx.x] = v;
+      p.amax_i[blockIdx.x * 32 + threadIdx.x] = i;
+    }
+  }
+}
+
+// Greedy id of each row from the wide GEMV's per-workgroup partials: one wave
+// per row, lanes stride over the groups, same tie rule.
+__global__ __launch_bounds__(64) void argmax_partials_kernel(const float* vals, const int32_t* idx, int groups,
+                                                            int32_t* out) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  float v = -__builtin_huge_valf();
+  int i = INT_MAX;
+  for (int gi = lane; gi < groups; gi += 64) amax_merge(v, i, vals[gi * 32 + row], idx[gi * 32 + row]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) amax_merge(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
+  if (lane == 0) out[row] = i;
+}
+
+// ---------------------------------------------------------------------------
 // Multistage MFMA GEMM over panel-packed weights (prefill, M > 32)
 // ---------------------------------------------------------------------------
 // Tile BM x BN = (WM * MT * 16) x (WN * R * 16), 4 waves as WM x WN, K in chunks of
@@ -1104,6 +1253,25 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   if (ln) {
     p.ln_gamma = g.ln_gamma; p.ln_beta = g.ln_beta; p.ln_eps = g.ln_eps;
   }
+  if constexpr (MT == 2) {
+    // The LM head: whole column blocks per wave over an LDS copy of A.
+    if (g.a_p32 && !ln && !deferred && p.epi.kind == EPI_F32 && p.nb >= 1024 && (p.kc == 12 || p.kc == 16)) {
+      // 16 column blocks per workgroup of 8 waves (two per wave): timed
+      // against 8 / 16 / 32 blocks and 4 / 8 / 16 waves on the GPT-2 head.
+      WideParams wp{};
+      wp.a = g.a; wp.w = p.w; wp.scales = p.scales; wp.m = p.m; wp.n = p.n; wp.nb = p.nb; wp.epi = p.epi;
+      wp.per = 16;
+      const int grid = (p.nb + wp.per - 1) / wp.per;
+      if (g.amax_v && g.amax_i && g.amax_groups && size_t(grid) * 32 <= g.amax_capacity) {
+        wp.amax_v = g.amax_v;
+        wp.amax_i = g.amax_i;
+        *g.amax_groups = grid;
+      }
+      if (p.kc == 12) hipLaunchKernelGGL((gemv_wide_kernel<2, 12, 8>), dim3(unsigned(grid)), dim3(512), 0, stream, wp);
+      else hipLaunchKernelGGL((gemv_wide_kernel<2, 16, 8>), dim3(unsigned(grid)), dim3(512), 0, stream, wp);
+      return hipGetLastError();
+    }
+  }
   int splits = 1;
   if (deferred && !ln && s && s->partials) {
     const int groups = p.nb;
@@ -1200,6 +1368,7 @@ hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, hipStream_t str
 
 hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   if (deferred) *deferred = 0;
+  if (g.amax_groups) *g.amax_groups = 0;
   if (g.m <= 0 || g.n <= 0 || g.k <= 0) return hipErrorInvalidValue;
   const uintptr_t wp = reinterpret_cast<uintptr_t>(g.w), ap = reinterpret_cast<uintptr_t>(g.a);
   // Whole 4-column groups may be loaded when rows are 4-aligned and the row
@@ -1232,6 +1401,13 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   if (g.m <= 32) return g.w_int8 ? launch_skinny<true, 2>(g, wvec, avec, s, stream, deferred)
                                  : launch_skinny<false, 2>(g, wvec, avec, s, stream, deferred);
   return g.w_int8 ? launch_tiled<true>(g, wvec, avec, stream) : launch_tiled<false>(g, wvec, avec, stream);
+}
+
+hipError_t argmax_partials(const float* vals, const int32_t* idx, int groups, int rows, int32_t* out,
+                           hipStream_t stream) {
+  if (rows < 1 || rows > 32 || groups < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(argmax_partials_kernel, dim3(unsigned(rows)), dim3(64), 0, stream, vals, idx, groups, out);
+  return hipGetLastError();
 }
 
 bool gemm_ln_supported(int m, int k, int n) {

@@ -61,6 +61,14 @@ struct GemmArgs {
   const void* w_packed = nullptr;
   // A is P32 fragment-packed (M <= 32, packed W; lda ignored).
   bool a_p32 = false;
+  // Optional greedy partials (EPI_F32 logits): when the wide LM-head GEMV runs
+  // it also writes each workgroup's best (value, column) per row to
+  // amax_v/amax_i[group * 32 + row] (capacity entries) and sets *amax_groups;
+  // otherwise *amax_groups = 0.  argmax_partials finishes them.
+  float* amax_v = nullptr;
+  int32_t* amax_i = nullptr;
+  size_t amax_capacity = 0;
+  int* amax_groups = nullptr;
   // Optional LayerNorm of the A rows (packed int8 W, M <= 32, gemm_ln_supported):
   // the GEMM multiplies fp16_rn((a - mean) * rsqrt(var + eps) * gamma + beta),
   // mean and var over the K columns of each row, as layernorm_f16 computes them.
@@ -69,6 +77,10 @@ struct GemmArgs {
   float ln_eps = 1e-5f;
   Epilogue epi;
 };
+// out[row] = the column of the largest value over the groups' partials (lowest
+// column on ties, NaN never wins), rows <= 32.
+hipError_t argmax_partials(const float* vals, const int32_t* idx, int groups, int rows, int32_t* out,
+                           hipStream_t stream);
 // Largest K / 64 a LayerNorm-prologue GEMM takes (one round of 8 waves x 4 chunks).
 constexpr int kLnMaxChunks = 32;
 bool gemm_ln_supported(int m, int k, int n);

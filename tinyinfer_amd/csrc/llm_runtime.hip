@@ -266,6 +266,10 @@ struct ti_llm_model {
   float* logits = nullptr;
   int32_t *d_meta = nullptr, *d_ids = nullptr, *d_slots = nullptr, *d_qlens = nullptr, *d_offsets = nullptr;
   int32_t *d_next = nullptr, *d_score_tokens = nullptr;
+  // Greedy partials of the wide head GEMV: [group][32] (value, column).
+  static constexpr size_t kAmaxEntries = size_t(4096) * 32;
+  float* d_amax_v = nullptr;
+  int32_t* d_amax_i = nullptr;
   uint8_t* d_score_mask = nullptr;
   double *d_loss = nullptr, *d_loss_sum = nullptr;
   int32_t *h_meta = nullptr, *h_ids = nullptr, *h_slots = nullptr, *h_qlens = nullptr, *h_offsets = nullptr;
@@ -421,6 +425,8 @@ struct ti_llm_model {
     d_qlens = d_slots + opt.max_batch;
     d_offsets = d_qlens + opt.max_batch;
     d_next = alloc<int32_t>(opt.max_batch);
+    d_amax_v = alloc<float>(kAmaxEntries);
+    d_amax_i = alloc<int32_t>(kAmaxEntries);
     d_score_tokens = alloc<int32_t>(opt.capacity);
     d_score_mask = alloc<uint8_t>(opt.capacity);
     d_loss = alloc<double>(opt.capacity);
@@ -440,7 +446,8 @@ struct ti_llm_model {
 
   // ---------------------------------------------------------------- launch helpers
   void gemm(const uint16_t* a, int m, const Linear& w, tia::Epilogue epi, int* deferred = nullptr,
-            const uint16_t* ln_g = nullptr, const uint16_t* ln_b = nullptr, bool a_p32 = false) {
+            const uint16_t* ln_g = nullptr, const uint16_t* ln_b = nullptr, bool a_p32 = false,
+            int* amax_groups = nullptr) {
     tia::GemmArgs g;
     g.a = a;
     g.lda = w.k;
@@ -453,6 +460,12 @@ struct ti_llm_model {
     g.ldw = w.ldw;
     g.w_packed = w.packed;
     g.a_p32 = a_p32;
+    if (amax_groups) {
+      g.amax_v = d_amax_v;
+      g.amax_i = d_amax_i;
+      g.amax_capacity = kAmaxEntries;
+      g.amax_groups = amax_groups;
+    }
     g.ln_gamma = ln_g;
     g.ln_beta = ln_b;
     g.ln_eps = 1e-5f;
@@ -629,8 +642,13 @@ struct ti_llm_model {
     e.kind = tia::EPI_F32;
     e.y = logits;
     e.ldy = head.ldw;
-    gemm(rows_in, b, head, e, nullptr, nullptr, nullptr, norm_p32 && qlen == 1);
-    if (greedy) {
+    // The wide head GEMV leaves per-workgroup argmax partials: then a small
+    // finishing kernel replaces the pass over all logits.
+    int groups = 0;
+    gemm(rows_in, b, head, e, nullptr, nullptr, nullptr, norm_p32 && qlen == 1, greedy ? &groups : nullptr);
+    if (greedy && groups > 0) {
+      ck(tia::argmax_partials(d_amax_v, d_amax_i, groups, b, d_next, stream));
+    } else if (greedy) {
       argmax_kernel<<<b, 1024, 0, stream>>>(logits, d_next, V, head.ldw);
       ck(hipGetLastError());
     }
