@@ -153,6 +153,10 @@ def _lib():
     lib.ti_amd_pack_w8.argtypes = [v, i, i, v, C.c_size_t, i]
     lib.ti_amd_packed_w8_bytes.restype = C.c_int64
     lib.ti_amd_packed_w8_bytes.argtypes = [i, i]
+    lib.ti_amd_packed_w16_bytes.restype = C.c_int64
+    lib.ti_amd_packed_w16_bytes.argtypes = [i, i]
+    lib.ti_amd_pack_w16.argtypes = [v, v, i, i, v, C.c_size_t, i]
+    lib.ti_amd_gemm_w16p_fused.argtypes = [v] * 5 + [i] * 4 + [C.c_size_t, i]
     lib.ti_amd_layernorm_f32.argtypes = [v, v, v, v, i, i, C.c_float, C.c_size_t, i]
     lib.ti_amd_softmax_f32.argtypes = [v, v, i, i, C.c_size_t, i]
     return ops, lib
@@ -165,8 +169,10 @@ def _check(lib, st):
 
 def run_gemm(rp, shapes, packed=False):
     """W8A16 linear with fused bias+GELU over rotating weight sets: row-major int8
-    weights through ti_amd_gemm_i8_fused, or (packed=True) the runtime's decode
-    layout through ti_amd_gemm_w8p_fused (weights packed once, outside the timing)."""
+    weights through ti_amd_gemm_i8_fused, (packed=True) the runtime's decode
+    layout through ti_amd_gemm_w8p_fused, or (packed="w16") the runtime's
+    pre-dequantised fp16 prefill layout through ti_amd_gemm_w16p_fused (weights
+    packed once, outside the timing)."""
     import torch
     ops, lib = _lib()
     dev = torch.device("cuda:0")
@@ -174,7 +180,9 @@ def run_gemm(rp, shapes, packed=False):
     g.manual_seed(20261101)
     out = {}
     for (m, k, n) in shapes:
-        wbytes = int(lib.ti_amd_packed_w8_bytes(k, n)) if packed else k * n
+        w16 = packed == "w16"
+        wbytes = (int(lib.ti_amd_packed_w16_bytes(k, n)) if w16 else
+                  int(lib.ti_amd_packed_w8_bytes(k, n)) if packed else k * n)
         nsets = max(1, ROTATE_BYTES // wbytes)
         q = torch.randint(-127, 128, (nsets, k * n), dtype=torch.int8, device=dev, generator=g)
         scales = (torch.rand((nsets, n), device=dev, generator=g) * 9e-3 + 1e-3).half().float()
@@ -184,14 +192,19 @@ def run_gemm(rp, shapes, packed=False):
         if packed:
             w = torch.empty((nsets, wbytes), dtype=torch.uint8, device=dev)
             for i in range(nsets):
-                _check(lib, lib.ti_amd_pack_w8(q[i].data_ptr(), k, n, w[i].data_ptr(),
-                                               torch.cuda.current_stream().cuda_stream, 0))
+                cs = torch.cuda.current_stream().cuda_stream
+                _check(lib, lib.ti_amd_pack_w16(q[i].data_ptr(), scales[i].data_ptr(), k, n, w[i].data_ptr(), cs, 0)
+                       if w16 else lib.ti_amd_pack_w8(q[i].data_ptr(), k, n, w[i].data_ptr(), cs, 0))
             torch.cuda.synchronize()
             del q
             q = w
         entry = lib.ti_amd_gemm_w8p_fused if packed else lib.ti_amd_gemm_i8_fused
 
         def launch(i):
+            if w16:
+                return lambda: _check(lib, lib.ti_amd_gemm_w16p_fused(
+                    a.data_ptr(), q[i].data_ptr(), bias[i].data_ptr(), y.data_ptr(), None,
+                    m, n, k, 1, rp.stream.cuda_stream, 0))
             return lambda: _check(lib, entry(
                 a.data_ptr(), q[i].data_ptr(), scales[i].data_ptr(), bias[i].data_ptr(), y.data_ptr(), None,
                 m, n, k, 1, rp.stream.cuda_stream, 0))
@@ -487,6 +500,7 @@ def main():
     if args.part in ("all", "kernels"):
         prefill = ((64, 768, 3072), (64, 3072, 768), (512, 768, 3072), (512, 3072, 768))
         line["kernels"] = {"gemm_prefill": run_gemm(rp, prefill, packed=True),
+                           "gemm_prefill_f16_packed": run_gemm(rp, prefill, packed="w16"),
                            "gemm_prefill_row_major_abi": run_gemm(rp, prefill),
                            "rowops_f32": run_rowops(rp), "decode_attention": run_decode_attention(rp),
                            "prefill_attention": run_prefill_attention(rp)}

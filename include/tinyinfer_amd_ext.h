@@ -39,6 +39,23 @@ int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, const float* sc
                           const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m, int n,
                           int k, int epilogue, uintptr_t stream, int device);
 
+/* Pre-dequantised fp16 weights for the prefill GEMM (M > 32): every weight
+ * fp16_rn(float(q[k,n]) * scales[n]) -- the values the int8 kernels compute on
+ * the fly (reference kernels/src/cuda/tc/gemm.cu:21,24) -- stored once, so the
+ * GEMM is a plain fp16 MFMA GEMM.  Layout: for column block cb (16 columns) and
+ * K group kk (32 rows), 1 KiB at (cb * ceil(K/32) + kk) * 1024 bytes, lane l's
+ * 16 bytes = column cb*16 + (l & 15), rows kk*32 + 8*(l >> 4) + 0..7; zero past
+ * K/N.  ti_amd_packed_w16_bytes: its size; ti_amd_pack_w16: device q int8 [K,N]
+ * + scales fp32 [N] -> packed; ti_amd_gemm_w16p_fused: Y = epilogue(A @ W +
+ * bias) with the epilogues of ti_amd_gemm_i8_fused, M > 32, K % 32 == 0, A and
+ * packed 16-byte aligned. */
+int64_t ti_amd_packed_w16_bytes(int k, int n);
+int ti_amd_pack_w16(const int8_t* q, const float* scales, int k, int n, void* packed, uintptr_t stream,
+                    int device);
+int ti_amd_gemm_w16p_fused(const uint16_t* a, const void* packed16, const uint16_t* bias, uint16_t* y,
+                           const uint16_t* residual, int m, int n, int k, int epilogue, uintptr_t stream,
+                           int device);
+
 /* ti_amd_gemm_w8p_ln_fused: the decode GEMV with the LayerNorm that precedes
  * every GPT-2 linear fed from the residual stream (reference
  * llm/src/runtime.cu:143 ln_1 -> c_attn, :150 ln_2 -> c_fc) computed in its

@@ -252,6 +252,78 @@ def test_packed_prefill_gemm_against_oracle(ops, m, k, n):
     close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, gelu=True)))
 
 
+def _pack16_gpu(lib, q_dev, s_dev, k, n):
+    t = torch()
+    lib.ti_amd_packed_w16_bytes.restype = C.c_int64
+    lib.ti_amd_packed_w16_bytes.argtypes = [C.c_int, C.c_int]
+    lib.ti_amd_pack_w16.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_size_t, C.c_int]
+    out = t.empty(lib.ti_amd_packed_w16_bytes(k, n), dtype=t.uint8, device="cuda")
+    st = lib.ti_amd_pack_w16(q_dev.data_ptr(), s_dev.data_ptr(), k, n, out.data_ptr(),
+                             t.cuda.current_stream().cuda_stream, 0)
+    assert st == 0, lib.ti_v2_last_error()
+    return out
+
+
+def _w16(lib, a, packed, bias, y, res, m, n, k, epi):
+    t = torch()
+    fn = lib.ti_amd_gemm_w16p_fused
+    fn.argtypes = [C.c_void_p] * 5 + [C.c_int] * 4 + [C.c_size_t, C.c_int]
+    ptr = lambda x: None if x is None else x.data_ptr()
+    return fn(ptr(a), ptr(packed), ptr(bias), ptr(y), ptr(res), m, n, k, epi, t.cuda.current_stream().cuda_stream, 0)
+
+
+@pytest.mark.parametrize("k,n", [(768, 3072), (200, 40), (1600, 48)])
+def test_pack_w16_layout_bit_exact(ops, k, n):
+    """The device dequantise-and-pack writes exactly the numpy restatement (the
+    int8 kernels' fp16_rn(float(q) * scale) values in MFMA B order)."""
+    from tests.test_packed_layout import pack_w16_numpy
+    rng = np.random.default_rng(k + 3 * n)
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    say("pack_w16", k, n)
+    got = host(_pack16_gpu(ops.lib, dev(q), dev(s), k, n)).view(np.uint16)
+    assert np.array_equal(got, pack_w16_numpy(q, s).view(np.uint16))
+
+
+@pytest.mark.parametrize("m,k,n", [(33, 768, 3072), (64, 3072, 768), (130, 128, 100), (512, 64, 2000),
+                                   (512, 768, 3072), (1024, 768, 2304), (2048, 3072, 768), (4100, 1600, 6400),
+                                   (70, 224, 40)])
+def test_f16_packed_prefill_gemm_against_oracle(ops, m, k, n):
+    """Prefill GEMM over the pre-dequantised fp16 weights: ragged row and column
+    tiles, K a multiple of 32 but not of 64, bias / bias+GELU / in-place residual epilogues against the
+    oracle's int8 linear (the same weight values)."""
+    t = torch()
+    rng = np.random.default_rng(13 * m + k + n)
+    a = f16(rng.standard_normal((m, k)))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("f16-packed prefill gemm", m, k, n)
+    packed = _pack16_gpu(ops.lib, dev(q), dev(s), k, n)
+    ad, bd = dev(a, t.float16), dev(bias, t.float16)
+    y = t.empty((m, n), dtype=t.float16, device="cuda")
+    assert _w16(ops.lib, ad, packed, bd, y, None, m, n, k, 0) == 0, ops.lib.ti_v2_last_error()
+    ref = oracle.linear(a, q=q, scales=s, bias_bits=bias)
+    close(h(hbits(y)), h(ref))
+    assert _w16(ops.lib, ad, packed, None, y, None, m, n, k, 1) == 0
+    close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, gelu=True)))
+    res = dev(f16(rng.standard_normal((m, n))), t.float16)
+    expect = (h(hbits(res)) + h(ref)).astype(np.float16).astype(np.float64)
+    assert _w16(ops.lib, ad, packed, bd, res, res, m, n, k, 2) == 0
+    close(h(hbits(res)), expect)
+
+
+def test_f16_packed_gemm_rejects_unsupported_shapes(ops):
+    t = torch()
+    a = t.zeros((64, 96), dtype=t.float16, device="cuda")
+    packed = t.zeros(1 << 16, dtype=t.uint8, device="cuda")
+    y = t.empty((64, 16), dtype=t.float16, device="cuda")
+    say("f16-packed gemm invalid")
+    assert _w16(ops.lib, a, packed, None, y, None, 64, 16, 80, 0) == 1   # K % 32 != 0
+    assert _w16(ops.lib, a, packed, None, y, None, 32, 16, 96, 0) == 1   # M <= 32: the decode GEMV's shapes
+    assert _w16(ops.lib, a, packed, None, y, None, 64, 16, 96, 3) == 1   # unknown epilogue
+
+
 def test_packed_gemv_rejects_unsupported_shapes(ops):
     t = torch()
     a = t.zeros((33, 64), dtype=t.float16, device="cuda")

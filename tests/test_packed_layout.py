@@ -26,6 +26,44 @@ def pack_w8_numpy(q):
     return np.ascontiguousarray(t).reshape(-1)
 
 
+def pack_w16_numpy(q, scales):
+    """q int8 [K, N], scales fp32 [N] -> fp16 records [ceil(N/16) * ceil(K/32) * 512]
+    of fp16_rn(float32(q) * scale) (the dequantisation of reference
+    kernels/src/cuda/tc/gemm.cu:21,24: an fp32 product, then fp16 rounding)."""
+    k, n = q.shape
+    kk, nb = -(-k // 32), -(-n // 16)
+    deq = (q.astype(np.float32) * scales.astype(np.float32)[None, :]).astype(np.float16)
+    dp = np.zeros((kk * 32, nb * 16), np.float16)
+    dp[:k, :n] = deq
+    # row = kk*32 + g*8 + r, col = cb*16 + j  ->  [cb][kk][g][j][r]
+    t = dp.reshape(kk, 4, 8, nb, 16).transpose(3, 0, 1, 4, 2)
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+def pack_w16_loops(q, scales):
+    k, n = q.shape
+    kk, nb = -(-k // 32), -(-n // 16)
+    out = np.zeros(nb * kk * 512, np.float16)
+    for cb in range(nb):
+        for c in range(kk):
+            for lane in range(64):
+                col, g = cb * 16 + (lane & 15), lane >> 4
+                for r in range(8):
+                    row = c * 32 + 8 * g + r
+                    if row < k and col < n:
+                        out[(cb * kk + c) * 512 + lane * 8 + r] = np.float16(np.float32(q[row, col]) *
+                                                                           np.float32(scales[col]))
+    return out
+
+
+def test_pack_w16_numpy_matches_loop_definition():
+    rng = np.random.default_rng(4)
+    for k, n in ((64, 16), (100, 40), (40, 33)):
+        q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+        s = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        assert np.array_equal(pack_w16_numpy(q, s).view(np.uint16), pack_w16_loops(q, s).view(np.uint16))
+
+
 def pack_w8_loops(q):
     k, n = q.shape
     kc, nb = -(-k // 64), -(-n // 16)

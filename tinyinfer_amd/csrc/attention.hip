@@ -111,7 +111,7 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
         skv[0] += ps[a.hidden];
         svv[0] += ps[2 * a.hidden];
       }
-      sq[lane] = f16(((sqv[0] + sqv[1]) + (sqv[2] + sqv[3])) + bqv);
+      sq[lane] = f16r(((sqv[0] + sqv[1]) + (sqv[2] + sqv[3])) + bqv);
       const int64_t pos = a.offsets[b];
       const int64_t at = slot * a.kv_sb + int64_t(h) * a.kv_sh + pos * D + lane;
       const_cast<uint16_t*>(a.k)[at] = f2h(((skv[0] + skv[1]) + (skv[2] + skv[3])) + bkv);
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
                                     : int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(qi) * a.o_sq + 8 * ds);
   half8_t o;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = f16(l > 0.f ? acc[e] * inv : 0.f);
+  for (int e = 0; e < 8; ++e) o[e] = f16r(l > 0.f ? acc[e] * inv : 0.f);
   if constexpr (VEC) *reinterpret_cast<half8_t*>(op) = o;
   else {
 #pragma unroll
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float pr = __builtin_amdgcn_exp2f(sc[kb][v] - base);
-          pt[kb][v] = f16(pr);
+          pt[kb][v] = f16r(pr);
           psum += pr;
         }
       psum += __shfl_xor(psum, 16, 64);
@@ -495,7 +495,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
   for (int d = 0; d < D / 16; ++d) {
     half4_t o;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) o[v] = f16(l > 0.f ? acc[d][v] * inv : 0.f);
+    for (int v = 0; v < 4; ++v) o[v] = f16r(l > 0.f ? acc[d][v] * inv : 0.f);
     *reinterpret_cast<half4_t*>(op + 16 * d + 4 * g) = o;
   }
 }

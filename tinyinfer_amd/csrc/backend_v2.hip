@@ -274,6 +274,52 @@ extern "C" int ti_amd_pack_w8(const int8_t* q, int k, int n, void* packed, uintp
   return hip_status(tia::pack_w8(q, n, k, n, packed, reinterpret_cast<hipStream_t>(stream)));
 }
 
+extern "C" int64_t ti_amd_packed_w16_bytes(int k, int n) {
+  if (!shape_fits({k, n}, 2)) return 0;
+  return int64_t(tia::packed_w16_bytes(k, n));
+}
+
+extern "C" int ti_amd_pack_w16(const int8_t* q, const float* scales, int k, int n, void* packed, uintptr_t stream,
+                               int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (!q || !aligned(scales, 4) || !aligned(packed, 16) || !shape_fits({k, n}, 2))
+    return fail(TI_V2_INVALID_ARGUMENT, "pack_w16 needs int8 q[K,N], fp32 scales[N] and a 16-byte aligned output");
+  return hip_status(tia::pack_w16(q, n, scales, k, n, packed, reinterpret_cast<hipStream_t>(stream)));
+}
+
+extern "C" int ti_amd_gemm_w16p_fused(const uint16_t* a, const void* packed16, const uint16_t* bias, uint16_t* y,
+                                      const uint16_t* residual, int m, int n, int k, int epilogue, uintptr_t stream,
+                                      int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (m <= 32 || !aligned(a, 16) || !aligned(packed16, 16) || !aligned(y, 2) || (bias && !aligned(bias, 2)) ||
+      k % 32 != 0 || !shape_fits({m, k}, 2) || !shape_fits({m, n}, 2) || !shape_fits({k, n}, 2))
+    return fail(TI_V2_INVALID_ARGUMENT,
+                "fp16-packed GEMM needs M > 32, K % 32 == 0 and 16-byte aligned A and packed weights");
+  if (epilogue < 0 || epilogue > 2 || (epilogue == 2 && !aligned(residual, 2)))
+    return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err = hipSuccess;
+  const tia::Scratch* scratch = tia::library_scratch(device, st, &err);
+  if (!scratch) return hip_status(err);
+  tia::GemmArgs g;
+  g.a = a;
+  g.lda = k;
+  g.w_f16p = packed16;
+  g.w_int8 = true;
+  g.m = m;
+  g.n = n;
+  g.k = k;
+  g.epi.kind = epilogue == 1 ? tia::EPI_GELU : (epilogue == 2 ? tia::EPI_RESIDUAL : tia::EPI_F16);
+  g.epi.bias = bias;
+  g.epi.y = y;
+  g.epi.ldy = n;
+  g.epi.residual = residual;
+  g.epi.ldr = n;
+  return hip_status(tia::gemm(g, scratch, st));
+}
+
 extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, const float* scales,
                                      const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m,
                                      int n, int k, int epilogue, uintptr_t stream, int device) {

@@ -26,11 +26,21 @@ __host__ __device__ __forceinline__ int64_t p32_off(int m, int k) {
          (k & 7);
 }
 
-// fp16 bits <-> fp32.  The conversion to fp16 is v_cvt_f16_f32, which rounds to
-// nearest-even under the default wave mode register.
+// fp16_rn of an fp32 value: the value is first rounded to fp32 as its own
+// step.  Without the opaque copy the compiler may fuse the operation that
+// produced it (a multiply, add or fma) with the conversion into one
+// mixed-precision fma that rounds the exact result straight to fp16 -- one
+// rounding where the reference's fp32 arithmetic followed by __float2half_rn
+// has two, so 1-ulp differences in rare cases.  The conversion itself is
+// v_cvt_f16_f32 (nearest-even under the default mode register).
+__device__ __forceinline__ f16 f16r(float v) {
+  asm volatile("" : "+v"(v));
+  return f16(v);
+}
+// fp16 bits <-> fp32.
 __device__ __forceinline__ float h2f(uint16_t bits) { return float(__builtin_bit_cast(f16, bits)); }
-__device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, f16(v)); }
-__device__ __forceinline__ float rt16(float v) { return float(f16(v)); }
+__device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, f16r(v)); }
+__device__ __forceinline__ float rt16(float v) { return float(f16r(v)); }
 
 // tanh-approximated GELU (GPT-2 "gelu_new"): 0.5 z (1 + tanh(sqrt(2/pi) (z + 0.044715 z^3))).
 // tanhf is ROCm's device libm.

@@ -179,7 +179,7 @@ __device__ __forceinline__ half8_t bfrag(const WFrag<INT8>& f, int c, float scal
   for (int r = 0; r < 8; ++r) {
     if constexpr (INT8) {
       const int8_t q = int8_t(f.d[r] >> (8 * c));
-      out[r] = f16(float(q) * scale);  // fp16_rn(float(q) * scale[n])
+      out[r] = f16r(float(q) * scale);  // fp16_rn(float(q) * scale[n])
     } else {
       const uint32_t word = f.d[2 * r + (c >> 1)];
       out[r] = __builtin_bit_cast(f16, uint16_t(word >> (16 * (c & 1))));
@@ -368,9 +368,9 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scale) {
   half8_t out;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) out[r] = f16(float(int8_t(lo >> (8 * r))) * scale);
+  for (int r = 0; r < 4; ++r) out[r] = f16r(float(int8_t(lo >> (8 * r))) * scale);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) out[4 + r] = f16(float(int8_t(hi >> (8 * r))) * scale);
+  for (int r = 0; r < 4; ++r) out[4 + r] = f16r(float(int8_t(hi >> (8 * r))) * scale);
   return out;
 }
 
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
             for (int e = 0; e < 8; ++e)
               af[i][s][t][e] =
-                  f16(fmaf(fmaf(float(af[i][s][t][e]), inv[t], shift[t]), float(gam[e]), float(bet[e])));
+                  f16r(fmaf(fmaf(float(af[i][s][t][e]), inv[t], shift[t]), float(gam[e]), float(bet[e])));
         }
       // Keep the weight dequantization (which waits for the records) after the
       // LayerNorm.
@@ -1012,7 +1012,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
           }
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) wreg[r][c] = f16(float(q[c]) * sc[c]);
+        for (int c = 0; c < 4; ++c) wreg[r][c] = f16r(float(q[c]) * sc[c]);
       } else {
         const uint16_t* wp = static_cast<const uint16_t*>(p.w);
         uint16_t h[4] = {0, 0, 0, 0};
@@ -1348,6 +1348,208 @@ hipError_t launch_panel(const GemmArgs& g, const Scratch* s, hipStream_t stream,
   return launch_panel_cfg<1, 4, 4, 1, 4>(g, s, stream, deferred);
 }
 
+// ---------------------------------------------------------------------------
+// Prefill GEMM over pre-dequantised fp16 weights (M > 32)
+// ---------------------------------------------------------------------------
+// With the weights dequantised once at load (fp16_rn(float(q) * scale), the
+// same values the int8 kernels compute on the fly) the prefill GEMM is a plain
+// fp16 MFMA GEMM: no dequantisation VALU per row tile, so each wave can own a
+// 64 x 64 output tile (16 accumulators of v_mfma_f32_16x16x32_f16), which cuts
+// the LDS bytes per MFMA to a quarter of the int8 panel kernel's.  fp16 B
+// records: (column block cb, K group kk of 32) is 1 KiB at (cb * KK + kk) *
+// 1024 bytes, lane l holding column cb * 16 + (l & 15), rows kk * 32 + 8 (l >> 4)
+// + 0..7 (the MFMA B operand); zero past K and N.
+struct F16GemmParams {
+  const uint16_t* a;
+  int64_t lda;
+  const u32x4_t* w;  // fp16 B records
+  int m, n, k;
+  int kk;            // K groups of 32
+  int tiles_n, tiles;
+  int chunks_per_split, splits;
+  bool defer;
+  Epilogue epi;
+  float* partials;
+};
+
+__global__ void pack_w16_kernel(const int8_t* q, int64_t ldq, const float* scales, int k, int n, int kk,
+                                int64_t records, u32x4_t* out) {
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= records * 64) return;
+  const int64_t rec = t >> 6;
+  const int lane = int(t & 63);
+  const int cb = int(rec / kk), g = int(rec % kk);
+  const int col = cb * 16 + (lane & 15), r0 = g * 32 + 8 * (lane >> 4);
+  half8_t v;
+  const float sc = col < n ? scales[col] : 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int row = r0 + e;
+    v[e] = (row < k && col < n) ? f16r(float(q[int64_t(row) * ldq + col]) * sc) : f16(0.f);
+  }
+  out[t] = __builtin_bit_cast(u32x4_t, v);
+}
+
+// Tile (2 * MT * 16) x (2 * R * 16), 4 waves as 2 x 2, each MT x R MFMA blocks;
+// K in chunks of 32 moved HBM/L2 -> LDS by global_load_lds_dwordx4 (A
+// fragments of 16 rows x 32 K in MFMA A order, B records as stored), S stages
+// as in the int8 panel kernel.  The epilogue runs from the accumulators.
+template <int MT, int R, int S>
+__global__ __launch_bounds__(256, 2) void f16_gemm_kernel(F16GemmParams p) {
+  constexpr int BM = 2 * MT * 16, BN = 2 * R * 16;
+  constexpr int NA = BM / 16, NB = BN / 16, NL = NA + NB;
+  static_assert(NL % 4 == 0, "loads must split evenly over the waves");
+  constexpr int LPW = NL / 4;
+  constexpr int STAGE = NL * 1024;
+  static_assert(S >= 3 && (S - 2) * LPW < 64, "in-flight loads within vmcnt");
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];  // max(S * STAGE, epilogue tile)
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nbk = gridDim.x, bid = blockIdx.x;
+  const int logical = (nbk % 8 == 0) ? (bid % 8) * (nbk / 8) + bid / 8 : bid;
+  const int tile = logical % p.tiles, split = logical / p.tiles;
+  const int tn = tile % p.tiles_n, tm = tile / p.tiles_n;
+  const int m0 = tm * BM, cb0 = tn * NB;
+  const int nbt = (p.n + 15) / 16;
+  const int c_begin = split * p.chunks_per_split;
+  const int kc = min(p.kk - c_begin, p.chunks_per_split);  // chunks of this split (>= 1)
+
+  // Load id < NA: A fragment t (rows m0 + 16t .. +15, clamped), lane (j, g) at
+  // k = 32c + 8g; otherwise B record cb0 + id - NA (clamped).
+  const char* src[LPW];
+  int stride[LPW];
+#pragma unroll
+  for (int l = 0; l < LPW; ++l) {
+    const int id = wave * LPW + l;
+    if (id < NA) {
+      const int row = min(m0 + 16 * id + j, p.m - 1);
+      src[l] = reinterpret_cast<const char*>(p.a + int64_t(row) * p.lda + 32 * c_begin + 8 * g);
+      stride[l] = 64;
+    } else {
+      const int cb = min(cb0 + id - NA, nbt - 1);
+      src[l] = reinterpret_cast<const char*>(p.w + (int64_t(cb) * p.kk + c_begin) * 64 + lane);
+      stride[l] = 1024;
+    }
+  }
+  auto issue = [&](int chunk, int stage) {
+#pragma unroll
+    for (int l = 0; l < LPW; ++l)
+      __builtin_amdgcn_global_load_lds((global_ptr)(src[l] + int64_t(chunk) * stride[l]),
+                                       (lds_ptr)(lds + stage * STAGE + (wave * LPW + l) * 1024), 16, 0, 0);
+  };
+  // The epilogue gives thread t the outputs of tile column t % BN: its bias is
+  // loaded now and used after the loop (a null bias reads A's first element).
+  static_assert(256 % BN == 0 || BN % 256 == 0, "epilogue column mapping");
+  const bool epi_now = p.splits == 1 && !p.defer;
+  const bool has_bias = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias;
+  const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
+  const int my_col = cb0 * 16 + int(threadIdx.x % BN);
+  const uint16_t braw = bsrc[has_bias ? min(my_col, p.n - 1) : 0];
+
+  float4_t acc[MT][R];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[t][r] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int c = 0; c < S - 1; ++c) issue(min(c, kc - 1), c);
+  for (int c = 0; c < kc; ++c) {
+    wait_chunk<LPW, 0, S - 2>(min(c + S - 2, kc - 1) - c);
+    __builtin_amdgcn_s_barrier();
+    if (c + S - 1 < kc) issue(c + S - 1, (c + S - 1) % S);
+    const uint8_t* st = lds + (c % S) * STAGE;
+    half8_t bf[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) bf[r] = *reinterpret_cast<const half8_t*>(st + (NA + wn * R + r) * 1024 + lane * 16);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const half8_t af = *reinterpret_cast<const half8_t*>(st + (wm * MT + t) * 1024 + lane * 16);
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[r], acc[t][r], 0, 0, 0);
+    }
+  }
+  wait_vmcnt<0>();
+
+  // Epilogue through an LDS fp32 tile [BM][BN + 1] (one epilogue call site,
+  // coalesced stores; the accumulators never meet the epilogue's registers).
+  __syncthreads();
+  float* ctile = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        ctile[((wm * MT + t) * 16 + 4 * g + v) * (BN + 1) + (wn * R + r) * 16 + j] = acc[t][r][v];
+  __syncthreads();
+  const int cl = int(threadIdx.x % BN);
+  const float bias = has_bias ? h2f(braw) : 0.f;
+  if (my_col < p.n) {
+    for (int rl = int(threadIdx.x / BN); rl < BM; rl += 256 / BN) {
+      const int row = m0 + rl;
+      if (row >= p.m) break;
+      const float val = ctile[rl * (BN + 1) + cl];
+      if (epi_now) apply_epilogue(p.epi, row, my_col, val, bias);
+      else p.partials[(int64_t(split) * p.m + row) * p.n + my_col] = val;
+    }
+  }
+}
+
+template <int MT, int R, int S>
+hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  constexpr int BM = 2 * MT * 16, BN = 2 * R * 16;
+  constexpr int NL = BM / 16 + BN / 16;
+  constexpr size_t kLds = std::max(size_t(S) * NL * 1024, size_t(BM) * (BN + 1) * 4);
+  static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&f16_gemm_kernel<MT, R, S>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds));
+  if (attr != hipSuccess) return attr;
+  F16GemmParams p{};
+  p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_f16p);
+  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.kk = (g.k + 31) / 32;
+  p.tiles_n = (g.n + BN - 1) / BN;
+  const int64_t tiles = int64_t(p.tiles_n) * ((g.m + BM - 1) / BM);
+  if (tiles > (int64_t(1) << 28)) return hipErrorInvalidValue;
+  p.tiles = int(tiles);
+  int splits = 1;
+  if (s && s->partials && tiles < 192) {
+    splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, p.kk / (S - 1))));
+    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
+  }
+  p.chunks_per_split = (p.kk + splits - 1) / splits;
+  splits = (p.kk + p.chunks_per_split - 1) / p.chunks_per_split;
+  p.splits = splits;
+  p.defer = deferred != nullptr && splits > 1;
+  p.partials = s ? s->partials : nullptr;
+  hipLaunchKernelGGL((f16_gemm_kernel<MT, R, S>), dim3(unsigned(tiles * splits)), dim3(256), kLds, stream, p);
+  if (p.defer) {
+    *deferred = splits;
+    return hipGetLastError();
+  }
+  if (splits > 1) {
+    const int64_t total = int64_t(g.m) * g.n;
+    const unsigned blocks = unsigned(std::min<int64_t>((total + 63) / 64, 8192));
+    hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m, g.n,
+                       g.epi);
+  }
+  return hipGetLastError();
+}
+
+// 128 x 128 tiles once they fill the chip (>= 256 tiles); below that the
+// 64 x 64 tile (or the int8 panel kernel, which times the same there) keeps
+// more workgroups busy.  Timed on MI355X: M = 8192, K = 1600, N = 6400 in
+// 308 us (0.55 PFLOP/s, against 369 us for the int8 panel kernel);
+// 128 x 64, 64 x 128 and 64 x 64 tiles fell between the two.
+bool f16_gemm_prefers_large(int m, int n) { return int64_t((m + 127) / 128) * ((n + 127) / 128) >= 256; }
+
+hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  if (f16_gemm_prefers_large(g.m, g.n)) return launch_f16_cfg<4, 4, 4>(g, s, stream, deferred);
+  return launch_f16_cfg<2, 2, 4>(g, s, stream, deferred);
+}
+
 template <bool INT8>
 hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, hipStream_t stream) {
   TiledParams p{};
@@ -1391,6 +1593,11 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
         reinterpret_cast<uintptr_t>(g.ln_beta) % 16 != 0)
       return hipErrorInvalidValue;
   }
+  // (K % 32 == 0: an A fragment never reads past its row.)  With int8 packed
+  // weights also present, the fp16 copy serves only the large-tile shapes.
+  if (g.w_f16p && g.m > 32 && !g.ln_gamma && !g.a_p32 && !g.epi.p32 && g.k % 32 == 0 && avec &&
+      reinterpret_cast<uintptr_t>(g.w_f16p) % 16 == 0 && (!g.w_packed || f16_gemm_prefers_large(g.m, g.n)))
+    return launch_f16(g, s, stream, deferred);
   if (g.w_int8 && g.w_packed && g.k % 64 == 0 && avec && reinterpret_cast<uintptr_t>(g.w_packed) % 16 == 0) {
     if (g.m <= 16) return launch_packed<1>(g, s, stream, deferred);
     if (g.m <= 32) return launch_packed<2>(g, s, stream, deferred);
@@ -1434,6 +1641,22 @@ const Scratch* library_scratch(int device, hipStream_t stream, hipError_t* err) 
   }
   s.partial_floats = kScratchPartialFloats;
   return &(table[{device, stream}] = s);
+}
+
+size_t packed_w16_bytes(int k, int n) {
+  if (k <= 0 || n <= 0) return 0;
+  return size_t((n + 15) / 16) * size_t((k + 31) / 32) * 1024;
+}
+
+hipError_t pack_w16(const int8_t* q, int64_t ldq, const float* scales, int k, int n, void* out,
+                    hipStream_t stream) {
+  if (k <= 0 || n <= 0 || !q || !scales || !out || ldq < n) return hipErrorInvalidValue;
+  const int kk = (k + 31) / 32;
+  const int64_t records = int64_t((n + 15) / 16) * kk;
+  const int64_t threads = records * 64;
+  hipLaunchKernelGGL(pack_w16_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream, q, ldq, scales, k,
+                     n, kk, records, static_cast<u32x4_t*>(out));
+  return hipGetLastError();
 }
 
 size_t packed_w8_bytes(int k, int n) {

@@ -59,6 +59,9 @@ struct GemmArgs {
   // Optional panel-packed copy of the int8 W (pack_w8).  When set, M <= 32,
   // K % 64 == 0 and A allows 16-byte loads, the GEMV over the packed records runs.
   const void* w_packed = nullptr;
+  // Optional pre-dequantised fp16 copy of the int8 W (pack_w16): the M > 32
+  // GEMM then runs as a plain fp16 MFMA GEMM over it (same values).
+  const void* w_f16p = nullptr;
   // A is P32 fragment-packed (M <= 32, packed W; lda ignored).
   bool a_p32 = false;
   // Optional greedy partials (EPI_F32 logits): when the wide LM-head GEMV runs
@@ -90,6 +93,12 @@ bool gemm_ln_supported(int m, int k, int n);
 // l = 0..63, column cb*16 + (l & 15) at rows kc*64 + 8*(l>>4) + 0..7 and
 // kc*64 + 32 + 8*(l>>4) + 0..7 (16 bytes); entries past K or N are zero.
 size_t packed_w8_bytes(int k, int n);
+// fp16 B records of fp16_rn(float(q) * scale): for column block cb (16 columns)
+// and K group kk (32 rows), 1 KiB at (cb * ceil(K/32) + kk) * 1024 bytes, lane l
+// holding column cb*16 + (l & 15), rows kk*32 + 8*(l>>4) + 0..7; zero past K, N.
+size_t packed_w16_bytes(int k, int n);
+hipError_t pack_w16(const int8_t* q, int64_t ldq, const float* scales, int k, int n, void* out,
+                    hipStream_t stream);
 hipError_t pack_w8(const int8_t* q, int64_t ldq, int k, int n, void* out, hipStream_t stream);
 
 // When `deferred` is non-null and the skinny (M <= 32) kernel runs, the epilogue

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const
         const tia::half8_t p =
             *reinterpret_cast<const tia::half8_t*>(wpe + int64_t(offsets[b] + t) * hidden + 8 * gi);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[i][k] = float(tia::f16(float(e[k]) + float(p[k])));
+        for (int k = 0; k < 8; ++k) v[i][k] = float(tia::f16r(float(e[k]) + float(p[k])));
       }
       tia::half8_t o;
 #pragma unroll
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const
       const tia::half8_t bb = *reinterpret_cast<const tia::half8_t*>(bt + 8 * gi);
       tia::half8_t o;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) o[k] = tia::f16((v[i][k] - mean) * inv * float(gg[k]) + float(bb[k]));
+      for (int k = 0; k < 8; ++k) o[k] = tia::f16r((v[i][k] - mean) * inv * float(gg[k]) + float(bb[k]));
       *reinterpret_cast<tia::half8_t*>(norm + (p32 ? tia::p32_off(row, 8 * gi) : int64_t(row) * hidden + 8 * gi)) = o;
     }
   }
@@ -247,6 +247,7 @@ struct ti_llm_model {
     int k = 0, n = 0;
     int64_t ldw = 0;
     const void* packed = nullptr;  // panel-packed int8 copy for the decode GEMV
+    const void* f16p = nullptr;    // pre-dequantised fp16 copy for large prefill GEMMs
   };
 
   ti_llm_options opt{};
@@ -396,11 +397,21 @@ struct ti_llm_model {
         ck(tia::pack_w8(static_cast<const int8_t*>(w.w), w.ldw, w.k, w.n, out, stream));
         w.packed = out;
       };
+      // Prefills large enough for 128 x 128 GEMM tiles (thousands of rows) read
+      // a pre-dequantised fp16 copy (2 bytes per weight; the decode GEMVs keep
+      // reading int8).
+      const bool f16_copies = int64_t(opt.max_batch) * opt.capacity >= 2048;
+      auto pack16 = [&](Linear& w) {
+        if (!f16_copies) return;
+        void* out = alloc<uint8_t>(tia::packed_w16_bytes(w.k, w.n));
+        ck(tia::pack_w16(static_cast<const int8_t*>(w.w), w.ldw, w.scales, w.k, w.n, out, stream));
+        w.f16p = out;
+      };
       for (int l = 0; l < L; ++l) {
-        pack(c_attn[l]);
-        pack(c_proj[l]);
-        pack(c_fc[l]);
-        pack(c_proj2[l]);
+        for (Linear* w : {&c_attn[l], &c_proj[l], &c_fc[l], &c_proj2[l]}) {
+          pack(*w);
+          pack16(*w);
+        }
       }
       pack(head);
     }
@@ -459,6 +470,7 @@ struct ti_llm_model {
     g.k = w.k;
     g.ldw = w.ldw;
     g.w_packed = w.packed;
+    g.w_f16p = w.f16p;
     g.a_p32 = a_p32;
     if (amax_groups) {
       g.amax_v = d_amax_v;
