@@ -499,8 +499,9 @@ def main():
                             "algorithmic_bytes": gemv_bytes(1, 3072, 768)}
     if args.part in ("all", "kernels"):
         prefill = ((64, 768, 3072), (64, 3072, 768), (512, 768, 3072), (512, 3072, 768))
-        line["kernels"] = {"gemm_prefill": run_gemm(rp, prefill, packed=True),
-                           "gemm_prefill_f16_packed": run_gemm(rp, prefill, packed="w16"),
+        prefill_xl = prefill + ((8192, 1600, 6400),)  # a GPT-2 XL c_fc prefill of 32 x 256 tokens
+        line["kernels"] = {"gemm_prefill": run_gemm(rp, prefill_xl, packed=True),
+                           "gemm_prefill_f16_packed": run_gemm(rp, prefill_xl, packed="w16"),
                            "gemm_prefill_row_major_abi": run_gemm(rp, prefill),
                            "rowops_f32": run_rowops(rp), "decode_attention": run_decode_attention(rp),
                            "prefill_attention": run_prefill_attention(rp)}
