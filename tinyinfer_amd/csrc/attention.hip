@@ -81,6 +81,22 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   const uint16_t* kb = a.k + slot * a.kv_sb + int64_t(h) * a.kv_sh + 8 * ds;
   const uint16_t* vb = a.v + slot * a.kv_sb + int64_t(h) * a.kv_sh + 8 * ds;
 
+  // Keys at or past `end` re-read key end-1 (valid, written data) instead of
+  // branching, so every load of a tile is unconditional and the compiler can
+  // wait for one tile while the next is still in flight; their scores are -inf
+  // and their probabilities 0 in `process`.
+  auto load_tile = [&](KVTile<NI>& t, int k0) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int key = min(k0 + kg + KPI * i, end - 1);
+      t.k[i] = load8<VEC>(kb + int64_t(key) * D);
+      t.v[i] = load8<VEC>(vb + int64_t(key) * D);
+    }
+  };
+  constexpr int STEP = TK * KW;
+  const int k_first = kbeg + kw * TK;
+  KVTile<NI> ta0, tb0;  // FUSEDQKV: the first pair, loaded before q, k, v are known
+  half8_t kfresh = {}, vfresh = {};
   half8_t qf = {};
   if constexpr (FUSEDQKV) {
     // Wave 0 finishes the deferred QKV GEMM for this (b, h): lane d sums the
@@ -88,7 +104,15 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
     // output), stores k and v into the cache at the new position, and shares q
     // through LDS.  The barrier orders those stores before any tile load.
     static_assert(D == 64 && QW == 1, "fused QKV decode is for 64-dim heads, one query");
-    __shared__ f16 sq[64];
+    __shared__ f16 sq[64], sk[64], sv[64];
+    // The first pair of tiles is already in flight while the new token's q, k,
+    // v are summed; its key end - 1 (the new token, not yet in the cache when
+    // loaded) is taken from LDS when scored.
+    if (k_first < end) {
+      load_tile(ta0, k_first);
+      load_tile(tb0, k_first + STEP);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     if (wave == 0 && q_valid > 0) {
       const int64_t plane = int64_t(a.batch) * 3 * a.hidden;
       const float* pp = a.qkv_partials + int64_t(b) * 3 * a.hidden + h * 64 + lane;
@@ -112,14 +136,24 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
         svv[0] += ps[2 * a.hidden];
       }
       sq[lane] = f16r(((sqv[0] + sqv[1]) + (sqv[2] + sqv[3])) + bqv);
+      const f16 kn = f16r(((skv[0] + skv[1]) + (skv[2] + skv[3])) + bkv);
+      const f16 vn = f16r(((svv[0] + svv[1]) + (svv[2] + svv[3])) + bvv);
+      sk[lane] = kn;
+      sv[lane] = vn;
       const int64_t pos = a.offsets[b];
       const int64_t at = slot * a.kv_sb + int64_t(h) * a.kv_sh + pos * D + lane;
-      const_cast<uint16_t*>(a.k)[at] = f2h(((skv[0] + skv[1]) + (skv[2] + skv[3])) + bkv);
-      const_cast<uint16_t*>(a.v)[at] = f2h(((svv[0] + svv[1]) + (svv[2] + svv[3])) + bvv);
+      const_cast<uint16_t*>(a.k)[at] = __builtin_bit_cast(uint16_t, kn);
+      const_cast<uint16_t*>(a.v)[at] = __builtin_bit_cast(uint16_t, vn);
     }
-    __syncthreads();
+    // LDS only: this workgroup never reads the new cache entry back (later
+    // kernels do, after the kernel boundary), and the tile loads stay in flight.
+    lds_barrier();
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[e] = sq[8 * ds + e];
+    for (int e = 0; e < 8; ++e) {
+      qf[e] = sq[8 * ds + e];
+      kfresh[e] = sk[8 * ds + e];
+      vfresh[e] = sv[8 * ds + e];
+    }
   }
   // Unfused: q is re-read with each pair of tiles (an L2 hit after the first)
   // rather than once up front, which would make the compiler wait for it
@@ -129,18 +163,6 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   float m = kNegInf, l = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
-  // Keys at or past `end` re-read key end-1 (valid, written data) instead of
-  // branching, so every load of a tile is unconditional and the compiler can
-  // wait for one tile while the next is still in flight; their scores are -inf
-  // and their probabilities 0 in `process`.
-  auto load_tile = [&](KVTile<NI>& t, int k0) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int key = min(k0 + kg + KPI * i, end - 1);
-      t.k[i] = load8<VEC>(kb + int64_t(key) * D);
-      t.v[i] = load8<VEC>(vb + int64_t(key) * D);
-    }
-  };
   // Online softmax per key group: the LPK lanes of a key group keep their own
   // (m, l, acc) over the keys they own, so a tile needs no cross-group
   // communication; the dot product of a key finishes with a DPP butterfly
@@ -170,8 +192,9 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + kg + KPI * i;
       float part = 0.f;
+      const half8_t kv8 = FUSEDQKV && key >= end - 1 ? kfresh : t.k[i];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part += float(qf[e]) * float(t.k[i][e]);
+      for (int e = 0; e < 8; ++e) part += float(qf[e]) * float(kv8[e]);
       part = group_sum(part);
       s[i] = key < end ? part * p.scale : kNegInf;
     }
@@ -188,8 +211,9 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
       const int key = k0 + kg + KPI * i;
       const float pr = key < end ? __expf(s[i] - nm) : 0.f;
       l += pr;
+      const half8_t vv8 = FUSEDQKV && key >= end - 1 ? vfresh : t.v[i];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += pr * float(t.v[i][e]);
+      for (int e = 0; e < 8; ++e) acc[e] += pr * float(vv8[e]);
     }
     m = nm;
   };
@@ -198,8 +222,15 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   // before the first is scored, so a pair costs one memory round trip.  (A
   // loop that issues the next tile while scoring the current one gets a full
   // vmcnt(0) at its header from the compiler, i.e. one round trip per tile.)
-  constexpr int STEP = TK * KW;
-  for (int k0 = kbeg + kw * TK; k0 < end; k0 += 2 * STEP) {
+  int k0 = k_first;
+  if constexpr (FUSEDQKV) {
+    if (k0 < end) {
+      process(ta0, k0, qf);
+      if (k0 + STEP < end) process(tb0, k0 + STEP, qf);
+    }
+    k0 += 2 * STEP;
+  }
+  for (; k0 < end; k0 += 2 * STEP) {
     half8_t qv = qf;
     if constexpr (!FUSEDQKV) qv = load8<VEC>(qptr);
     KVTile<NI> ta, tb;

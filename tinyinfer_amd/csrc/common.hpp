@@ -48,6 +48,14 @@ __device__ __forceinline__ float gelu_tanh(float z) {
   return 0.5f * z * (1.f + tanhf(0.7978845608028654f * (z + 0.044715f * z * z * z)));
 }
 
+// Workgroup barrier that orders LDS accesses only: outstanding global loads
+// stay in flight across it (__syncthreads would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Butterfly reductions across the 64 lanes of a wave.  Every lane ends with the
 // full result.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -356,14 +356,6 @@ struct PackedParams {
   float ln_eps;
 };
 
-// Workgroup barrier that orders LDS accesses only: outstanding global loads
-// stay in flight across it (__syncthreads would wait for them).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // fp16_rn(float(q) * scale) of the 8 bytes in (lo, hi): one MFMA B operand.
 __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scale) {
   half8_t out;
