@@ -186,6 +186,27 @@ def test_decode_b17_and_one_row_score_match_oracle(model, cpu_model):
     model.reset_all()
 
 
+def test_long_prefill_matches_oracle(model, cpu_model):
+    """16 requests of 128 tokens: a 2048-row prefill, where the linears run on
+    the pre-dequantised fp16 weights (64 x 64 tiles) instead of the int8 panels."""
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, 50257, 128).tolist() for _ in range(16)]
+    slots = list(range(16))
+    say("2048-row prefill vs oracle")
+    model.reset_all()
+    gpu = logits_of(model.forward(slots, prompts))
+    for s in slots:
+        cpu_model.reset(s)
+    cpu, nxt = cpu_model.forward(slots, prompts)
+    print(f"2048-row prefill max |logit diff| {np.abs(gpu - cpu).max():.3g}")
+    assert np.abs(gpu - cpu).max() <= 5e-2
+    step = [[int(t)] for t in nxt]
+    gpu2 = logits_of(model.forward(slots, step))
+    cpu2, _ = cpu_model.forward(slots, step)
+    assert np.abs(gpu2 - cpu2).max() <= 5e-2
+    model.reset_all()
+
+
 def test_decode_graph_equals_eager(model):
     ids = token_ids(20, seed=9)
     say("graph vs eager")

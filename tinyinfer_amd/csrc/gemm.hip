@@ -796,6 +796,7 @@ struct PanelParams {
   int m, n, k;
   int nb, kc;           // column blocks, K chunks
   int tiles_n, tiles;   // tiles per row of tiles, tiles per split
+  int group_m;          // tile rows per group of the tile order
   int chunks_per_split, splits;
   bool defer;
   Epilogue epi;
@@ -823,6 +824,23 @@ __device__ __forceinline__ void wait_chunk(int outstanding) {
   }
 }
 
+// Workgroup -> (split, tile row, tile column).  Workgroups are dispatched to
+// the 8 XCDs round-robin by id, so ids are first regrouped into 8 contiguous
+// runs (one per XCD); within a split, tiles are walked in groups of GM tile
+// rows, column by column, so the workgroups one XCD runs together share GM
+// A row panels and a few weight column panels in that XCD's L2 instead of
+// each streaming every weight column panel (gm_max = 1: row-major order).
+__device__ __forceinline__ void tile_of_block(int gm_max, int tiles_n, int tiles, int& split, int& tm, int& tn) {
+  const int nbk = gridDim.x, bid = blockIdx.x;
+  const int logical = (nbk % 8 == 0) ? (bid % 8) * (nbk / 8) + bid / 8 : bid;
+  const int tile = logical % tiles, tiles_m = tiles / tiles_n;
+  split = logical / tiles;
+  const int per_group = gm_max * tiles_n, group = tile / per_group, first = group * gm_max;
+  const int gm = min(tiles_m - first, gm_max), r = tile - group * per_group;
+  tm = first + r % gm;
+  tn = r / gm;
+}
+
 template <int WM, int WN, int MT, int R, int S>
 __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
   constexpr int BM = WM * MT * 16, BN = WN * R * 16;
@@ -836,10 +854,8 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int wm = wave / WN, wn = wave % WN;
-  const int nbk = gridDim.x, bid = blockIdx.x;
-  const int logical = (nbk % 8 == 0) ? (bid % 8) * (nbk / 8) + bid / 8 : bid;
-  const int tile = logical % p.tiles, split = logical / p.tiles;
-  const int tn = tile % p.tiles_n, tm = tile / p.tiles_n;
+  int split, tm, tn;
+  tile_of_block(p.group_m, p.tiles_n, p.tiles, split, tm, tn);
   const int m0 = tm * BM, cb0 = tn * NB;
   const int c_begin = split * p.chunks_per_split;
   const int kc = min(p.kc - c_begin, p.chunks_per_split);  // chunks of this split (>= 1)
@@ -1305,6 +1321,7 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
   p.nb = (g.n + 15) / 16;
   p.kc = g.k / 64;
   p.tiles_n = (g.n + BN - 1) / BN;
+  p.group_m = 8;  // M = 8192, 1600->6400: 356 us against 379 in row-major tile order
   const int64_t tiles = int64_t(p.tiles_n) * ((g.m + BM - 1) / BM);
   if (tiles > (int64_t(1) << 28)) return hipErrorInvalidValue;
   p.tiles = int(tiles);
@@ -1358,6 +1375,7 @@ struct F16GemmParams {
   int m, n, k;
   int kk;            // K groups of 32
   int tiles_n, tiles;
+  int group_m;       // tile rows per group of the tile order
   int chunks_per_split, splits;
   bool defer;
   Epilogue epi;
@@ -1399,10 +1417,8 @@ __global__ __launch_bounds__(256, 2) void f16_gemm_kernel(F16GemmParams p) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
-  const int nbk = gridDim.x, bid = blockIdx.x;
-  const int logical = (nbk % 8 == 0) ? (bid % 8) * (nbk / 8) + bid / 8 : bid;
-  const int tile = logical % p.tiles, split = logical / p.tiles;
-  const int tn = tile % p.tiles_n, tm = tile / p.tiles_n;
+  int split, tm, tn;
+  tile_of_block(p.group_m, p.tiles_n, p.tiles, split, tm, tn);
   const int m0 = tm * BM, cb0 = tn * NB;
   const int nbt = (p.n + 15) / 16;
   const int c_begin = split * p.chunks_per_split;
@@ -1503,6 +1519,7 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.kk = (g.k + 31) / 32;
   p.tiles_n = (g.n + BN - 1) / BN;
+  p.group_m = 2;  // M = 8192, 1600->6400: 315 us; row-major order 321, groups of 8 rows 327
   const int64_t tiles = int64_t(p.tiles_n) * ((g.m + BM - 1) / BM);
   if (tiles > (int64_t(1) << 28)) return hipErrorInvalidValue;
   p.tiles = int(tiles);
@@ -1530,15 +1547,23 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
   return hipGetLastError();
 }
 
-// 128 x 128 tiles once they fill the chip (>= 256 tiles); below that the
-// 64 x 64 tile (or the int8 panel kernel, which times the same there) keeps
-// more workgroups busy.  Timed on MI355X: M = 8192, K = 1600, N = 6400 in
-// 308 us (0.55 PFLOP/s, against 369 us for the int8 panel kernel);
-// 128 x 64, 64 x 128 and 64 x 64 tiles fell between the two.
-bool f16_gemm_prefers_large(int m, int n) { return int64_t((m + 127) / 128) * ((n + 127) / 128) >= 256; }
+// Tile choice over the fp16 records, and when they beat the int8 panel
+// kernel, from timings on MI355X (graph replays over rotating weights):
+// * 128 x 128 tiles win once K is long and the grid holds >= 384 of them
+//   (GPT-2 XL prefill, M = 10723: 1600->4800 306 us against 347 for int8
+//   panels, 1600->6400 388 against 456, 6400->1600 346 against 439; M = 8192
+//   3072->768 81 against 86);
+// * at K < 1536 the 128 x 128 epilogue and tail dominate (M = 8192, 768->2304
+//   101 us) and 64 x 64 tiles win (76 us; int8 panels 87), from M = 2048
+//   (768->2304 29 against 31 us); below that the two 64 x 64 kernels time the
+//   same and the int8 panels are kept.
+bool f16_gemm_large(int m, int n, int k) {
+  return k >= 1536 && int64_t((m + 127) / 128) * ((n + 127) / 128) >= 384;
+}
+bool f16_gemm_preferred(int m, int n, int k) { return f16_gemm_large(m, n, k) || (m >= 2048 && k < 1536); }
 
 hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
-  if (f16_gemm_prefers_large(g.m, g.n)) return launch_f16_cfg<4, 4, 4>(g, s, stream, deferred);
+  if (f16_gemm_large(g.m, g.n, g.k)) return launch_f16_cfg<4, 4, 4>(g, s, stream, deferred);
   return launch_f16_cfg<2, 2, 4>(g, s, stream, deferred);
 }
 
@@ -1586,9 +1611,9 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
       return hipErrorInvalidValue;
   }
   // (K % 32 == 0: an A fragment never reads past its row.)  With int8 packed
-  // weights also present, the fp16 copy serves only the large-tile shapes.
+  // weights also present, the fp16 copy serves only the shapes where it wins.
   if (g.w_f16p && g.m > 32 && !g.ln_gamma && !g.a_p32 && !g.epi.p32 && g.k % 32 == 0 && avec &&
-      reinterpret_cast<uintptr_t>(g.w_f16p) % 16 == 0 && (!g.w_packed || f16_gemm_prefers_large(g.m, g.n)))
+      reinterpret_cast<uintptr_t>(g.w_f16p) % 16 == 0 && (!g.w_packed || f16_gemm_preferred(g.m, g.n, g.k)))
     return launch_f16(g, s, stream, deferred);
   if (g.w_int8 && g.w_packed && g.k % 64 == 0 && avec && reinterpret_cast<uintptr_t>(g.w_packed) % 16 == 0) {
     if (g.m <= 16) return launch_packed<1>(g, s, stream, deferred);

@@ -397,9 +397,9 @@ struct ti_llm_model {
         ck(tia::pack_w8(static_cast<const int8_t*>(w.w), w.ldw, w.k, w.n, out, stream));
         w.packed = out;
       };
-      // Prefills large enough for 128 x 128 GEMM tiles (thousands of rows) read
-      // a pre-dequantised fp16 copy (2 bytes per weight; the decode GEMVs keep
-      // reading int8).
+      // Prefills of 2048 rows and more read a pre-dequantised fp16 copy where
+      // its GEMM beats the int8 panels (2 bytes per weight; the decode GEMVs
+      // keep reading int8).
       const bool f16_copies = int64_t(opt.max_batch) * opt.capacity >= 2048;
       auto pack16 = [&](Linear& w) {
         if (!f16_copies) return;
