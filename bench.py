@@ -9,7 +9,8 @@ achieved HBM GB/s".
   as reference llm/evaluate.py:195 defines it.  One "step" is one such greedy
   batch; batch 1 is reported beside it.
 * roofline: the W8A16 decode GEMV over the runtime's panel-packed int8 weights
-  (one kernel, M=1, K=3072 -> N=768, fused bias+GELU) replayed back-to-back from
+  (one kernel, M=1, K=3072 -> N=768, fused bias+GELU: gemv_part_kernel, 96
+  workgroups of 8 waves, 8 output columns each) replayed back-to-back from
   a HIP graph over >= 600 MiB of distinct weight sets (beyond the 256 MiB
   Infinity Cache), timed with HIP events on the launch stream; algorithmic bytes
   2MK + KN + 4N + 2N + 2MN.  gemv adds the other configs[1] M <= 8 shapes and
@@ -500,7 +501,7 @@ def main():
         line["gemv_row_major_abi"] = run_gemm(rp, sweep)
         dom = gemv["M1_K3072_N768"]
         line["roofline"] = {"bound": "hbm",
-                            "kernel": "gemv_packed_kernel<MT=1,W=16,CPW=3> (panel-packed int8), M=1 K=3072 N=768",
+                            "kernel": "gemv_part_kernel<W=8,LPW=3,QC=8> (panel-packed int8, 8 columns per workgroup), M=1 K=3072 N=768",
                             "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": pmc_traffic(),
                             "algorithmic_bytes": gemv_bytes(1, 3072, 768)}

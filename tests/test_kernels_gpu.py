@@ -213,6 +213,32 @@ def test_packed_gemv_against_oracle(ops, m, k, n):
     close(h(hbits(res)), expect)
 
 
+@pytest.mark.parametrize("k,n", [(768, 768), (1600, 1600), (6400, 1600), (192, 2040), (64, 8), (3072, 2048)])
+def test_packed_gemv_single_row_parts(ops, k, n):
+    """M = 1 over at most 2048 columns (the 8-column part-block kernel): odd and
+    multi-round chunk counts (K = 1600 -> 25, 6400 -> 100), a ragged last block
+    (2040, 8 columns), bias / no bias + GELU / in-place residual epilogues."""
+    t = torch()
+    rng = np.random.default_rng(5 * k + n)
+    a = f16(rng.standard_normal((1, k)))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("packed gemv single row", k, n)
+    packed = _pack_gpu(ops.lib, dev(q), k, n)
+    ad, sd, bd = dev(a, t.float16), dev(s), dev(bias, t.float16)
+    y = t.empty((1, n), dtype=t.float16, device="cuda")
+    _packed(ops.lib, ad, packed, sd, bd, y, None, 1, n, k, 0)
+    ref = oracle.linear(a, q=q, scales=s, bias_bits=bias)
+    close(h(hbits(y)), h(ref))
+    _packed(ops.lib, ad, packed, sd, None, y, None, 1, n, k, 1)
+    close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, gelu=True)))
+    res = dev(f16(rng.standard_normal((1, n))), t.float16)
+    expect = (h(hbits(res)) + h(ref)).astype(np.float16).astype(np.float64)
+    _packed(ops.lib, ad, packed, sd, bd, res, res, 1, n, k, 2)
+    close(h(hbits(res)), expect)
+
+
 @pytest.mark.parametrize("m,k,n", [(32, 1600, 8192), (24, 768, 50257), (32, 3072, 2048)])
 def test_packed_gemv_column_block_groups(ops, m, k, n):
     """M in (16, 32] over a wide matrix: four column blocks share each A fragment,

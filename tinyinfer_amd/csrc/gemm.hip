@@ -7,7 +7,9 @@
 //    loads of a wave are in flight before its first wait, the waves of a
 //    workgroup split K and reduce through LDS, and the epilogue runs in the
 //    same kernel (K is split across workgroups only when the caller finishes
-//    the partials itself).
+//    the partials itself).  A single row (M = 1) over at most 2048 columns
+//    takes the part-block kernel instead: no MFMA, 8 columns per workgroup,
+//    twice the workgroups of the 16-column MFMA blocks.
 //  * skinny (M <= 32, row-major weights of the ABI): every wave streams weight fragments straight from
 //    HBM into MFMA B-operand registers (no LDS for weights), dequantises them in
 //    registers as fp16_rn(float(q) * scale[n]) and runs v_mfma_f32_16x16x32_f16
@@ -623,6 +625,80 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     if (epi_now) apply_epilogue(p.epi, row, n, s, bias, has_res ? h2f(res_raw[it]) : 0.f);
     else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Part-block GEMV for a single row of A (M = 1) over the panel-packed weights,
+// without MFMA.  A workgroup owns QC in {4, 8} columns of a 16-column block, so
+// N = 768 runs on 96 (QC 8) or 192 (QC 4) workgroups instead of 48, each
+// streaming a part of the bytes (a single-row product has no use for the
+// 16-row MFMA shape).  QC 4 reads half cache lines and measured slower; the
+// launcher uses QC 8.  In a record the QC columns of part h sit in lanes
+// QC*h .. QC*h + QC - 1 of each 16-lane group, four runs of 16*QC bytes; a wave
+// load takes those runs of 16 / QC consecutive records.  Lane L holds column
+// 16 cb + QC h + (L % QC) at the 16 rows of lane group (L / QC) % 4 of record
+// (16 / QC) * step + L / (4 QC).  Products are fp16_rn(float(q) * scale) times
+// A in fp16 (dot2, fp32 sums); the lanes of a column, then the W waves
+// (through LDS), are summed and the epilogue runs in the kernel (or the fp32
+// sums go to partials split 0 for a deferred launch).  Wave w takes record
+// steps w, w + W, ... and issues LPW of them before the first wait; records
+// past the end are clamped to the last one and weighted 0.
+template <int W, int LPW, int QC>
+__global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
+  static_assert(QC == 4 || QC == 8, "4 or 8 columns per workgroup");
+  constexpr int RPL = 16 / QC;  // records per wave load
+  __shared__ float red[W][QC];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane % QC, g = (lane / QC) & 3, r = lane / (4 * QC);
+  const int cb = blockIdx.x / RPL, h = blockIdx.x % RPL;
+  const int col = cb * 16 + QC * h + c;
+  const bool epi_now = !p.defer;
+  const bool has_bias = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias;
+  const bool has_res = epi_now && p.epi.kind == EPI_RESIDUAL;
+  // Epilogue operands of output column cb*16 + QC h + threadIdx.x % QC, loaded
+  // first and unconditionally (A's first element stands in), converted at use.
+  const int ecol = min(cb * 16 + QC * h + int(threadIdx.x % QC), p.n - 1);
+  const uint16_t bias_raw = (has_bias ? p.epi.bias : p.a)[has_bias ? ecol : 0];
+  const uint16_t res_raw = (has_res ? p.epi.residual : p.a)[has_res ? r_off(p.epi, 0, ecol) : 0];
+  const float scale = p.scales[min(col, p.n - 1)] * (col < p.n ? 1.f : 0.f);
+  const u32x4_t* wb = p.w + int64_t(cb) * p.kc * 64 + g * 16 + QC * h + c;
+  const uint16_t* arow = p.a + 8 * g;
+  const int steps = (p.kc + RPL - 1) / RPL;
+  float acc = 0.f;
+  for (int s0 = wave; s0 < steps; s0 += W * LPW) {
+    u32x4_t wf[LPW];
+    half8_t af[LPW][2];
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int kc = min(RPL * min(s0 + i * W, steps - 1) + r, p.kc - 1);
+      wf[i] = __builtin_nontemporal_load(wb + int64_t(kc) * 64);
+      af[i][0] = *reinterpret_cast<const half8_t*>(arow + kc * 64);
+      af[i][1] = *reinterpret_cast<const half8_t*>(arow + kc * 64 + 32);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const bool live = s0 + i * W < steps && RPL * (s0 + i * W) + r < p.kc;
+      const float si = live ? scale : 0.f;
+      const half8_t b0 = dequant8(wf[i][0], wf[i][1], si);
+      const half8_t b1 = dequant8(wf[i][2], wf[i][3], si);
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        acc = __builtin_amdgcn_fdot2(half2_t{af[i][0][e], af[i][0][e + 1]}, half2_t{b0[e], b0[e + 1]}, acc, false);
+        acc = __builtin_amdgcn_fdot2(half2_t{af[i][1][e], af[i][1][e + 1]}, half2_t{b1[e], b1[e + 1]}, acc, false);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = QC; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane < QC) red[wave][lane] = acc;
+  __syncthreads();
+  if (threadIdx.x >= QC || cb * 16 + QC * h + int(threadIdx.x) >= p.n) return;
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < W; ++w) s += red[w][threadIdx.x];
+  if (epi_now) apply_epilogue(p.epi, 0, ecol, s, has_bias ? h2f(bias_raw) : 0.f, has_res ? h2f(res_raw) : 0.f);
+  else p.partials[ecol] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -1248,6 +1324,35 @@ hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipS
   return hipErrorInvalidValue;
 }
 
+// M = 1 over packed weights with at most 128 column blocks (N <= 2048): the
+// part-block kernel, 8 columns per workgroup.  W x LPW covers the record pairs
+// in one round up to K = 3072 (timed on GPT-2 small / XL shapes: 768 -> 768
+// 3.07 -> 2.73 us, 3072 -> 768 4.37 -> 3.30 us, 1600 -> 1600 3.95 -> 3.07 us;
+// at 2304 columns and more the MFMA GEMV is as fast or faster).
+bool part_gemv_preferred(const GemmArgs& g) {
+  return g.m == 1 && !g.a_p32 && !g.ln_gamma && (g.n + 15) / 16 <= 128;
+}
+
+hipError_t launch_part(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  PackedParams p{};
+  p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
+  p.m = 1; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.nb = (g.n + 15) / 16;
+  p.kc = g.k / 64;
+  p.chunks_per_split = p.kc;
+  p.splits = 1;
+  p.defer = deferred != nullptr;
+  p.partials = s ? s->partials : nullptr;
+  if (p.defer && (!p.partials || size_t(g.n) > s->partial_floats)) return hipErrorInvalidValue;
+  if (deferred) *deferred = 1;
+  const int steps = (p.kc + 1) / 2;
+  const dim3 grid(unsigned(2 * p.nb));
+  if (steps <= 6) hipLaunchKernelGGL((gemv_part_kernel<3, 2, 8>), grid, dim3(192), 0, stream, p);
+  else if (steps <= 16) hipLaunchKernelGGL((gemv_part_kernel<8, 2, 8>), grid, dim3(512), 0, stream, p);
+  else hipLaunchKernelGGL((gemv_part_kernel<8, 3, 8>), grid, dim3(512), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <int MT>
 hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   PackedParams p{};
@@ -1616,6 +1721,7 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
       reinterpret_cast<uintptr_t>(g.w_f16p) % 16 == 0 && (!g.w_packed || f16_gemm_preferred(g.m, g.n, g.k)))
     return launch_f16(g, s, stream, deferred);
   if (g.w_int8 && g.w_packed && g.k % 64 == 0 && avec && reinterpret_cast<uintptr_t>(g.w_packed) % 16 == 0) {
+    if (part_gemv_preferred(g)) return launch_part(g, s, stream, deferred);
     if (g.m <= 16) return launch_packed<1>(g, s, stream, deferred);
     if (g.m <= 32) return launch_packed<2>(g, s, stream, deferred);
     return launch_panel(g, s, stream, deferred);
