@@ -160,6 +160,7 @@ def _lib():
     lib.ti_amd_gemm_w16p_fused.argtypes = [v] * 5 + [i] * 4 + [C.c_size_t, i]
     lib.ti_amd_layernorm_f32.argtypes = [v, v, v, v, i, i, C.c_float, C.c_size_t, i]
     lib.ti_amd_softmax_f32.argtypes = [v, v, i, i, C.c_size_t, i]
+    lib.ti_amd_layernorm_softmax_f32.argtypes = [v, v, v, v, i, i, C.c_float, C.c_size_t, i]
     return ops, lib
 
 
@@ -247,10 +248,17 @@ def run_rowops(rp):
     for i in range(sets):
         pair += [ln(i), sm2(i)]
     us2 = rp.time_us(pair) * 2
-    res["layernorm_softmax_f32_4096x768"] = {"us_per_pair": us2, "GBps_fused_ideal_bytes": nb / us2 / 1e3,
-                                             "hbm_frac": nb / us2 / 1e3 / HBM_PEAK_GBS,
-                                             "note": "two launches, as the reference's graph; bytes counted as the "
-                                                     "fused ideal 2*rows*cols*4"}
+    res["layernorm_then_softmax_f32_4096x768"] = {"us_per_pair": us2, "GBps_fused_ideal_bytes": nb / us2 / 1e3,
+                                                  "hbm_frac": nb / us2 / 1e3 / HBM_PEAK_GBS,
+                                                  "note": "two launches, as the reference's graph; bytes counted as "
+                                                          "the fused ideal 2*rows*cols*4"}
+    fused = lambda i: (lambda: _check(lib, lib.ti_amd_layernorm_softmax_f32(
+        x[i].data_ptr(), gam.data_ptr(), bet.data_ptr(), y[i].data_ptr(), rows, cols, 1e-5, s(), 0)))
+    us3 = rp.time_us([fused(i) for i in range(sets)])
+    res["layernorm_softmax_f32_4096x768"] = {"us_per_launch": us3, "GBps": nb / us3 / 1e3,
+                                             "hbm_frac": nb / us3 / 1e3 / HBM_PEAK_GBS,
+                                             "note": "one pass per row (ti_amd_layernorm_softmax_f32), same values "
+                                                     "as the two launches"}
     del x, y
     torch.cuda.empty_cache()
     rows, cols = 4096, 1024

@@ -81,6 +81,13 @@ int ti_amd_gemm_w8p_ln_fused(const uint16_t* a, const uint16_t* gamma, const uin
 int ti_amd_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
                          int rows, int cols, float eps, uintptr_t stream, int device);
 int ti_amd_softmax_f32(const float* x, float* y, int rows, int cols, uintptr_t stream, int device);
+/* y = softmax(LayerNorm(x; gamma, beta, eps)) over the last axis, FP32, one
+ * pass per row: the LayerNorm -> Softmax graph that tinyc's norm_softmax issues
+ * as ti_cuda_layernorm then ti_cuda_softmax (reference bench/integrated.py:87-92,
+ * backend/runtime.cpp:10-12), with the same values as those two calls at half
+ * the memory traffic.  Validation as ti_amd_layernorm_f32; y must not overlap x. */
+int ti_amd_layernorm_softmax_f32(const float* x, const float* gamma, const float* beta, float* y,
+                                 int rows, int cols, float eps, uintptr_t stream, int device);
 #ifdef __cplusplus
 }
 #endif

@@ -603,6 +603,35 @@ def test_fp32_layernorm_then_softmax_config2():
     close(host(y), ref, rtol=1e-4, atol=1e-8)
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 768), (9, 4096), (5, 100), (3, 2048), (6, 4098), (2, 1)])
+def test_fp32_fused_layernorm_softmax(rows, cols):
+    """ti_amd_layernorm_softmax_f32 (one pass per row) returns exactly what the two
+    calls ti_cuda_layernorm then ti_cuda_softmax return (same values, maxima and
+    sums in the same lane order; widths past 4096 or not a multiple of 4 take those
+    two kernels), and 1e-4 relative of the float64 reference."""
+    rng = np.random.default_rng(rows + 3 * cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(cols)).astype(np.float32)
+    dx, dg, db = dev(x), dev(g), dev(b)
+    mid, y2, y = (torch().empty_like(dx) for _ in range(3))
+    lib = _legacy()
+    say("fp32 fused LN->softmax", rows, cols)
+    lib.ti_cuda_layernorm(dx.data_ptr(), dg.data_ptr(), db.data_ptr(), mid.data_ptr(), rows, cols, 1e-5)
+    lib.ti_cuda_softmax(mid.data_ptr(), y2.data_ptr(), rows, cols)
+    fn = lib.ti_amd_layernorm_softmax_f32
+    fn.argtypes = [C.c_void_p] * 4 + [C.c_int, C.c_int, C.c_float, C.c_size_t, C.c_int]
+    st = fn(dx.data_ptr(), dg.data_ptr(), db.data_ptr(), y.data_ptr(), rows, cols, 1e-5,
+            torch().cuda.current_stream().cuda_stream, 0)
+    assert st == 0
+    got = host(y)
+    assert np.array_equal(got.view(np.uint32), host(y2).view(np.uint32))
+    close(got, oracle.softmax_f32_exact(oracle.layernorm_f32_exact(x, g, b)), rtol=1e-4, atol=1e-8)
+    # an output that overlaps the input is rejected before anything is queued
+    assert fn(dx.data_ptr(), dg.data_ptr(), db.data_ptr(), dx.data_ptr(), rows, cols, 1e-5,
+              torch().cuda.current_stream().cuda_stream, 0) == 1
+
+
 def test_ti_cuda_gemm_legacy_order():
     rng = np.random.default_rng(12)
     m, k, n = 37, 70, 45

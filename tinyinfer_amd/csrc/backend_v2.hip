@@ -401,6 +401,20 @@ extern "C" int ti_amd_layernorm_f32(const float* x, const float* g, const float*
   return hip_status(tia::layernorm_f32(x, g, b, y, rows, cols, eps, reinterpret_cast<hipStream_t>(stream)));
 }
 
+extern "C" int ti_amd_layernorm_softmax_f32(const float* x, const float* g, const float* b, float* y, int rows,
+                                            int cols, float eps, uintptr_t stream, int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (!shape_fits({rows, cols}, 4) || !std::isfinite(eps) || eps <= 0.f || !aligned(x, 4) || !aligned(g, 4) ||
+      !aligned(b, 4) || !aligned(y, 4))
+    return fail(TI_V2_INVALID_ARGUMENT, "invalid LayerNorm->softmax arguments");
+  const int64_t bytes = int64_t(rows) * cols * 4;
+  const auto xb = reinterpret_cast<uintptr_t>(x), yb = reinterpret_cast<uintptr_t>(y);
+  if (rows > 0 && cols > 0 && xb < yb + uintptr_t(bytes) && yb < xb + uintptr_t(bytes))
+    return fail(TI_V2_INVALID_ARGUMENT, "LayerNorm->softmax output must not overlap its input");
+  return hip_status(tia::layernorm_softmax_f32(x, g, b, y, rows, cols, eps, reinterpret_cast<hipStream_t>(stream)));
+}
+
 extern "C" int ti_amd_softmax_f32(const float* x, float* y, int rows, int cols, uintptr_t stream, int device) {
   int status = begin(device);
   if (status) return status;

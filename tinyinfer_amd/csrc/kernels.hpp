@@ -173,5 +173,8 @@ hipError_t gelu_f16(const uint16_t* x, uint16_t* y, int64_t count, hipStream_t s
 hipError_t layernorm_f32(const float* x, const float* g, const float* b, float* y, int rows,
                          int cols, float eps, hipStream_t stream);
 hipError_t softmax_f32(const float* x, float* y, int rows, int cols, hipStream_t stream);
+// y = softmax(LayerNorm(x)) row by row in one pass (y may not alias x).
+hipError_t layernorm_softmax_f32(const float* x, const float* g, const float* b, float* y, int rows,
+                                int cols, float eps, hipStream_t stream);
 
 }  // namespace tia

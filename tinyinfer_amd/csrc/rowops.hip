@@ -33,11 +33,16 @@ struct Elem<uint16_t> {
 };
 
 // VPL consecutive elements per lane per vector (16 bytes when VPL * sizeof(T) == 16).
-template <typename T, int VPL>
+// NT: a nontemporal (streaming) access, for row data touched once; the FP32
+// row kernels stream x in and y out that way (measured at configs[2]: 12-24 %
+// less time), while gamma and beta, read by every row, stay cached.
+template <typename T, int VPL, bool NT = false>
 __device__ __forceinline__ void load_vec(const T* p, float* out) {
   if constexpr (VPL * sizeof(T) == 16) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    u32x4_t u;
+    if constexpr (NT) u = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    else u = *reinterpret_cast<const u32x4_t*>(p);
+    const uint32_t w[4] = {u[0], u[1], u[2], u[3]};
     if constexpr (sizeof(T) == 4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[i] = __builtin_bit_cast(float, w[i]);
@@ -50,7 +55,7 @@ __device__ __forceinline__ void load_vec(const T* p, float* out) {
     for (int i = 0; i < VPL; ++i) out[i] = Elem<T>::load(p + i);
   }
 }
-template <typename T, int VPL>
+template <typename T, int VPL, bool NT = false>
 __device__ __forceinline__ void store_vec(T* p, const float* v) {
   if constexpr (VPL * sizeof(T) == 16) {
     uint32_t w[4];
@@ -61,7 +66,8 @@ __device__ __forceinline__ void store_vec(T* p, const float* v) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[i] = uint32_t(f2h(v[2 * i])) | (uint32_t(f2h(v[2 * i + 1])) << 16);
     }
-    *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+    if constexpr (NT) __builtin_nontemporal_store(u32x4_t{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4_t*>(p));
+    else *reinterpret_cast<u32x4_t*>(p) = u32x4_t{w[0], w[1], w[2], w[3]};
   } else {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) Elem<T>::store(p + i, v[i]);
@@ -69,23 +75,26 @@ __device__ __forceinline__ void store_vec(T* p, const float* v) {
 }
 
 // One wave per row; lane l owns elements [VPL*l + 64*VPL*i, +VPL) for i < NV.
+// gamma and beta are requested with the row (they do not depend on it), so the
+// output pass needs no further round trip.
 // P32: x and y are fragment-packed decode matrices (common.hpp p32_off; VPL 8).
-template <typename T, int VPL, int NV, bool P32 = false>
-__global__ __launch_bounds__(256) void layernorm_wave(const T* x, const T* g, const T* b, T* y,
-                                                      int rows, int cols, float eps) {
+template <typename T, int VPL, int NV, bool P32 = false, bool NT = false>
+__device__ __forceinline__ void layernorm_row(const T* x, const T* g, const T* b, int row, int cols, float eps,
+                                              float (&v)[NV][VPL]) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
   auto at = [&](int c) { return P32 ? p32_off(row, c) : int64_t(row) * cols + c; };
-  float v[NV][VPL];
+  float gv[NV][VPL], bv[NV][VPL];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = VPL * lane + 64 * VPL * i;
-    if (c < cols) load_vec<T, VPL>(x + at(c), v[i]);
-    else {
+    if (c < cols) {
+      load_vec<T, VPL, NT>(x + at(c), v[i]);
+      load_vec<T, VPL>(g + c, gv[i]);
+      load_vec<T, VPL>(b + c, bv[i]);
+    } else {
 #pragma unroll
-      for (int e = 0; e < VPL; ++e) v[i][e] = 0.f;
+      for (int e = 0; e < VPL; ++e) v[i][e] = gv[i][e] = bv[i][e] = 0.f;
     }
 #pragma unroll
     for (int e = 0; e < VPL; ++e) s += v[i][e];
@@ -105,40 +114,35 @@ __global__ __launch_bounds__(256) void layernorm_wave(const T* x, const T* g, co
   }
   const float inv = rsqrtf(wave_sum(ss) / float(cols) + eps);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = VPL * lane + 64 * VPL * i;
-    if (c < cols) {
-      float gv[VPL], bv[VPL], o[VPL];
-      load_vec<T, VPL>(g + c, gv);
-      load_vec<T, VPL>(b + c, bv);
+  for (int i = 0; i < NV; ++i)
 #pragma unroll
-      for (int e = 0; e < VPL; ++e) o[e] = (v[i][e] - mean) * inv * gv[e] + bv[e];
-      store_vec<T, VPL>(y + at(c), o);
-    }
-  }
+    for (int e = 0; e < VPL; ++e) v[i][e] = (v[i][e] - mean) * inv * gv[i][e] + bv[i][e];
 }
 
-template <typename T, int VPL, int NV>
-__global__ __launch_bounds__(256) void softmax_wave(const T* x, T* y, int rows, int cols) {
+template <typename T, int VPL, int NV, bool P32 = false, bool NT = false>
+__global__ __launch_bounds__(256) void layernorm_wave(const T* x, const T* g, const T* b, T* y,
+                                                      int rows, int cols, float eps) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const T* xr = x + int64_t(row) * cols;
-  T* yr = y + int64_t(row) * cols;
-  const float ninf = -__builtin_huge_valf();
   float v[NV][VPL];
-  float mx = ninf;
+  layernorm_row<T, VPL, NV, P32, NT>(x, g, b, row, cols, eps, v);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = VPL * lane + 64 * VPL * i;
-    if (c < cols) load_vec<T, VPL>(xr + c, v[i]);
-    else {
+    if (c < cols) store_vec<T, VPL, NT>(y + (P32 ? p32_off(row, c) : int64_t(row) * cols + c), v[i]);
+  }
+}
+
+// Softmax of a row held as v (entries past cols are -inf): max, exp, sum, scale
+// in place, in the order softmax_wave uses.
+template <int VPL, int NV>
+__device__ __forceinline__ void softmax_row(float (&v)[NV][VPL]) {
+  float mx = -__builtin_huge_valf();
 #pragma unroll
-      for (int e = 0; e < VPL; ++e) v[i][e] = ninf;
-    }
+  for (int i = 0; i < NV; ++i)
 #pragma unroll
     for (int e = 0; e < VPL; ++e) mx = fmaxf(mx, v[i][e]);
-  }
   mx = wave_max(mx);
   float s = 0.f;
 #pragma unroll
@@ -150,14 +154,62 @@ __global__ __launch_bounds__(256) void softmax_wave(const T* x, T* y, int rows, 
     }
   const float inv = 1.f / wave_sum(s);
 #pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) v[i][e] *= inv;
+}
+
+template <typename T, int VPL, int NV, bool NT = false>
+__global__ __launch_bounds__(256) void softmax_wave(const T* x, T* y, int rows, int cols) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + int64_t(row) * cols;
+  T* yr = y + int64_t(row) * cols;
+  float v[NV][VPL];
+#pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = VPL * lane + 64 * VPL * i;
-    if (c < cols) {
-      float o[VPL];
+    if (c < cols) load_vec<T, VPL, NT>(xr + c, v[i]);
+    else {
 #pragma unroll
-      for (int e = 0; e < VPL; ++e) o[e] = v[i][e] * inv;
-      store_vec<T, VPL>(yr + c, o);
+      for (int e = 0; e < VPL; ++e) v[i][e] = -__builtin_huge_valf();
     }
+  }
+  softmax_row<VPL, NV>(v);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = VPL * lane + 64 * VPL * i;
+    if (c < cols) store_vec<T, VPL, NT>(yr + c, v[i]);
+  }
+}
+
+// LayerNorm then last-axis softmax of each row in one pass: the graph that
+// tinyc's norm_softmax issues as two calls, ti_*_layernorm then ti_*_softmax
+// (reference bench/integrated.py:87-92).  The LayerNorm output stays in
+// registers in the lane layout softmax_wave reads it with, so the values,
+// maximum and sum are those of the two kernels through memory, for half the
+// HBM traffic (x read once, y written once).
+template <int VPL, int NV>
+__global__ __launch_bounds__(256) void layernorm_softmax_wave(const float* x, const float* g, const float* b,
+                                                              float* y, int rows, int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float v[NV][VPL];
+  layernorm_row<float, VPL, NV, false, true>(x, g, b, row, cols, eps, v);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (VPL * lane + 64 * VPL * i >= cols) {
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) v[i][e] = -__builtin_huge_valf();
+    }
+  }
+  softmax_row<VPL, NV>(v);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = VPL * lane + 64 * VPL * i;
+    if (c < cols) store_vec<float, VPL, true>(y + int64_t(row) * cols + c, v[i]);
   }
 }
 
@@ -298,7 +350,9 @@ hipError_t layernorm_dispatch(const T* x, const T* g, const T* b, T* y, int rows
   const bool vec = cols % VPL == 0 && al16(x) && al16(g) && al16(b) && al16(y);
   const dim3 grid(unsigned((rows + 3) / 4)), block(256);
   const int per = 64 * VPL;
-#define TIA_LN(V, NV) hipLaunchKernelGGL((layernorm_wave<T, V, NV>), grid, block, 0, st, x, g, b, y, rows, cols, eps)
+  constexpr bool NT = sizeof(T) == 4;  // FP32 rows stream; fp16 outputs feed the next decode kernel
+#define TIA_LN(V, NV) \
+  hipLaunchKernelGGL((layernorm_wave<T, V, NV, false, NT>), grid, block, 0, st, x, g, b, y, rows, cols, eps)
   if (vec && cols <= per) TIA_LN(VPL, 1);
   else if (vec && cols <= 2 * per) TIA_LN(VPL, 2);
   else if (vec && cols <= 4 * per) TIA_LN(VPL, 4);
@@ -316,7 +370,8 @@ hipError_t softmax_dispatch(const T* x, T* y, int rows, int cols, hipStream_t st
   const bool vec = cols % VPL == 0 && al16(x) && al16(y);
   const dim3 grid(unsigned((rows + 3) / 4)), block(256);
   const int per = 64 * VPL;
-#define TIA_SM(V, NV) hipLaunchKernelGGL((softmax_wave<T, V, NV>), grid, block, 0, st, x, y, rows, cols)
+  constexpr bool NT = sizeof(T) == 4;
+#define TIA_SM(V, NV) hipLaunchKernelGGL((softmax_wave<T, V, NV, NT>), grid, block, 0, st, x, y, rows, cols)
   if (vec && cols <= per) TIA_SM(VPL, 1);
   else if (vec && cols <= 2 * per) TIA_SM(VPL, 2);
   else if (vec && cols <= 4 * per) TIA_SM(VPL, 4);
@@ -356,6 +411,26 @@ hipError_t layernorm_f32(const float* x, const float* g, const float* b, float* 
 }
 hipError_t softmax_f32(const float* x, float* y, int rows, int cols, hipStream_t st) {
   return softmax_dispatch<float>(x, y, rows, cols, st);
+}
+hipError_t layernorm_softmax_f32(const float* x, const float* g, const float* b, float* y, int rows, int cols,
+                                float eps, hipStream_t st) {
+  const bool vec = cols % 4 == 0 && al16(x) && al16(g) && al16(b) && al16(y);
+  const dim3 grid(unsigned((rows + 3) / 4)), block(256);
+#define TIA_LNSM(NV) \
+  hipLaunchKernelGGL((layernorm_softmax_wave<4, NV>), grid, block, 0, st, x, g, b, y, rows, cols, eps)
+  if (vec && cols <= 256) TIA_LNSM(1);
+  else if (vec && cols <= 512) TIA_LNSM(2);
+  else if (vec && cols <= 1024) TIA_LNSM(4);
+  else if (vec && cols <= 2048) TIA_LNSM(8);
+  else if (vec && cols <= 4096) TIA_LNSM(16);
+  else {
+    // Any other width or alignment: the two kernels, softmax in place on y.
+    const hipError_t e = layernorm_dispatch<float>(x, g, b, y, rows, cols, eps, st);
+    if (e != hipSuccess) return e;
+    return softmax_dispatch<float>(y, y, rows, cols, st);
+  }
+#undef TIA_LNSM
+  return hipGetLastError();
 }
 hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows, int cols,
                                      const uint16_t* bias, uint16_t* x, const uint16_t* gamma,
