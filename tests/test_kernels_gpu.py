@@ -239,7 +239,7 @@ def test_packed_gemv_single_row_parts(ops, k, n):
     close(h(hbits(res)), expect)
 
 
-@pytest.mark.parametrize("m,k,n", [(32, 1600, 8192), (24, 768, 50257), (32, 3072, 2048)])
+@pytest.mark.parametrize("m,k,n", [(32, 1600, 8192), (24, 768, 50257), (32, 3072, 2048), (32, 6400, 1600), (20, 1600, 4800)])
 def test_packed_gemv_column_block_groups(ops, m, k, n):
     """M in (16, 32] over a wide matrix: four column blocks share each A fragment,
     including a split longer than one round of loads (K = 1600 -> 25 chunks)."""

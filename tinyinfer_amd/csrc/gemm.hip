@@ -1271,14 +1271,18 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   return hipGetLastError();
 }
 
-// Launch shape of the packed GEMV (timed on MI355X over the GPT-2 decode
-// shapes, M = 1 and 32, K = 768 / 3072, N = 768 .. 50257):
+// Launch shape of the packed GEMV (timed on MI355X over the GPT-2 small and XL
+// decode shapes, M = 1 and 32, K = 768 .. 6400, N = 768 .. 50257):
 //  * W waves x CPW chunks per wave cover a split's K range with the fewest dead
 //    slots (a dead slot re-reads a chunk): 12 chunks -> 4 x 3, 16 -> 4 x 4,
 //    24 -> 8 x 3, 32 -> 8 x 4, 48 -> 16 x 3 (M <= 16);
 //  * at M > 16 every 16-column block re-reads A (4 KiB per chunk against 1 KiB
-//    of weights), and more than 8 waves only queue more A requests on one CU:
-//    longer ranges take several rounds of 8 x 2;
+//    of weights), so up to 16 chunks 4 waves suffice; longer ranges: 25
+//    chunks (K = 1600) over at least 200 column blocks as 16 x 2 with two
+//    blocks sharing each A fragment (1600 -> 4800 / 6400: 7.4 / 7.7 -> 6.4 /
+//    6.5 us), over fewer blocks 8 x 3 (1600 -> 1600: 4.9 -> 4.7 us); 48
+//    chunks (K = 3072) as 12 x 4 (3072 -> 768: 6.3 -> 6.0 us); more as
+//    rounds of 16 x 3 (6400 -> 1600: 10.6 -> 10.3 us);
 //  * at M > 16 two column blocks share each A fragment (CBG = 2) when that
 //    still leaves >= 512 workgroups (the LM head);
 //  * a deferred launch splits K to reach ~192 workgroups, keeping >= 4 chunks
@@ -1289,7 +1293,7 @@ struct GemvShape {
   int w, cpw, cbg;
 };
 
-GemvShape gemv_shape(int mt, int chunks, bool one_round) {
+GemvShape gemv_shape(int mt, int chunks, bool one_round, int nb) {
   if (chunks <= 12) return {4, 3, 1};
   if (chunks <= 16) return {4, 4, 1};
   if (one_round || mt == 1) {
@@ -1297,7 +1301,9 @@ GemvShape gemv_shape(int mt, int chunks, bool one_round) {
     if (chunks <= 32) return {8, 4, 1};
     if (mt == 1) return chunks <= 48 ? GemvShape{16, 3, 1} : GemvShape{16, 4, 1};
   }
-  return {8, 2, 1};
+  if (chunks <= 32) return nb >= 200 ? GemvShape{16, 2, 2} : GemvShape{8, 3, 1};
+  if (chunks <= 48) return {12, 4, 1};
+  return {16, 3, 1};
 }
 
 template <int MT, bool LNA, bool PA>
@@ -1319,7 +1325,11 @@ hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipS
     TIA_GEMV(16, 3, 1)
     TIA_GEMV(16, 4, 1)
   }
-  if constexpr (MT == 2 && !LNA) TIA_GEMV(8, 2, 1)
+  if constexpr (MT == 2 && !LNA) {
+    TIA_GEMV(16, 2, 2)
+    TIA_GEMV(12, 4, 1)
+    TIA_GEMV(16, 3, 1)
+  }
 #undef TIA_GEMV
   return hipErrorInvalidValue;
 }
@@ -1395,7 +1405,7 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
   p.splits = splits;
   if (p.defer && (!p.partials || size_t(splits) * g.m * g.n > s->partial_floats)) return hipErrorInvalidValue;
-  GemvShape sh = gemv_shape(MT, p.chunks_per_split, ln);
+  GemvShape sh = gemv_shape(MT, p.chunks_per_split, ln, p.nb);
   if (ln && sh.w * sh.cpw < p.kc) return hipErrorInvalidValue;
   if (MT == 2 && !p.defer && sh.w == 4 && (p.nb + 1) / 2 >= 512) sh.cbg = 2;
   const int grid = (p.nb + sh.cbg - 1) / sh.cbg * splits;
