@@ -1515,23 +1515,24 @@ __global__ void pack_w16_kernel(const int8_t* q, int64_t ldq, const float* scale
   out[t] = __builtin_bit_cast(u32x4_t, v);
 }
 
-// Tile (2 * MT * 16) x (2 * R * 16), 4 waves as 2 x 2, each MT x R MFMA blocks;
+// Tile (WM * MT * 16) x (WN * R * 16), WM x WN waves, each MT x R MFMA blocks;
 // K in chunks of 32 moved HBM/L2 -> LDS by global_load_lds_dwordx4 (A
 // fragments of 16 rows x 32 K in MFMA A order, B records as stored), S stages
 // as in the int8 panel kernel.  The epilogue runs from the accumulators.
-template <int MT, int R, int S>
-__global__ __launch_bounds__(256, 2) void f16_gemm_kernel(F16GemmParams p) {
-  constexpr int BM = 2 * MT * 16, BN = 2 * R * 16;
+template <int WM, int WN, int MT, int R, int S, int EP = 1, int OCC = 2>
+__global__ __launch_bounds__(WM * WN * 64, OCC) void f16_gemm_kernel(F16GemmParams p) {
+  constexpr int W = WM * WN, NT = W * 64;
+  constexpr int BM = WM * MT * 16, BN = WN * R * 16;
   constexpr int NA = BM / 16, NB = BN / 16, NL = NA + NB;
-  static_assert(NL % 4 == 0, "loads must split evenly over the waves");
-  constexpr int LPW = NL / 4;
+  static_assert(NL % W == 0, "loads must split evenly over the waves");
+  constexpr int LPW = NL / W;
   constexpr int STAGE = NL * 1024;
   static_assert(S >= 3 && (S - 2) * LPW < 64, "in-flight loads within vmcnt");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];  // max(S * STAGE, epilogue tile)
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   int split, tm, tn;
   tile_of_block(p.group_m, p.tiles_n, p.tiles, split, tm, tn);
   const int m0 = tm * BM, cb0 = tn * NB;
@@ -1564,7 +1565,7 @@ __global__ __launch_bounds__(256, 2) void f16_gemm_kernel(F16GemmParams p) {
   };
   // The epilogue gives thread t the outputs of tile column t % BN: its bias is
   // loaded now and used after the loop (a null bias reads A's first element).
-  static_assert(256 % BN == 0 || BN % 256 == 0, "epilogue column mapping");
+  static_assert(NT % BN == 0, "epilogue column mapping");
   const bool epi_now = p.splits == 1 && !p.defer;
   const bool has_bias = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias;
   const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
@@ -1596,37 +1597,45 @@ __global__ __launch_bounds__(256, 2) void f16_gemm_kernel(F16GemmParams p) {
   }
   wait_vmcnt<0>();
 
-  // Epilogue through an LDS fp32 tile [BM][BN + 1] (one epilogue call site,
-  // coalesced stores; the accumulators never meet the epilogue's registers).
-  __syncthreads();
+  // Epilogue through an LDS fp32 tile of BM / EP rows x (BN + 1), EP passes
+  // (one epilogue call site, coalesced stores; the accumulators never meet the
+  // epilogue's registers; EP = 2 halves the LDS the kernel needs).
+  constexpr int PR = BM / EP;  // rows per pass
+  static_assert(BM % EP == 0 && PR % 16 == 0, "whole 16-row blocks per pass");
   float* ctile = reinterpret_cast<float*>(lds);
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        ctile[((wm * MT + t) * 16 + 4 * g + v) * (BN + 1) + (wn * R + r) * 16 + j] = acc[t][r][v];
-  __syncthreads();
   const int cl = int(threadIdx.x % BN);
   const float bias = has_bias ? h2f(braw) : 0.f;
-  if (my_col < p.n) {
-    for (int rl = int(threadIdx.x / BN); rl < BM; rl += 256 / BN) {
-      const int row = m0 + rl;
-      if (row >= p.m) break;
-      const float val = ctile[rl * (BN + 1) + cl];
-      if (epi_now) apply_epilogue(p.epi, row, my_col, val, bias);
-      else p.partials[(int64_t(split) * p.m + row) * p.n + my_col] = val;
+#pragma unroll
+  for (int pass = 0; pass < EP; ++pass) {
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int rb = (wm * MT + t) * 16 - pass * PR;  // block row inside this pass
+      if (rb < 0 || rb >= PR) continue;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ctile[(rb + 4 * g + v) * (BN + 1) + (wn * R + r) * 16 + j] = acc[t][r][v];
+    }
+    __syncthreads();
+    if (my_col < p.n) {
+      for (int rl = int(threadIdx.x / BN); rl < PR; rl += NT / BN) {
+        const int row = m0 + pass * PR + rl;
+        if (row >= p.m) break;
+        const float val = ctile[rl * (BN + 1) + cl];
+        if (epi_now) apply_epilogue(p.epi, row, my_col, val, bias);
+        else p.partials[(int64_t(split) * p.m + row) * p.n + my_col] = val;
+      }
     }
   }
 }
 
-template <int MT, int R, int S>
+template <int WM, int WN, int MT, int R, int S, int EP = 1, int OCC = 2>
 hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
-  constexpr int BM = 2 * MT * 16, BN = 2 * R * 16;
+  constexpr int BM = WM * MT * 16, BN = WN * R * 16;
   constexpr int NL = BM / 16 + BN / 16;
-  constexpr size_t kLds = std::max(size_t(S) * NL * 1024, size_t(BM) * (BN + 1) * 4);
-  static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&f16_gemm_kernel<MT, R, S>),
+  constexpr size_t kLds = std::max(size_t(S) * NL * 1024, size_t(BM / EP) * (BN + 1) * 4);
+  static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds));
   if (attr != hipSuccess) return attr;
   F16GemmParams p{};
@@ -1648,7 +1657,8 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
   p.splits = splits;
   p.defer = deferred != nullptr && splits > 1;
   p.partials = s ? s->partials : nullptr;
-  hipLaunchKernelGGL((f16_gemm_kernel<MT, R, S>), dim3(unsigned(tiles * splits)), dim3(256), kLds, stream, p);
+  hipLaunchKernelGGL((f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC>), dim3(unsigned(tiles * splits)), dim3(WM * WN * 64),
+                     kLds, stream, p);
   if (p.defer) {
     *deferred = splits;
     return hipGetLastError();
@@ -1664,22 +1674,24 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
 
 // Tile choice over the fp16 records, and when they beat the int8 panel
 // kernel, from timings on MI355X (graph replays over rotating weights):
-// * 128 x 128 tiles win once K is long and the grid holds >= 384 of them
-//   (GPT-2 XL prefill, M = 10723: 1600->4800 306 us against 347 for int8
-//   panels, 1600->6400 388 against 456, 6400->1600 346 against 439; M = 8192
-//   3072->768 81 against 86);
-// * at K < 1536 the 128 x 128 epilogue and tail dominate (M = 8192, 768->2304
-//   101 us) and 64 x 64 tiles win (76 us; int8 panels 87), from M = 2048
-//   (768->2304 29 against 31 us); below that the two 64 x 64 kernels time the
-//   same and the int8 panels are kept.
+// * 128 x 128 tiles on 8 waves (each 64 x 32, 3 stages, the epilogue in 4
+//   passes of 32 rows so three workgroups fit a CU) once the grid holds >= 384
+//   of them, or >= 192 at K >= 1536: M = 8192 1600->6400 247 us (679 TF/s;
+//   4 waves of 64 x 64: 309 us), 768->2304 65 us (64 x 64 tiles: 76),
+//   3072->768 71 us (81); M = 4096 1600->4800 107 us (138); M = 2048
+//   1600->1600 35 us (41);
+// * below that, 64 x 64 tiles on 8 waves (each 32 x 16): M = 2048 768->2304
+//   27.5 us (4 waves: 29.3), 3072->768 37 us (40);
+// * the int8 panels stay for M < 2048 at K < 1536, where the two time the same.
 bool f16_gemm_large(int m, int n, int k) {
-  return k >= 1536 && int64_t((m + 127) / 128) * ((n + 127) / 128) >= 384;
+  const int64_t tiles = int64_t((m + 127) / 128) * ((n + 127) / 128);
+  return tiles >= 384 || (k >= 1536 && tiles >= 192);
 }
 bool f16_gemm_preferred(int m, int n, int k) { return f16_gemm_large(m, n, k) || (m >= 2048 && k < 1536); }
 
 hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
-  if (f16_gemm_large(g.m, g.n, g.k)) return launch_f16_cfg<4, 4, 4>(g, s, stream, deferred);
-  return launch_f16_cfg<2, 2, 4>(g, s, stream, deferred);
+  if (f16_gemm_large(g.m, g.n, g.k)) return launch_f16_cfg<2, 4, 4, 2, 3, 4, 3>(g, s, stream, deferred);
+  return launch_f16_cfg<2, 4, 2, 1, 3, 1, 3>(g, s, stream, deferred);
 }
 
 template <bool INT8>
