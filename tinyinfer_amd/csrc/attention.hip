@@ -366,8 +366,12 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
 // So a query's running max, sum and rescale stay in the four lanes (j, g) that
 // hold it (two cross-lane steps per tile for max and sum).  A workgroup of 4
 // waves takes 64 queries (16 per wave) and walks 64-key tiles of K and V through
-// double-buffered LDS (the next tile's global loads are in flight during the
-// current tile's MFMAs), stopping at the last key any of its queries may see.
+// double-buffered LDS, stopping at the last key any of its queries may see.
+// The global loads of the next two tiles are in flight during a tile's MFMAs
+// (one tile ahead left every tile waiting a full memory round trip).  Staging
+// gives each wave instruction 64 consecutive keys of one 8-dim segment, so the
+// transposed V stores fill whole LDS rows (8 dims per lane over 8 keys made
+// them 8-way bank conflicts, two thirds of the kernel's LDS cycles).
 // Numerics: scores, max, sum and accumulation in fp32 (exponentials in base 2
 // of the log2(e)-scaled scores), probabilities rounded to fp16 for the PV
 // product; rows with no visible key, and padded queries, are exactly zero.
@@ -409,25 +413,29 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
     }
   }
 
-  // Cooperative tile staging: piece r of thread t is key (t + 256 r) / SEGS,
-  // 8 dims at ((t + 256 r) % SEGS) * 8; keys past key_end re-read key_end - 1.
-  half8_t kr[PIECES], vr[PIECES];
-  auto load_tile = [&](int t) {
+  // Cooperative tile staging: piece r of thread t is key (t + 256 r) % BT
+  // (the lane), 8 dims at ((t + 256 r) / BT) * 8 (uniform in a wave); keys past
+  // key_end re-read key_end - 1.  Two register sets hold the next two tiles.
+  struct Staged {
+    half8_t k[PIECES], v[PIECES];
+  };
+  Staged st0, st1;
+  auto load_tile = [&](Staged& r_, int t) {
 #pragma unroll
     for (int r = 0; r < PIECES; ++r) {
-      const int piece = threadIdx.x + 256 * r, key = piece / SEGS, seg = piece % SEGS;
+      const int piece = threadIdx.x + 256 * r, key = piece % BT, seg = piece / BT;
       const int64_t kk = min(t * BT + key, key_end - 1);
-      kr[r] = *reinterpret_cast<const half8_t*>(kbase + kk * D + 8 * seg);
-      vr[r] = *reinterpret_cast<const half8_t*>(vbase + kk * D + 8 * seg);
+      r_.k[r] = *reinterpret_cast<const half8_t*>(kbase + kk * D + 8 * seg);
+      r_.v[r] = *reinterpret_cast<const half8_t*>(vbase + kk * D + 8 * seg);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](const Staged& r_, int buf) {
 #pragma unroll
     for (int r = 0; r < PIECES; ++r) {
-      const int piece = threadIdx.x + 256 * r, key = piece / SEGS, seg = piece % SEGS;
-      *reinterpret_cast<half8_t*>(&ks[buf][key][8 * seg]) = kr[r];
+      const int piece = threadIdx.x + 256 * r, key = piece % BT, seg = piece / BT;
+      *reinterpret_cast<half8_t*>(&ks[buf][key][8 * seg]) = r_.k[r];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vt[buf][8 * seg + e][key] = vr[r][e];
+      for (int e = 0; e < 8; ++e) vt[buf][8 * seg + e][key] = r_.v[r][e];
     }
   };
 
@@ -436,14 +444,19 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
 #pragma unroll
   for (int d = 0; d < D / 16; ++d) acc[d] = float4_t{0.f, 0.f, 0.f, 0.f};
 
+  // Tile t sits in LDS buffer t & 1; its registers were set t & 1 (st0 / st1).
   if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
+    load_tile(st0, 0);
+    store_tile(st0, 0);
   }
-  for (int t = 0; t < ntiles; ++t) {
+  if (ntiles > 1) load_tile(st1, 1);
+  if (ntiles > 2) load_tile(st0, 2);
+  __syncthreads();
+  // One tile: the math on buffer t & 1, then tile t + 1 from its registers into
+  // the other buffer (its loads were issued two tiles ago), then the loads of
+  // tile t + 3 into the registers just freed.
+  auto step = [&](int t, Staged& next) {
     const int buf = t & 1;
-    if (t + 1 < ntiles) load_tile(t + 1);
     // This wave's queries see nothing of this tile: skip the math, keep the barriers.
     const int wave_end = int(min<int64_t>(kvv, a.causal ? off + min(q0 + 16 * wave + 15, q_valid - 1) + 1 : kvv));
     if (q0 + 16 * wave < q_valid && t * BT < wave_end) {
@@ -515,8 +528,13 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
           acc[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pt[kb], acc[d], 0, 0, 0);
         }
     }
-    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    if (t + 1 < ntiles) store_tile(next, buf ^ 1);
     __syncthreads();
+    if (t + 3 < ntiles) load_tile(next, t + 3);
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, st1);
+    if (t + 1 < ntiles) step(t + 1, st0);
   }
 
   if (my_q >= a.q_len) return;
