@@ -54,9 +54,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--part", default="all",
-                   choices=["all", "decode", "gemv", "kernels", "roofline", "copy", "limits", "xl"],
+                   choices=["all", "decode", "gemv", "kernels", "roofline", "copy", "limits", "prefill", "xl"],
                    help="run one part only (for profiler passes; 'roofline' = the dominant GEMV shape only, "
                         "'copy' = a 512 MiB device copy used to calibrate the HBM byte counters, "
+                        "'prefill' = the XL-shaped fp16-record prefill GEMM and the prefill attention cases only, "
                         "'xl' = configs[4] GPT-2 XL, not part of 'all': its synthetic artifact takes ~2 min "
                         "to write); the driver's JSON line needs 'all'")
     return p.parse_args()
@@ -495,9 +496,13 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "copies": 4}))
         return
-    rp = Replay() if args.part in ("all", "gemv", "kernels", "roofline", "limits") else None
+    rp = Replay() if args.part in ("all", "gemv", "kernels", "roofline", "limits", "prefill") else None
     if args.part == "limits":
         print(json.dumps({"limits": run_limits(rp)}))
+        return
+    if args.part == "prefill":
+        print(json.dumps({"gemm_prefill_f16_packed": run_gemm(rp, ((8192, 1600, 6400),), packed="w16"),
+                          "prefill_attention": run_prefill_attention(rp)}), flush=True)
         return
     if args.part == "roofline":
         print(json.dumps({"roofline_gemv": run_gemm(rp, ((1, 3072, 768),), packed=True)}))

@@ -513,6 +513,26 @@ def test_attention_prefill_and_long(ops, nq, nk):
     close(h(hbits(out)), h(oracle.attention_f16(q, k, v, ql, kl, off, True)))
 
 
+@pytest.mark.parametrize("causal", [0, 1])
+def test_attention_prefill_many_tiles(ops, causal):
+    """More than 512 query tiles (8 x 12 x 6 = 576 workgroups) take the 4-wave
+    prefill kernel, fewer the 8-wave key-split one (covered above); ragged
+    per-request lengths, offsets and a request with no query."""
+    t = torch()
+    rng = np.random.default_rng(21 + causal)
+    B, H, D, nq, nk = 8, 12, 64, 384, 420
+    ql = [384, 300, 1, 0, 129, 384, 64, 250]
+    kl = [420, 310, 5, 17, 129, 384, 400, 251]
+    off = [max(0, kv - qv) for qv, kv in zip(ql, kl)]
+    q = f16(rng.standard_normal((B, H, nq, D)) * 0.5)
+    k = f16(rng.standard_normal((B, H, nk, D)) * 0.5)
+    v = f16(rng.standard_normal((B, H, nk, D)))
+    say("attention prefill many tiles", causal)
+    out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
+                        kv_lengths=kl, query_offsets=off, causal=bool(causal))
+    close(h(hbits(out)), h(oracle.attention_f16(q, k, v, ql, kl, off, bool(causal))))
+
+
 # ---------------------------------------------------------------- row ops fp16
 @pytest.mark.parametrize("cols", [1, 7, 257, 768, 3072, 5000])
 def test_layernorm_gelu_softmax_f16(ops, cols):

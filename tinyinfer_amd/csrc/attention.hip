@@ -375,32 +375,38 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
 // Numerics: scores, max, sum and accumulation in fp32 (exponentials in base 2
 // of the log2(e)-scaled scores), probabilities rounded to fp16 for the PV
 // product; rows with no visible key, and padded queries, are exactly zero.
-template <int D>
-__global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
+template <int D, int KS>
+__global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
   constexpr int BQ = 64, BT = 64, KP = D + 8, VP = BT + 8;
   constexpr int SEGS = D / 8;                 // 16-byte pieces per key row
   constexpr int PIECES = BT * SEGS / 256;     // per thread per tile (2 or 4)
-  __shared__ __attribute__((aligned(16))) f16 ks[2][BT][KP];
-  __shared__ __attribute__((aligned(16))) f16 vt[2][D][VP];
+  // Dynamic LDS: [2 buffers][KS tiles] of K rows, then of transposed V.
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
+  auto ks = reinterpret_cast<f16(*)[KS][BT][KP]>(lds_raw);
+  auto vt = reinterpret_cast<f16(*)[KS][D][VP]>(lds_raw + 2 * KS * BT * KP * sizeof(f16));
   const AttnArgs& a = p.a;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // KS = 2: waves 4..7 are a second key group taking the odd tiles of each
+  // step; each group stages its own tile and the two merge at the end.
+  const int grp = wave >> 2, qw = wave & 3, gt = int(threadIdx.x & 255);
   const int j = lane & 15, g = lane >> 4;
   const int h = blockIdx.y, b = blockIdx.z, q0 = blockIdx.x * BQ;
 
   const int q_valid = max(0, min(a.q_len, a.q_lengths[b]));
   const int64_t off = a.offsets ? int64_t(a.offsets[b]) : 0;
   const int kvv = int(a.kv_from_offsets ? off + q_valid : max(0, min(a.kv_len, a.kv_lengths[b])));
-  const int my_q = q0 + 16 * wave + j;
+  const int my_q = q0 + 16 * qw + j;
   const int last_q = min(q0 + BQ, q_valid) - 1;
   const int key_end = last_q < q0 ? 0 : int(min<int64_t>(kvv, a.causal ? off + last_q + 1 : kvv));
   const int ntiles = (key_end + BT - 1) / BT;
+  const int nsteps = (ntiles + KS - 1) / KS;
   const int64_t slot = a.kv_slot ? int64_t(a.kv_slot[b]) : int64_t(b);
   const uint16_t* kbase = a.k + slot * a.kv_sb + int64_t(h) * a.kv_sh;
   const uint16_t* vbase = a.v + slot * a.kv_sb + int64_t(h) * a.kv_sh;
   // Query my_q sees keys [0, my_end); every valid query of this wave sees at
   // least [0, my_end_min) (its first query's range), so tiles below that need no mask.
   const int my_end = my_q < q_valid ? int(min<int64_t>(kvv, a.causal ? off + my_q + 1 : kvv)) : 0;
-  const int wq0 = q0 + 16 * wave;
+  const int wq0 = q0 + 16 * qw;
   const int my_end_min = (wq0 + 15 < q_valid) ? int(min<int64_t>(kvv, a.causal ? off + wq0 + 1 : kvv)) : 0;
 
   half8_t qf[D / 32];
@@ -413,17 +419,19 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
     }
   }
 
-  // Cooperative tile staging: piece r of thread t is key (t + 256 r) % BT
-  // (the lane), 8 dims at ((t + 256 r) / BT) * 8 (uniform in a wave); keys past
-  // key_end re-read key_end - 1.  Two register sets hold the next two tiles.
+  // Cooperative tile staging: each group of 256 threads stages its tile of a
+  // step; piece r of group thread t is key (t + 256 r) % BT (the lane), 8 dims
+  // at ((t + 256 r) / BT) * 8 (uniform in a wave); keys past key_end re-read
+  // key_end - 1.  Two register sets hold the next two steps.
   struct Staged {
     half8_t k[PIECES], v[PIECES];
   };
   Staged st0, st1;
-  auto load_tile = [&](Staged& r_, int t) {
+  auto load_tile = [&](Staged& r_, int step) {
+    const int t = step * KS + grp;
 #pragma unroll
     for (int r = 0; r < PIECES; ++r) {
-      const int piece = threadIdx.x + 256 * r, key = piece % BT, seg = piece / BT;
+      const int piece = gt + 256 * r, key = piece % BT, seg = piece / BT;
       const int64_t kk = min(t * BT + key, key_end - 1);
       r_.k[r] = *reinterpret_cast<const half8_t*>(kbase + kk * D + 8 * seg);
       r_.v[r] = *reinterpret_cast<const half8_t*>(vbase + kk * D + 8 * seg);
@@ -432,10 +440,10 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
   auto store_tile = [&](const Staged& r_, int buf) {
 #pragma unroll
     for (int r = 0; r < PIECES; ++r) {
-      const int piece = threadIdx.x + 256 * r, key = piece % BT, seg = piece / BT;
-      *reinterpret_cast<half8_t*>(&ks[buf][key][8 * seg]) = r_.k[r];
+      const int piece = gt + 256 * r, key = piece % BT, seg = piece / BT;
+      *reinterpret_cast<half8_t*>(&ks[buf][grp][key][8 * seg]) = r_.k[r];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vt[buf][8 * seg + e][key] = r_.v[r][e];
+      for (int e = 0; e < 8; ++e) vt[buf][grp][8 * seg + e][key] = r_.v[r][e];
     }
   };
 
@@ -444,29 +452,30 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
 #pragma unroll
   for (int d = 0; d < D / 16; ++d) acc[d] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Tile t sits in LDS buffer t & 1; its registers were set t & 1 (st0 / st1).
-  if (ntiles > 0) {
+  // Step s (tiles s * KS + group) sits in LDS buffer s & 1; its registers were
+  // set s & 1 (st0 / st1).
+  if (nsteps > 0) {
     load_tile(st0, 0);
     store_tile(st0, 0);
   }
-  if (ntiles > 1) load_tile(st1, 1);
-  if (ntiles > 2) load_tile(st0, 2);
+  if (nsteps > 1) load_tile(st1, 1);
+  if (nsteps > 2) load_tile(st0, 2);
   __syncthreads();
-  // One tile: the math on buffer t & 1, then tile t + 1 from its registers into
-  // the other buffer (its loads were issued two tiles ago), then the loads of
-  // tile t + 3 into the registers just freed.
-  auto step = [&](int t, Staged& next) {
-    const int buf = t & 1;
+  // One step: the math on buffer s & 1, then step s + 1 from its registers into
+  // the other buffer (its loads were issued two steps ago), then the loads of
+  // step s + 3 into the registers just freed.
+  auto step = [&](int s_, Staged& next) {
+    const int buf = s_ & 1, t = s_ * KS + grp;
     // This wave's queries see nothing of this tile: skip the math, keep the barriers.
-    const int wave_end = int(min<int64_t>(kvv, a.causal ? off + min(q0 + 16 * wave + 15, q_valid - 1) + 1 : kvv));
-    if (q0 + 16 * wave < q_valid && t * BT < wave_end) {
+    const int wave_end = int(min<int64_t>(kvv, a.causal ? off + min(q0 + 16 * qw + 15, q_valid - 1) + 1 : kvv));
+    if (t < ntiles && q0 + 16 * qw < q_valid && t * BT < wave_end) {
       float4_t sc[4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         sc[kb] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < D / 32; ++s) {
-          const half8_t kf = *reinterpret_cast<const half8_t*>(&ks[buf][16 * kb + j][32 * s + 8 * g]);
+          const half8_t kf = *reinterpret_cast<const half8_t*>(&ks[buf][grp][16 * kb + j][32 * s + 8 * g]);
           sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sc[kb], 0, 0, 0);
         }
       }
@@ -524,17 +533,43 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnParams p) {
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int d = 0; d < D / 16; ++d) {
-          const half4_t vf = *reinterpret_cast<const half4_t*>(&vt[buf][16 * d + j][16 * kb + 4 * g]);
+          const half4_t vf = *reinterpret_cast<const half4_t*>(&vt[buf][grp][16 * d + j][16 * kb + 4 * g]);
           acc[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pt[kb], acc[d], 0, 0, 0);
         }
     }
-    if (t + 1 < ntiles) store_tile(next, buf ^ 1);
+    if (s_ + 1 < nsteps) store_tile(next, buf ^ 1);
     __syncthreads();
-    if (t + 3 < ntiles) load_tile(next, t + 3);
+    if (s_ + 3 < nsteps) load_tile(next, s_ + 3);
   };
-  for (int t = 0; t < ntiles; t += 2) {
-    step(t, st1);
-    if (t + 1 < ntiles) step(t + 1, st0);
+  for (int s_ = 0; s_ < nsteps; s_ += 2) {
+    step(s_, st1);
+    if (s_ + 1 < nsteps) step(s_ + 1, st0);
+  }
+  if constexpr (KS == 2) {
+    // Group 1 hands its (m, l, acc) per lane to group 0 through LDS (free after
+    // the last barrier); group 0 merges on the larger reference: the states
+    // are sums of 2^(x - m).
+    constexpr int PER = D / 16 * 4 + 2;
+    float* xs = reinterpret_cast<float*>(lds_raw) + (qw * 64 + lane) * PER;
+    if (grp == 1) {
+#pragma unroll
+      for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xs[4 * d + v] = acc[d][v];
+      xs[PER - 2] = m;
+      xs[PER - 1] = l;
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float m1 = xs[PER - 2], l1 = xs[PER - 1];
+    const float nm = fmaxf(l > 0.f ? m : kNegInf, l1 > 0.f ? m1 : kNegInf);
+    const float f0 = l > 0.f ? __builtin_amdgcn_exp2f(m - nm) : 0.f;
+    const float f1 = l1 > 0.f ? __builtin_amdgcn_exp2f(m1 - nm) : 0.f;
+    l = l * f0 + l1 * f1;
+#pragma unroll
+    for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[d][v] = acc[d][v] * f0 + xs[4 * d + v] * f1;
   }
 
   if (my_q >= a.q_len) return;
@@ -597,7 +632,24 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
     dim3 grid = blocks_per;
     if constexpr (VEC) {
       grid.x = unsigned((a.q_len + 63) / 64);
-      hipLaunchKernelGGL((prefill_mfma_kernel<D>), grid, dim3(256), 0, stream, p);
+      // Few query tiles (<= 512 workgroups, e.g. one long sequence of a few
+      // heads): 8 waves per tile in two key groups, so each SIMD holds two waves
+      // (causal B1 H4 4096^2: 75 -> 54 us, B1 H12 2048^2: 54 -> 48 us); from
+      // 768 workgroups the 4-wave kernel is as fast or faster (B8 H12 512^2:
+      // 26 against 28 us, B32 H25 320^2: 55 against 65 us).
+      const int64_t wgs = int64_t(grid.x) * grid.y * grid.z;
+      constexpr size_t lds1 = 2 * 64 * (D + 8) * 2 + 2 * D * (64 + 8) * 2;
+      if (wgs <= 512) {
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, 2>),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(2 * lds1));
+        if (attr != hipSuccess) return attr;
+        hipLaunchKernelGGL((prefill_mfma_kernel<D, 2>), grid, dim3(512), 2 * lds1, stream, p);
+      } else {
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, 1>),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds1));
+        if (attr != hipSuccess) return attr;
+        hipLaunchKernelGGL((prefill_mfma_kernel<D, 1>), grid, dim3(256), lds1, stream, p);
+      }
     } else {
       grid.x = unsigned((a.q_len + 3) / 4);
       hipLaunchKernelGGL((attention_kernel<D, 4, 1, VEC>), grid, dim3(256), 0, stream, p);
