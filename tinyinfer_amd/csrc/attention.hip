@@ -479,7 +479,9 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
           sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sc[kb], 0, 0, 0);
         }
       }
-      // Scores in base 2: x = s * D^-1/2 * log2(e), p = 2^(x - ref).  Keys past a
+      // Scores in base 2: x = s * D^-1/2 * log2(e), p = 2^(x - ref), the scaling
+      // folded into the exponent's fma (the maximum is taken on the raw scores:
+      // scaling by a positive constant keeps their order).  Keys past a
       // query's end are masked only on tiles that reach some query's end (a
       // wave-uniform test).  The reference ref is raised only when a score
       // exceeds it by more than 8 (p <= 256 stays exact enough in fp16 and the
@@ -490,22 +492,19 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            sc[kb][v] *= l2s;
-            tmax = fmaxf(tmax, sc[kb][v]);
-          }
+          for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[kb][v]);
       } else {
         const int lim = my_end - t * BT - 4 * g;  // key 16 kb + v of this lane is visible iff < lim
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            sc[kb][v] = 16 * kb + v < lim ? sc[kb][v] * l2s : kNegInf;
+            sc[kb][v] = 16 * kb + v < lim ? sc[kb][v] : kNegInf;
             tmax = fmaxf(tmax, sc[kb][v]);
           }
       }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * l2s;
       const bool raise = tmax > m + 8.f;
       if (__ballot(raise)) {
         const float nref = raise ? tmax : m;
@@ -522,7 +521,7 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float pr = __builtin_amdgcn_exp2f(sc[kb][v] - base);
+          const float pr = __builtin_amdgcn_exp2f(fmaf(sc[kb][v], l2s, -base));
           pt[kb][v] = f16r(pr);
           psum += pr;
         }
