@@ -239,6 +239,27 @@ def test_packed_gemv_single_row_parts(ops, k, n):
     close(h(hbits(res)), expect)
 
 
+@pytest.mark.parametrize("m,k,n", [(1024, 768, 768), (512, 768, 3072)])
+def test_panel_and_f16_record_gemm_agree_bitwise(ops, m, k, n):
+    """Unsplit, the int8 panel GEMM and the fp16-record GEMM run the same MFMA
+    sequence over the same weight values: their outputs are equal bit for bit
+    (the runtime's batch-invariant prefill takes either, by shape)."""
+    t = torch()
+    rng = np.random.default_rng(m + k + n)
+    a = f16(rng.standard_normal((m, k)))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("panel vs f16 records", m, k, n)
+    ad, qd, sd, bd = dev(a, t.float16), dev(q), dev(s), dev(bias, t.float16)
+    packed, packed16 = _pack_gpu(ops.lib, qd, k, n), _pack16_gpu(ops.lib, qd, sd, k, n)
+    y8 = t.empty((m, n), dtype=t.float16, device="cuda")
+    y16 = t.empty((m, n), dtype=t.float16, device="cuda")
+    _packed(ops.lib, ad, packed, sd, bd, y8, None, m, n, k, 1)
+    assert _w16(ops.lib, ad, packed16, bd, y16, None, m, n, k, 1) == 0
+    assert np.array_equal(hbits(y8), hbits(y16))
+
+
 @pytest.mark.parametrize("m,k,n", [(32, 1600, 8192), (24, 768, 50257), (32, 3072, 2048), (32, 6400, 1600), (20, 1600, 4800)])
 def test_packed_gemv_column_block_groups(ops, m, k, n):
     """M in (16, 32] over a wide matrix: four column blocks share each A fragment,

@@ -222,6 +222,27 @@ def test_decode_graph_equals_eager(model):
     model.reset_all()
 
 
+@pytest.mark.parametrize("others", [1, 4, 15])
+def test_prefill_and_decode_are_batch_invariant(model, others):
+    """A request's logits do not depend on the batch it runs in: its prompt
+    prefilled alone or beside others of other lengths (rows of the prefill GEMMs
+    and attention summed in one order whatever the batch), then decode steps of
+    1 to 16 rows.  The epoll server batches requests as they arrive and its
+    greedy output must equal direct greedy decoding."""
+    ids = token_ids(24, seed=11)
+    rows = [token_ids(5 + 3 * i, seed=100 + i) for i in range(others)]
+    say("batch invariance", others)
+    model.reset_all()
+    alone = logits_of(model.forward([0], [ids]))[0]
+    batched = logits_of(model.forward(list(range(1, others + 2)), [ids] + rows))[0]
+    assert np.array_equal(alone, batched)
+    for tok in (ids[-1], 7, 50000):
+        alone = logits_of(model.forward([0], [[tok]]))[0]
+        batched = logits_of(model.forward(list(range(1, others + 2)), [[tok]] + [[3]] * others))[0]
+        assert np.array_equal(alone, batched)
+    model.reset_all()
+
+
 def first_divergence(a, b):
     for i, (x, y) in enumerate(zip(a, b)):
         if x != y:

@@ -591,13 +591,13 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
     // Decode: one workgroup per (b, h) whose KW waves split the keys.  Each
     // wave keeps at least 4 tiles of 32/16 keys (two double-buffered rounds;
     // fewer make the LDS merge of the waves cost more than the parallelism
-    // gains), and at most ~4096 waves in total (timed on GPT-2 small, 96 keys:
-    // KW 1; GPT-2 XL, 640 keys and 800 heads: KW 4).
+    // gains; timed on GPT-2 small, 96 keys: KW 1; GPT-2 XL, 640 keys and 800
+    // heads: KW 4).  KW follows the cache length only, not the batch, so a
+    // request's result does not depend on the requests decoded with it.
     const int tile_keys = D == 64 ? 32 : 16;
     const int tiles = (a.kv_len + tile_keys - 1) / tile_keys;
-    const int64_t groups = int64_t(a.batch) * a.heads;
     int kw = 1;
-    while (kw < 8 && kw * 2 * 4 <= tiles && groups * kw * 2 <= 4096) kw *= 2;
+    while (kw < 8 && kw * 2 * 4 <= tiles) kw *= 2;
     dim3 grid = blocks_per;
     grid.x = 1;
     if (p.parts) {
@@ -636,9 +636,11 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
       // (causal B1 H4 4096^2: 75 -> 54 us, B1 H12 2048^2: 54 -> 48 us); from
       // 768 workgroups the 4-wave kernel is as fast or faster (B8 H12 512^2:
       // 26 against 28 us, B32 H25 320^2: 55 against 65 us).
+      // batch_invariant (the runtime's prefill) always takes the key-split
+      // kernel, so a query's sums never depend on the grid.
       const int64_t wgs = int64_t(grid.x) * grid.y * grid.z;
       constexpr size_t lds1 = 2 * 64 * (D + 8) * 2 + 2 * D * (64 + 8) * 2;
-      if (wgs <= 512) {
+      if (wgs <= 512 || a.batch_invariant) {
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, 2>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, int(2 * lds1));
         if (attr != hipSuccess) return attr;

@@ -78,6 +78,12 @@ struct GemmArgs {
   const uint16_t* ln_gamma = nullptr;
   const uint16_t* ln_beta = nullptr;
   float ln_eps = 1e-5f;
+  // Batch-invariant sums (packed int8 or fp16-record weights): every
+  // output element is accumulated in one order whatever M is -- K in 32-row
+  // MFMA steps from 0 upward, no split-K -- so a prompt's rows come out the same
+  // whether it is prefilled alone or beside others (the int8 panel and fp16
+  // record kernels then agree bit for bit).
+  bool canonical = false;
   Epilogue epi;
 };
 // out[row] = the column of the largest value over the groups' partials (lowest
@@ -157,6 +163,9 @@ struct AttnArgs {
   // Output row b * q_len + qi, columns h * head_dim + d, written P32
   // fragment-packed (rows < 32, heads * head_dim % 64 == 0); o_* ignored.
   bool out_p32 = false;
+  // Several queries per request: one kernel variant whatever the grid, so a
+  // query's result does not depend on the other requests of the call.
+  bool batch_invariant = false;
 };
 // With a scratch, single-query attention over a long cache (kv_len 512 ..
 // 4096 for head_dim 64, 256 .. 2048 for 128) splits the keys of each (b, h)

@@ -482,8 +482,17 @@ struct ti_llm_model {
     g.ln_beta = ln_b;
     g.ln_eps = 1e-5f;
     g.epi = epi;
+    g.canonical = prefill_pass;
     ck(tia::gemm(g, &scratch, stream, deferred));
   }
+
+  // Set for the GEMMs of a prefill pass (several tokens per request) and the head
+  // over its last rows: their rows are then summed in one order whatever the
+  // batch (tia::GemmArgs::canonical), so a prompt decodes the same alone or
+  // beside others, as the reference runtime does (the epoll server batches
+  // prompts as they arrive).  Decode GEMVs of 1..16 rows are batch-invariant by
+  // construction (one kernel and one K split per shape for every M up to 16).
+  bool prefill_pass = false;
 
   // x += a @ w + bias (fp16 rounding points of reference runtime.cu:149/153), then
   // norm = LayerNorm(x; g, beta).  Decode-sized GEMMs leave split-K partials that
@@ -534,6 +543,7 @@ struct ti_llm_model {
   // (both P32 fragment-packed after an ln_fused pass, row-major otherwise).
   void layers(int b, int qlen) {
     const int rows = b * qlen;
+    prefill_pass = qlen > 1;
     const bool fuse = ln_fused(b, qlen);
     // Fragment-packed activations from two rows up: a single row reads one
     // cache line per A fragment either way, and its row-major output writes
@@ -612,6 +622,7 @@ struct ti_llm_model {
       at.head_dim = kHeadDim;
       at.causal = true;
       at.out_p32 = p32;
+      at.batch_invariant = true;
       ck(tia::attention(at, stream));
 
       tia::Epilogue gl;
