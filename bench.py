@@ -8,9 +8,11 @@ achieved HBM GB/s".
   seeded prompt ids per request, 64 new tokens, rate B*(new-1)/(t_last-t_first)
   as reference llm/evaluate.py:195 defines it.  One "step" is one such greedy
   batch; batch 1 is reported beside it.
-* roofline: the W8A16 decode GEMV over the runtime's panel-packed int8 weights
-  (one kernel, M=1, K=3072 -> N=768, fused bias+GELU: gemv_part_kernel, 96
-  workgroups of 8 waves, 8 output columns each) replayed back-to-back from
+* roofline: the standalone W8A16 GEMV of configs[1] at M=1 over the panel-packed
+  int8 layout (ti_amd_gemm_w8p_fused; one kernel, K=3072 -> N=768, fused
+  bias+GELU: gemv_part_kernel, 96 workgroups of 8 waves, 8 output columns each;
+  the runtime's decode keeps the 16-row MFMA GEMV at every batch size so its
+  results do not depend on the batch) replayed back-to-back from
   a HIP graph over >= 600 MiB of distinct weight sets (beyond the 256 MiB
   Infinity Cache), timed with HIP events on the launch stream; algorithmic bytes
   2MK + KN + 4N + 2N + 2MN.  gemv adds the other configs[1] M <= 8 shapes and

@@ -7,9 +7,10 @@
 //    loads of a wave are in flight before its first wait, the waves of a
 //    workgroup split K and reduce through LDS, and the epilogue runs in the
 //    same kernel (K is split across workgroups only when the caller finishes
-//    the partials itself).  Up to 16 rows over at most 2048 columns take the
-//    part-block kernel instead: no MFMA, 8 columns per workgroup (twice the
-//    workgroups of the 16-column MFMA blocks), one workgroup row per A row.
+//    the partials itself).  A single row (M = 1) over at most 2048 columns
+//    takes the part-block kernel instead when the caller does not batch rows
+//    (standalone GEMV calls): no MFMA, 8 columns per workgroup, twice the
+//    workgroups of the 16-column MFMA blocks.
 //  * skinny (M <= 32, row-major weights of the ABI): every wave streams weight fragments straight from
 //    HBM into MFMA B-operand registers (no LDS for weights), dequantises them in
 //    registers as fp16_rn(float(q) * scale[n]) and runs v_mfma_f32_16x16x32_f16
@@ -628,10 +629,8 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Part-block GEMV, one row of A per workgroup row (blockIdx.y), over the
-// panel-packed weights, without MFMA.  Every row is summed by the same code in
-// the same order whatever M is, so a request's results do not depend on the
-// batch it is decoded in.  A workgroup owns QC in {4, 8} columns of a 16-column block, so
+// Part-block GEMV for a single row of A (M = 1) over the panel-packed weights,
+// without MFMA.  A workgroup owns QC in {4, 8} columns of a 16-column block, so
 // N = 768 runs on 96 (QC 8) or 192 (QC 4) workgroups instead of 48, each
 // streaming a part of the bytes (a single-row product has no use for the
 // 16-row MFMA shape).  QC 4 reads half cache lines and measured slower; the
@@ -645,14 +644,14 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 // sums go to partials split 0 for a deferred launch).  Wave w takes record
 // steps w, w + W, ... and issues LPW of them before the first wait; records
 // past the end are clamped to the last one and weighted 0.
-template <int W, int LPW, int QC, bool PA>
+template <int W, int LPW, int QC>
 __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
   static_assert(QC == 4 || QC == 8, "4 or 8 columns per workgroup");
   constexpr int RPL = 16 / QC;  // records per wave load
   __shared__ float red[W][QC];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane % QC, g = (lane / QC) & 3, r = lane / (4 * QC);
-  const int cb = blockIdx.x / RPL, h = blockIdx.x % RPL, row = blockIdx.y;
+  const int cb = blockIdx.x / RPL, h = blockIdx.x % RPL;
   const int col = cb * 16 + QC * h + c;
   const bool epi_now = !p.defer;
   const bool has_bias = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias;
@@ -661,13 +660,10 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
   // first and unconditionally (A's first element stands in), converted at use.
   const int ecol = min(cb * 16 + QC * h + int(threadIdx.x % QC), p.n - 1);
   const uint16_t bias_raw = (has_bias ? p.epi.bias : p.a)[has_bias ? ecol : 0];
-  const uint16_t res_raw = (has_res ? p.epi.residual : p.a)[has_res ? r_off(p.epi, row, ecol) : 0];
+  const uint16_t res_raw = (has_res ? p.epi.residual : p.a)[has_res ? r_off(p.epi, 0, ecol) : 0];
   const float scale = p.scales[min(col, p.n - 1)] * (col < p.n ? 1.f : 0.f);
   const u32x4_t* wb = p.w + int64_t(cb) * p.kc * 64 + g * 16 + QC * h + c;
-  // 8 consecutive K elements of a row are contiguous in both A layouts.
-  auto a8 = [&](int k) {
-    return *reinterpret_cast<const half8_t*>(p.a + (PA ? p32_off(row, k) : int64_t(row) * p.lda + k));
-  };
+  const uint16_t* arow = p.a + 8 * g;
   const int steps = (p.kc + RPL - 1) / RPL;
   float acc = 0.f;
   for (int s0 = wave; s0 < steps; s0 += W * LPW) {
@@ -677,8 +673,8 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
     for (int i = 0; i < LPW; ++i) {
       const int kc = min(RPL * min(s0 + i * W, steps - 1) + r, p.kc - 1);
       wf[i] = __builtin_nontemporal_load(wb + int64_t(kc) * 64);
-      af[i][0] = a8(kc * 64 + 8 * g);
-      af[i][1] = a8(kc * 64 + 32 + 8 * g);
+      af[i][0] = *reinterpret_cast<const half8_t*>(arow + kc * 64);
+      af[i][1] = *reinterpret_cast<const half8_t*>(arow + kc * 64 + 32);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -702,8 +698,8 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
   float s = 0.f;
 #pragma unroll
   for (int w = 0; w < W; ++w) s += red[w][threadIdx.x];
-  if (epi_now) apply_epilogue(p.epi, row, ecol, s, has_bias ? h2f(bias_raw) : 0.f, has_res ? h2f(res_raw) : 0.f);
-  else p.partials[int64_t(row) * p.n + ecol] = s;
+  if (epi_now) apply_epilogue(p.epi, 0, ecol, s, has_bias ? h2f(bias_raw) : 0.f, has_res ? h2f(res_raw) : 0.f);
+  else p.partials[ecol] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -1339,41 +1335,37 @@ hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipS
   return hipErrorInvalidValue;
 }
 
-// M <= 16 rows over packed weights with at most 128 column blocks (N <= 2048):
-// the part-block kernel, 8 columns per workgroup, one workgroup row per A row.
-// W x LPW covers the record pairs in one round up to K = 3072 (timed at M = 1
-// on GPT-2 small / XL shapes: 768 -> 768 3.07 -> 2.73 us, 3072 -> 768 4.37 ->
-// 3.30 us, 1600 -> 1600 3.95 -> 3.07 us against the MFMA GEMV; at 2304
-// columns and more the MFMA GEMV is as fast or faster and takes every M).
-// Using it for every M up to 16, not only M = 1, keeps a row's sums the same
-// for every batch size of a decode step.
+// M = 1 over packed weights with at most 128 column blocks (N <= 2048): the
+// part-block kernel, 8 columns per workgroup.  W x LPW covers the record pairs
+// in one round up to K = 3072 (timed on GPT-2 small / XL shapes: 768 -> 768
+// 3.07 -> 2.73 us, 3072 -> 768 4.37 -> 3.30 us, 1600 -> 1600 3.95 -> 3.07 us;
+// at 2304 columns and more the MFMA GEMV is as fast or faster).  Not for a
+// batching caller's decode (GemmArgs::decode_batches): there one kernel family
+// serves every M up to 16, so a row's sums do not depend on the batch; the
+// part-block kernel with several rows per workgroup measured slower than the
+// MFMA GEMV from two rows up (b = 8 decode 25.8 K against 26.6 K tok/s, b = 16
+// 44 K against 51 K).
 bool part_gemv_preferred(const GemmArgs& g) {
-  return g.m >= 1 && g.m <= 16 && !g.ln_gamma && (g.n + 15) / 16 <= 128;
+  return g.m == 1 && !g.a_p32 && !g.ln_gamma && !g.decode_batches && (g.n + 15) / 16 <= 128;
 }
 
 hipError_t launch_part(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   PackedParams p{};
   p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
-  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.m = 1; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.nb = (g.n + 15) / 16;
   p.kc = g.k / 64;
   p.chunks_per_split = p.kc;
   p.splits = 1;
   p.defer = deferred != nullptr;
   p.partials = s ? s->partials : nullptr;
-  if (p.defer && (!p.partials || size_t(g.m) * g.n > s->partial_floats)) return hipErrorInvalidValue;
+  if (p.defer && (!p.partials || size_t(g.n) > s->partial_floats)) return hipErrorInvalidValue;
   if (deferred) *deferred = 1;
   const int steps = (p.kc + 1) / 2;
-  const dim3 grid(unsigned(2 * p.nb), unsigned(g.m));
-  if (g.a_p32) {
-    if (steps <= 6) hipLaunchKernelGGL((gemv_part_kernel<3, 2, 8, true>), grid, dim3(192), 0, stream, p);
-    else if (steps <= 16) hipLaunchKernelGGL((gemv_part_kernel<8, 2, 8, true>), grid, dim3(512), 0, stream, p);
-    else hipLaunchKernelGGL((gemv_part_kernel<8, 3, 8, true>), grid, dim3(512), 0, stream, p);
-  } else {
-    if (steps <= 6) hipLaunchKernelGGL((gemv_part_kernel<3, 2, 8, false>), grid, dim3(192), 0, stream, p);
-    else if (steps <= 16) hipLaunchKernelGGL((gemv_part_kernel<8, 2, 8, false>), grid, dim3(512), 0, stream, p);
-    else hipLaunchKernelGGL((gemv_part_kernel<8, 3, 8, false>), grid, dim3(512), 0, stream, p);
-  }
+  const dim3 grid(unsigned(2 * p.nb));
+  if (steps <= 6) hipLaunchKernelGGL((gemv_part_kernel<3, 2, 8>), grid, dim3(192), 0, stream, p);
+  else if (steps <= 16) hipLaunchKernelGGL((gemv_part_kernel<8, 2, 8>), grid, dim3(512), 0, stream, p);
+  else hipLaunchKernelGGL((gemv_part_kernel<8, 3, 8>), grid, dim3(512), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -84,6 +84,10 @@ struct GemmArgs {
   // whether it is prefilled alone or beside others (the int8 panel and fp16
   // record kernels then agree bit for bit).
   bool canonical = false;
+  // Decode rows of a caller that batches requests (the runtime): the kernel
+  // family and K split are the same for every M up to 16, so a row's sums do
+  // not depend on the batch (the single-row part-block GEMV is not used).
+  bool decode_batches = false;
   Epilogue epi;
 };
 // out[row] = the column of the largest value over the groups' partials (lowest

@@ -483,6 +483,7 @@ struct ti_llm_model {
     g.ln_eps = 1e-5f;
     g.epi = epi;
     g.canonical = prefill_pass;
+    g.decode_batches = !prefill_pass;
     ck(tia::gemm(g, &scratch, stream, deferred));
   }
 
@@ -491,7 +492,8 @@ struct ti_llm_model {
   // batch (tia::GemmArgs::canonical), so a prompt decodes the same alone or
   // beside others, as the reference runtime does (the epoll server batches
   // prompts as they arrive).  Decode GEMVs of 1..16 rows are batch-invariant by
-  // construction (one kernel and one K split per shape for every M up to 16).
+  // construction: one kernel and one K split per shape for every M up to 16
+  // (tia::GemmArgs::decode_batches).
   bool prefill_pass = false;
 
   // x += a @ w + bias (fp16 rounding points of reference runtime.cu:149/153), then
