@@ -359,12 +359,14 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
 //   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = 16 keys x 32 dims of K (LDS),
 //                 B = Q^T (registers: lane (j, g) holds query j, dims 8g..8g+7);
 //                 lane (j, g) receives the scores of query j for keys 4g..4g+3;
-//   P^T = exp(S^T - m) rounded to fp16: exactly the B operand of
-//   O^T += V^T P^T  v_mfma_f32_16x16x16_f16, A = 16 dims x 16 keys of V^T (LDS,
-//                 V is staged transposed), lane (j, g) accumulates query j's
-//                 dims 16db + 4g + v.
+//   P^T = exp(S^T - m) rounded to fp16: two 16-key blocks of it side by side
+//                 are exactly the B operand of
+//   O^T += V^T P^T  v_mfma_f32_16x16x32_f16, A = 16 dims x (two 4-key runs per
+//                 lane) of V^T (LDS, V is staged transposed), lane (j, g)
+//                 accumulates query j's dims 16db + 4g + v;
+//   l   += 1 P^T  the same MFMA with an A of ones: the row sums, in every lane.
 // So a query's running max, sum and rescale stay in the four lanes (j, g) that
-// hold it (two cross-lane steps per tile for max and sum).  A workgroup of 4
+// hold it (cross-lane steps only on tiles that raise the maximum).  A workgroup of 4
 // waves takes 64 queries (16 per wave) and walks 64-key tiles of K and V through
 // double-buffered LDS, stopping at the last key any of its queries may see.
 // The global loads of the next two tiles are in flight during a tile's MFMAs
@@ -374,9 +376,10 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
 // them 8-way bank conflicts, two thirds of the kernel's LDS cycles).
 // Numerics: scores, max, sum and accumulation in fp32 (exponentials in base 2
 // of the log2(e)-scaled scores), probabilities rounded to fp16 for the PV
-// product; rows with no visible key, and padded queries, are exactly zero.
+// product and its row sum (numerator and denominator weigh each key alike);
+// rows with no visible key, and padded queries, are exactly zero.
 template <int D, int KS>
-__global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma_kernel(AttnParams p) {
   constexpr int BQ = 64, BT = 64, KP = D + 8, VP = BT + 8;
   constexpr int SEGS = D / 8;                 // 16-byte pieces per key row
   constexpr int PIECES = BT * SEGS / 256;     // per thread per tile (2 or 4)
@@ -390,7 +393,24 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
   // step; each group stages its own tile and the two merge at the end.
   const int grp = wave >> 2, qw = wave & 3, gt = int(threadIdx.x & 255);
   const int j = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y, b = blockIdx.z, q0 = blockIdx.x * BQ;
+  // Workgroups go to the 8 XCDs round-robin by linear id.  Taken as is, the
+  // grid (query tiles, heads, batch) would give XCD x query tile x (mod 8) of
+  // every row, so under the causal mask the XCDs' loads differ by up to 8x at
+  // 8 query tiles, and the query tiles of one (b, h) would fetch its K and V into
+  // eight L2s.  Instead ids are regrouped into 8 contiguous runs (one per XCD)
+  // of whole (b, h) rows, and within a row the query tiles alternate light and
+  // heavy (0, n-1, 1, n-2, ...), so a run that splits a row is balanced too.
+  int b, h, q0;
+  {
+    const int nq = int(gridDim.x), nh = int(gridDim.y);
+    const int n = nq * nh * int(gridDim.z), n8 = n & ~7;
+    const int id = int(blockIdx.x) + nq * (int(blockIdx.y) + nh * int(blockIdx.z));
+    const int li = id < n8 ? (id & 7) * (n8 >> 3) + (id >> 3) : id;
+    const int k = li % nq, row = li / nq;
+    h = row % nh;
+    b = row / nh;
+    q0 = ((k & 1) ? nq - 1 - (k >> 1) : (k >> 1)) * BQ;
+  }
 
   const int q_valid = max(0, min(a.q_len, a.q_lengths[b]));
   const int64_t off = a.offsets ? int64_t(a.offsets[b]) : 0;
@@ -447,7 +467,8 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
     }
   };
 
-  float m = kNegInf, l = 0.f;
+  float m = kNegInf;
+  float4_t accl = {0.f, 0.f, 0.f, 0.f};  // every entry: the running sum l of this lane's query
   float4_t acc[D / 16];
 #pragma unroll
   for (int d = 0; d < D / 16; ++d) acc[d] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -485,7 +506,9 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
       // query's end are masked only on tiles that reach some query's end (a
       // wave-uniform test).  The reference ref is raised only when a score
       // exceeds it by more than 8 (p <= 256 stays exact enough in fp16 and the
-      // sums are fp32), so acc and l are rescaled on few tiles, not every tile.
+      // sums are fp32), so acc and l are rescaled on few tiles, not every tile;
+      // a lane's own maximum decides whether any query of the wave may raise,
+      // and only then are the four lanes of each query reduced.
       const float l2s = p.scale * 1.4426950408889634f;
       float tmax = kNegInf;
       if (t * BT + BT <= my_end_min) {
@@ -503,38 +526,55 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
             tmax = fmaxf(tmax, sc[kb][v]);
           }
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * l2s;
-      const bool raise = tmax > m + 8.f;
-      if (__ballot(raise)) {
+      if (__ballot(tmax * l2s > m + 8.f)) {
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * l2s;
+        const bool raise = tmax > m + 8.f;
         const float nref = raise ? tmax : m;
-        const float alpha = l == 0.f ? 0.f : __builtin_amdgcn_exp2f(m - nref);
-        l *= alpha;
+        const float alpha = accl[0] == 0.f ? 0.f : __builtin_amdgcn_exp2f(m - nref);
+        accl[0] *= alpha;
 #pragma unroll
         for (int d = 0; d < D / 16; ++d) acc[d] *= alpha;
         m = nref;
       }
       const float base = m == kNegInf ? 0.f : m;  // -inf only while every key so far is masked
-      half4_t pt[4];
-      float psum = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float pr = __builtin_amdgcn_exp2f(fmaf(sc[kb][v], l2s, -base));
-          pt[kb][v] = f16r(pr);
-          psum += pr;
-        }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
-      l += psum;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      // P^T as two B operands of v_mfma_f32_16x16x32_f16: pair c holds, in
+      // lane (j, g), the probabilities of keys 32c + 4g + v and 32c + 16 + 4g + v
+      // (v < 4), and the A operand (V^T) takes the same two 4-key runs of each
+      // dim row.  A third A operand of ones gives every lane the row sum
+      // l = sum of the fp16 probabilities, in fp32, with no cross-lane step.
+      // V^T fragments of a key pair: the first pair's LDS reads complete while
+      // the exponentials run, the second's during the first pair's MFMAs.
+      auto vfrag = [&](half8_t (&vf)[D / 16], int c) {
 #pragma unroll
         for (int d = 0; d < D / 16; ++d) {
-          const half4_t vf = *reinterpret_cast<const half4_t*>(&vt[buf][grp][16 * d + j][16 * kb + 4 * g]);
-          acc[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pt[kb], acc[d], 0, 0, 0);
+          const f16* vrow = &vt[buf][grp][16 * d + j][32 * c + 4 * g];
+          const half4_t lo = *reinterpret_cast<const half4_t*>(vrow);
+          const half4_t hi = *reinterpret_cast<const half4_t*>(vrow + 16);
+          vf[d] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
+      };
+      half8_t vf[D / 16];
+      vfrag(vf, 0);
+      half8_t pp[2];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          pp[kb >> 1][4 * (kb & 1) + v] = f16r(__builtin_amdgcn_exp2f(fmaf(sc[kb][v], l2s, -base)));
+      const half8_t ones = {f16(1.f), f16(1.f), f16(1.f), f16(1.f), f16(1.f), f16(1.f), f16(1.f), f16(1.f)};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        half8_t vn[D / 16];
+        if (c == 0) vfrag(vn, 1);
+#pragma unroll
+        for (int d = 0; d < D / 16; ++d) acc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[d], pp[c], acc[d], 0, 0, 0);
+        accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pp[c], accl, 0, 0, 0);
+        if (c == 0) {
+#pragma unroll
+          for (int d = 0; d < D / 16; ++d) vf[d] = vn[d];
+        }
+      }
     }
     if (s_ + 1 < nsteps) store_tile(next, buf ^ 1);
     __syncthreads();
@@ -556,15 +596,16 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) xs[4 * d + v] = acc[d][v];
       xs[PER - 2] = m;
-      xs[PER - 1] = l;
+      xs[PER - 1] = accl[0];
     }
     __syncthreads();
     if (grp == 1) return;
+    const float l = accl[0];
     const float m1 = xs[PER - 2], l1 = xs[PER - 1];
     const float nm = fmaxf(l > 0.f ? m : kNegInf, l1 > 0.f ? m1 : kNegInf);
     const float f0 = l > 0.f ? __builtin_amdgcn_exp2f(m - nm) : 0.f;
     const float f1 = l1 > 0.f ? __builtin_amdgcn_exp2f(m1 - nm) : 0.f;
-    l = l * f0 + l1 * f1;
+    accl[0] = l * f0 + l1 * f1;
 #pragma unroll
     for (int d = 0; d < D / 16; ++d)
 #pragma unroll
@@ -572,6 +613,7 @@ __global__ __launch_bounds__(256 * KS) void prefill_mfma_kernel(AttnParams p) {
   }
 
   if (my_q >= a.q_len) return;
+  const float l = accl[0];
   const float inv = l > 0.f ? 1.f / l : 0.f;
   uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(my_q) * a.o_sq;
 #pragma unroll
