@@ -26,6 +26,8 @@ achieved HBM GB/s".
   empty kernel, pure streaming reads of the same sizes; libtinyinfer_diag.so).
 * cpu_baseline: the CPU restatement of the reference runtime (oracle/) decoding
   the same batch-32 workload for a bounded number of steps on this host.
+* --part cpu: host-core baselines of configs[1..3] (the reference's own CPU
+  LayerNorm / Softmax / matmul_blocked where oracle/_ref holds them); no GPU.
 """
 from __future__ import annotations
 
@@ -56,12 +58,14 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--part", default="all",
-                   choices=["all", "decode", "gemv", "kernels", "roofline", "copy", "limits", "prefill", "xl"],
+                   choices=["all", "decode", "gemv", "kernels", "roofline", "copy", "limits", "prefill", "xl",
+                            "cpu"],
                    help="run one part only (for profiler passes; 'roofline' = the dominant GEMV shape only, "
                         "'copy' = a 512 MiB device copy used to calibrate the HBM byte counters, "
                         "'prefill' = the XL-shaped fp16-record prefill GEMM and the prefill attention cases only, "
                         "'xl' = configs[4] GPT-2 XL, not part of 'all': its synthetic artifact takes ~2 min "
-                        "to write); the driver's JSON line needs 'all'")
+                        "to write; 'cpu' = host-core baselines of configs[1..3], no GPU); the driver's JSON "
+                        "line needs 'all'")
     return p.parse_args()
 
 
@@ -431,6 +435,92 @@ def run_prefill_attention(rp):
     return res
 
 
+def _cpu_us(fn, repeat_s=0.15):
+    """Reference bench/integrated.py:24-32 timing: warm-up calls, then 7 repeats of
+    N calls each, the median over repeats of the per-call median (microseconds)."""
+    t0 = time.perf_counter()
+    fn()
+    one = time.perf_counter() - t0
+    for _ in range(min(20, max(1, int(0.3 / max(one, 1e-6))))):
+        fn()
+    n = max(1, min(200, int(repeat_s / max(one, 1e-6))))
+    meds = []
+    for _ in range(7):
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        meds.append(float(np.median(ts)))
+    return 1e6 * float(np.median(meds))
+
+
+def cpu_baseline_kernels():
+    """Host-core baselines for configs[1..3] beside the GPU kernels: the reference's
+    own CPU kernels (kernels/src/cpu/{layernorm,softmax,matmul}.cpp, compiled from
+    its sources into oracle/_ref) where that library is present, else the oracle's
+    restatement; W8A16 as the reference's fp32 matmul_blocked over weights
+    dequantised once (the reference has no CPU INT8 GEMM; the dequantisation is
+    timed on its own); decode attention through the oracle (the reference has no
+    CPU attention)."""
+    import ctypes as C
+    import oracle
+    ref = oracle.ref_lib()
+    kind = "reference" if ref is not None else "port"
+    rng = np.random.default_rng(7)
+    f = lambda a: a.ctypes.data_as(C.c_void_p)
+    out = {"cores": oracle.num_threads(), "kind": kind}
+
+    x = rng.standard_normal((4096, 768)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(768)).astype(np.float32)
+    bb = (0.1 * rng.standard_normal(768)).astype(np.float32)
+    y = np.empty_like(x)
+    xs = (3 * rng.standard_normal((4096, 1024))).astype(np.float32)
+    ys = np.empty_like(xs)
+    if ref is not None:
+        ln = lambda: ref.ref_layernorm_fused(f(x), f(g), f(bb), f(y), 4096, 768, C.c_float(1e-5))
+        sm = lambda: ref.ref_softmax_fused(f(xs), f(ys), 4096, 1024)
+        lnsm = lambda: (ln(), ref.ref_softmax_fused(f(y), f(y), 4096, 768))
+    else:
+        ln = lambda: oracle.layernorm_f32_fused(x, g, bb)
+        sm = lambda: oracle.softmax_f32_fused(xs)
+        lnsm = lambda: oracle.softmax_f32_fused(oracle.layernorm_f32_fused(x, g, bb))
+    out["layernorm_f32_4096x768_us"] = _cpu_us(ln)
+    out["softmax_f32_4096x1024_us"] = _cpu_us(sm)
+    out["layernorm_then_softmax_f32_4096x768_us"] = _cpu_us(lnsm)
+
+    gemm = {}
+    for k, n in ((768, 3072), (3072, 768)):
+        q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+        s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+        gemm[f"dequantize_K{k}_N{n}_us"] = _cpu_us(lambda: oracle.dequantize(q, s))
+        w = oracle.f16_bits_to_f32(oracle.dequantize(q, s)).reshape(k, n).astype(np.float32)
+        for m in (1, 8, 64, 512):
+            a = rng.standard_normal((m, k)).astype(np.float32)
+            c = np.empty((m, n), np.float32)
+            if ref is not None:
+                mm = lambda: ref.ref_matmul_blocked(f(a), f(w), f(c), m, n, k)
+            else:
+                mm = lambda: oracle.matmul_blocked(a, w)
+            us = _cpu_us(mm)
+            gemm[f"matmul_blocked_M{m}_K{k}_N{n}_us"] = us
+            gemm[f"matmul_blocked_M{m}_K{k}_N{n}_GFLOPs"] = 2.0 * m * k * n / us / 1e3
+    out["w8a16_fp32_matmul_blocked"] = gemm
+
+    B, H, D, T = 32, 12, 64, 1024
+    lens = np.random.default_rng(3).integers(128, 1025, B).astype(np.int32)
+    scale = np.float32(1 / 8)
+    qb = oracle.f32_to_f16_bits(rng.standard_normal((B, H, 1, D)).astype(np.float32) * scale)
+    kb = oracle.f32_to_f16_bits(rng.standard_normal((B, H, T, D)).astype(np.float32) * scale)
+    vb = oracle.f32_to_f16_bits(rng.standard_normal((B, H, T, D)).astype(np.float32) * scale)
+    ones, zeros = np.ones(B, np.int32), np.zeros(B, np.int32)
+    us = _cpu_us(lambda: oracle.attention_f16(qb, kb, vb, ones, lens, zeros, causal=False))
+    kv_bytes = float(lens.sum()) * H * D * 4
+    out["decode_attention_configs3"] = {"us": us, "GBps": kv_bytes / us / 1e3, "kind": "port",
+                                        "kv_bytes": kv_bytes}
+    return out
+
+
 def cpu_baseline_decode(manifest, seconds):
     """The oracle's CPU GPT-2 (restating reference llm/src/runtime.cu) on the batch-32
     workload: one prefill of 32 x 32 tokens, then single-token steps until the time
@@ -458,6 +548,9 @@ def main():
         print(f"bench.py measures one GPU (asked for --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
+    if args.part == "cpu":
+        print(json.dumps({"cpu_kernels": cpu_baseline_kernels()}), flush=True)
+        return
     import torch
     from tinyinfer_amd import LLM_LIB, require
     from tinyinfer_amd.runtime import NativeModel

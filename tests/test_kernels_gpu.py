@@ -102,10 +102,18 @@ def test_gemm_reference_gate_shapes(ops, golden, config, int8):
 
 @pytest.mark.parametrize("m,n,k", [(1, 768, 3072), (3, 100, 1000), (8, 3072, 768), (20, 2304, 768),
                                    (32, 768, 3072), (33, 70, 129), (64, 3072, 768), (100, 50, 40),
-                                   (2, 50257, 768)])
+                                   (2, 50257, 768), (64, 768, 3072), (512, 768, 3072), (40, 130, 2000)])
 def test_gemm_split_k_and_tiled_paths(ops, m, n, k):
     say("gemm paths", m, n, k)
     gemm_case(ops, m, n, k, 0, True, seed=1)
+
+
+@pytest.mark.parametrize("config", [0, 6])
+def test_gemm_tiled_split_k_fp16_weights(ops, config):
+    """Row-major fp16 W over few tiles (M = 64, 3072 -> 768): K split over the
+    library scratch, fused bias (config 0) or the fp32 workspace + bias pass (6)."""
+    say("gemm tiled split fp16", config)
+    gemm_case(ops, 64, 768, 3072, config, False, seed=2)
 
 
 def test_gemm_repeat_calls_are_identical(ops):

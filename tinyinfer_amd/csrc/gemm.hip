@@ -1054,6 +1054,10 @@ struct TiledParams {
   int m, n, k;
   int64_t ldw;
   Epilogue epi;
+  // Split-K (gridDim.z > 1): split z takes K steps [z * steps_per_split, ...)
+  // and stores raw fp32 sums at partials[(z * m + row) * n + col].
+  int steps_per_split;
+  float* partials;
 };
 constexpr int TBM = 64, TBN = 64, TBK = 32, TPAD = 40;  // LDS row pitch in halves
 
@@ -1074,55 +1078,56 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) sc[c] = (INT8 && n0 + w_c4 + c < p.n) ? p.scales[n0 + w_c4 + c] : 0.f;
 
-  half8_t areg;
-  f16 wreg[2][4];
-
-  auto load_global = [&](int k0) {
-    areg = afrag<AVEC>(p.a, p.lda, p.m, p.k, m0 + a_row, k0 + a_kseg);
+  // Staged K step: the A fragment and the raw W bytes (int8: 4 per K row,
+  // fp16: 4 halves in two words), dequantised only when stored to LDS, so a
+  // step's loads stay in flight while earlier steps compute.
+  struct Staged {
+    half8_t a;
+    uint32_t w[2][2];
+  };
+  auto load_global = [&](Staged& r_, int k0) {
+    r_.a = afrag<AVEC>(p.a, p.lda, p.m, p.k, m0 + a_row, k0 + a_kseg);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int k = k0 + w_kr + r, col = n0 + w_c4;
-      if constexpr (INT8) {
-        const int8_t* wp = static_cast<const int8_t*>(p.w);
-        int8_t q[4] = {0, 0, 0, 0};
-        if (k < p.k) {
+      uint32_t lo = 0, hi = 0;
+      if (k < p.k) {
+        if constexpr (INT8) {
+          const int8_t* wp = static_cast<const int8_t*>(p.w) + int64_t(k) * p.ldw + col;
           if (WVEC && col < p.n) {
-            const uint32_t v = *reinterpret_cast<const uint32_t*>(wp + int64_t(k) * p.ldw + col);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) q[c] = int8_t(v >> (8 * c));
+            lo = *reinterpret_cast<const uint32_t*>(wp);
           } else if (!WVEC) {
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-              if (col + c < p.n) q[c] = wp[int64_t(k) * p.ldw + col + c];
+              if (col + c < p.n) lo |= uint32_t(uint8_t(wp[c])) << (8 * c);
           }
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) wreg[r][c] = f16r(float(q[c]) * sc[c]);
-      } else {
-        const uint16_t* wp = static_cast<const uint16_t*>(p.w);
-        uint16_t h[4] = {0, 0, 0, 0};
-        if (k < p.k) {
+        } else {
+          const uint16_t* wp = static_cast<const uint16_t*>(p.w) + int64_t(k) * p.ldw + col;
           if (WVEC && col < p.n) {
-            const uint2 u = *reinterpret_cast<const uint2*>(wp + int64_t(k) * p.ldw + col);
-            h[0] = uint16_t(u.x); h[1] = uint16_t(u.x >> 16); h[2] = uint16_t(u.y); h[3] = uint16_t(u.y >> 16);
+            const uint2 u = *reinterpret_cast<const uint2*>(wp);
+            lo = u.x;
+            hi = u.y;
           } else if (!WVEC) {
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-              if (col + c < p.n) h[c] = wp[int64_t(k) * p.ldw + col + c];
+              if (col + c < p.n) (c < 2 ? lo : hi) |= uint32_t(wp[c]) << (16 * (c & 1));
           }
         }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) wreg[r][c] = __builtin_bit_cast(f16, h[c]);
       }
+      r_.w[r][0] = lo;
+      r_.w[r][1] = hi;
     }
   };
-  auto store_lds = [&](int s) {
-    *reinterpret_cast<half8_t*>(&As[s][a_row][a_kseg]) = areg;
+  auto store_lds = [&](const Staged& r_, int s) {
+    *reinterpret_cast<half8_t*>(&As[s][a_row][a_kseg]) = r_.a;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       half2_t pair;
-      pair[0] = wreg[0][c];
-      pair[1] = wreg[1][c];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        if constexpr (INT8) pair[r] = f16r(float(int8_t(r_.w[r][0] >> (8 * c))) * sc[c]);
+        else pair[r] = __builtin_bit_cast(f16, uint16_t(r_.w[r][c >> 1] >> (16 * (c & 1))));
+      }
       *reinterpret_cast<half2_t*>(&Bs[s][w_c4 + c][w_kr]) = pair;
     }
   };
@@ -1134,12 +1139,19 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
     for (int c = 0; c < 2; ++c) acc[t][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   const int steps = (p.k + TBK - 1) / TBK;
-  load_global(0);
-  store_lds(0);
+  const int split = int(blockIdx.z);
+  const int st0 = split * p.steps_per_split, nst = min(steps, st0 + p.steps_per_split) - st0;
+  // Local step i's data lives in register set i % 3: steps i + 1 .. i + 3 are
+  // in flight while step i computes from LDS buffer i & 1.
+  Staged s0, s1, s2;
+  load_global(s0, st0 * TBK);
+  if (nst > 1) load_global(s1, (st0 + 1) * TBK);
+  if (nst > 2) load_global(s2, (st0 + 2) * TBK);
+  store_lds(s0, 0);
   __syncthreads();
-  for (int st = 0; st < steps; ++st) {
-    const int cur = st & 1;
-    if (st + 1 < steps) load_global((st + 1) * TBK);
+  if (nst > 3) load_global(s0, (st0 + 3) * TBK);
+  auto step = [&](int i, Staged& nxt) {
+    const int cur = i & 1;
     half8_t af[2], bf[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) af[t] = *reinterpret_cast<const half8_t*>(&As[cur][wm * 32 + 16 * t + j][8 * g]);
@@ -1149,11 +1161,18 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int c = 0; c < 2; ++c) acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bf[c], acc[t][c], 0, 0, 0);
-    if (st + 1 < steps) {
-      store_lds(cur ^ 1);
+    if (i + 1 < nst) {
+      store_lds(nxt, cur ^ 1);
       __syncthreads();
     }
+    if (i + 4 < nst) load_global(nxt, (st0 + i + 4) * TBK);
+  };
+  for (int i = 0; i < nst; i += 3) {
+    step(i, s1);
+    if (i + 1 < nst) step(i + 1, s2);
+    if (i + 2 < nst) step(i + 2, s0);
   }
+  const bool raw = gridDim.z > 1;
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1161,7 +1180,9 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = m0 + wm * 32 + 16 * t + 4 * g + v, n = n0 + wn * 32 + 16 * c + j;
-        if (m < p.m && n < p.n) apply_epilogue(p.epi, m, n, acc[t][c][v]);
+        if (m >= p.m || n >= p.n) continue;
+        if (raw) p.partials[(int64_t(split) * p.m + m) * p.n + n] = acc[t][c][v];
+        else apply_epilogue(p.epi, m, n, acc[t][c][v]);
       }
 }
 
@@ -1701,19 +1722,41 @@ hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, i
   return launch_f16_cfg<2, 4, 2, 1, 3, 1, 3>(g, s, stream, deferred);
 }
 
+// Row-major W (the reference ABI's [K, N]).  Each K step of a workgroup waits
+// for one global round trip, so a grid of few tiles (M = 64, 3072 -> 768: 12
+// tiles x 96 steps, 138 us) splits K over the library scratch until >= 256
+// workgroups run (at least 4 steps each), then splitk_epilogue_kernel sums the
+// splits in a fixed order and applies the epilogue.  Canonical (batch-invariant)
+// calls stay unsplit: their K order must not depend on M.
 template <bool INT8>
-hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, hipStream_t stream) {
+hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, const Scratch* s, hipStream_t stream) {
   TiledParams p{};
   p.a = g.a; p.lda = g.lda; p.w = g.w; p.scales = g.scales;
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.ldw = g.ldw > 0 ? g.ldw : g.n;
-  const dim3 grid(unsigned((g.n + TBN - 1) / TBN), unsigned((g.m + TBM - 1) / TBM));
+  const int steps = (g.k + TBK - 1) / TBK;
+  const int64_t tiles = int64_t((g.n + TBN - 1) / TBN) * ((g.m + TBM - 1) / TBM);
+  int splits = 1;
+  if (!g.canonical && s && s->partials && tiles < 256) {
+    splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, steps / 4)));
+    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
+  }
+  p.steps_per_split = (steps + splits - 1) / splits;
+  splits = (steps + p.steps_per_split - 1) / p.steps_per_split;
+  p.partials = splits > 1 ? s->partials : nullptr;
+  const dim3 grid(unsigned((g.n + TBN - 1) / TBN), unsigned((g.m + TBM - 1) / TBM), unsigned(splits));
 #define TIA_TILED(WV, AV) hipLaunchKernelGGL((tiled_kernel<INT8, WV, AV>), grid, dim3(256), 0, stream, p)
   if (wvec && avec) TIA_TILED(true, true);
   else if (wvec) TIA_TILED(true, false);
   else if (avec) TIA_TILED(false, true);
   else TIA_TILED(false, false);
 #undef TIA_TILED
+  if (splits > 1) {
+    const int64_t total = int64_t(g.m) * g.n;
+    const unsigned blocks = unsigned(std::min<int64_t>((total + 63) / 64, 8192));
+    hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m, g.n,
+                       g.epi);
+  }
   return hipGetLastError();
 }
 
@@ -1769,7 +1812,7 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
                                  : launch_skinny<false, 1>(g, wvec, avec, s, stream, deferred);
   if (g.m <= 32) return g.w_int8 ? launch_skinny<true, 2>(g, wvec, avec, s, stream, deferred)
                                  : launch_skinny<false, 2>(g, wvec, avec, s, stream, deferred);
-  return g.w_int8 ? launch_tiled<true>(g, wvec, avec, stream) : launch_tiled<false>(g, wvec, avec, stream);
+  return g.w_int8 ? launch_tiled<true>(g, wvec, avec, s, stream) : launch_tiled<false>(g, wvec, avec, s, stream);
 }
 
 hipError_t argmax_partials(const float* vals, const int32_t* idx, int groups, int rows, int32_t* out,
