@@ -1307,7 +1307,8 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
 //    rounds of 16 x 3 (6400 -> 1600: 10.6 -> 10.3 us);
 //  * at M > 16 two column blocks share each A fragment (CBG = 2) when that
 //    still leaves >= 512 workgroups (the LM head);
-//  * a deferred launch splits K to reach ~192 workgroups, keeping >= 4 chunks
+//  * a deferred launch splits K to reach ~GemmArgs::defer_workgroups (192 by
+//    default) workgroups, keeping >= 4 chunks
 //    per split and the partials within the scratch; otherwise one split and
 //    the epilogue runs in the kernel;
 //  * a LayerNorm-prologue launch is one split covered by one round.
@@ -1425,7 +1426,8 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   int splits = 1;
   if (deferred && !ln && s && s->partials) {
     const int groups = p.nb;
-    splits = std::max(1, std::min((192 + groups - 1) / groups, p.kc / 4));
+    const int target = std::max(1, g.defer_workgroups);
+    splits = std::max(1, std::min((target + groups - 1) / groups, p.kc / 4));
     while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
   }
   p.chunks_per_split = (p.kc + splits - 1) / splits;

@@ -88,6 +88,10 @@ struct GemmArgs {
   // family and K split are the same for every M up to 16, so a row's sums do
   // not depend on the batch (the single-row part-block GEMV is not used).
   bool decode_batches = false;
+  // A deferred launch over packed weights splits K towards this many
+  // workgroups (at least 4 K chunks per split, partials within the scratch).
+  // The split count depends on the shape only, never on M.
+  int defer_workgroups = 192;
   Epilogue epi;
 };
 // out[row] = the column of the largest value over the groups' partials (lowest
@@ -121,11 +125,12 @@ hipError_t gemm(const GemmArgs& args, const Scratch* scratch, hipStream_t stream
 //   x[r][c]    = fp16_rn(x[r][c] + fp16_rn(sum_s partials[s][r][c] + bias[c]))
 //   norm[r][:] = LayerNorm(x[r][:]; gamma, beta, eps)   (fp16 out)
 // i.e. the residual add of reference llm/src/runtime.cu:149/153 followed by the
-// next ln (cols <= 2048).
+// next ln (cols <= 2048).  p32: x and norm are P32 fragment-packed (rows <= 32,
+// cols % 64 == 0); the partials stay row-major.
 hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows, int cols,
                                      const uint16_t* bias, uint16_t* x, const uint16_t* gamma,
                                      const uint16_t* beta, uint16_t* norm, float eps,
-                                     hipStream_t stream);
+                                     hipStream_t stream, bool p32 = false);
 // Per-(device, stream) scratch owned by the library, created on the first call
 // on that stream (never under graph capture).  Returns nullptr and sets *err if
 // it cannot be created.

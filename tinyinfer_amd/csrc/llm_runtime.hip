@@ -46,6 +46,11 @@ namespace {
 thread_local std::string error_text;
 constexpr int kScoreRows = 16;
 constexpr int kHeadDim = 64;
+// Workgroups a split residual GEMV (decode above hidden 1024) aims at: two K
+// splits of the XL residual GEMVs (100 column blocks).  Timed at XL decode,
+// 64 requests: 192 -> 12.06 K tok/s, 384 -> 11.66 K (unsplit with a separate
+// LayerNorm row kernel: 11.4 K).
+constexpr int kResidualSplitWorkgroups = 192;
 
 struct GpuError : std::runtime_error {
   using std::runtime_error::runtime_error;
@@ -458,7 +463,7 @@ struct ti_llm_model {
   // ---------------------------------------------------------------- launch helpers
   void gemm(const uint16_t* a, int m, const Linear& w, tia::Epilogue epi, int* deferred = nullptr,
             const uint16_t* ln_g = nullptr, const uint16_t* ln_b = nullptr, bool a_p32 = false,
-            int* amax_groups = nullptr) {
+            int* amax_groups = nullptr, int defer_workgroups = 192) {
     tia::GemmArgs g;
     g.a = a;
     g.lda = w.k;
@@ -484,6 +489,7 @@ struct ti_llm_model {
     g.epi = epi;
     g.canonical = prefill_pass;
     g.decode_batches = !prefill_pass;
+    g.defer_workgroups = defer_workgroups;
     ck(tia::gemm(g, &scratch, stream, deferred));
   }
 
@@ -498,8 +504,10 @@ struct ti_llm_model {
 
   // x += a @ w + bias (fp16 rounding points of reference runtime.cu:149/153), then
   // norm = LayerNorm(x; g, beta).  Decode-sized GEMMs leave split-K partials that
-  // one fused kernel reduces, adds and normalizes.
-  void residual_ln(const uint16_t* a, int rows, const Linear& w, const uint16_t* g, const uint16_t* beta) {
+  // one fused kernel reduces, adds and normalizes.  p32: a, x and norm are P32
+  // fragment-packed (a decode pass); the split then aims at `workgroups`.
+  void residual_ln(const uint16_t* a, int rows, const Linear& w, const uint16_t* g, const uint16_t* beta,
+                   bool p32 = false, int workgroups = 192) {
     tia::Epilogue r;
     r.kind = tia::EPI_RESIDUAL;
     r.bias = w.bias;
@@ -507,12 +515,16 @@ struct ti_llm_model {
     r.ldy = H;
     r.residual = x;
     r.ldr = H;
+    // (A deferred launch runs no epilogue: x is written by the finisher, so the
+    // epilogue keeps its row-major default.)
     int splits = 0;
-    gemm(a, rows, w, r, &splits);
+    gemm(a, rows, w, r, &splits, nullptr, nullptr, p32, nullptr, workgroups);
     if (splits > 0)
-      ck(tia::splitk_residual_layernorm(scratch.partials, splits, rows, H, w.bias, x, g, beta, norm, 1e-5f, stream));
+      ck(tia::splitk_residual_layernorm(scratch.partials, splits, rows, H, w.bias, x, g, beta, norm, 1e-5f, stream,
+                                        p32));
     else
-      ck(tia::layernorm_f16(x, g, beta, norm, rows, H, 1e-5f, stream));
+      ck(p32 ? tia::layernorm_f16_p32(x, g, beta, norm, rows, H, 1e-5f, stream)
+             : tia::layernorm_f16(x, g, beta, norm, rows, H, 1e-5f, stream));
   }
 
   // x += a @ w + bias in the GEMM's epilogue (no LayerNorm after it); a and x
@@ -557,9 +569,15 @@ struct ti_llm_model {
     ck(hipGetLastError());
     // The LayerNorm before c_attn / c_fc: in the GEMV's prologue up to hidden
     // 1024; above, every one of the GEMV's workgroups normalising all rows
-    // costs more VALU time than one row-kernel launch into norm (measured at
-    // GPT-2 XL's 1600).  Layer 0's ln_1 is already in norm (embedding kernel).
+    // costs more VALU time than a row kernel (measured at GPT-2 XL's 1600).
+    // There the residual GEMVs (c_proj, mlp c_proj: N = hidden, too few column
+    // blocks to fill the machine unsplit) split K and one finisher per row sums
+    // the partials, adds bias and residual and writes the next LayerNorm into
+    // norm (ln_2, the next layer's ln_1, or ln_f): the same launch count as
+    // GEMV + LayerNorm row kernel.  Layer 0's ln_1 is already in norm
+    // (embedding kernel).
     const bool ln_prologue = H <= 1024;
+    const bool split_residual = fuse && !ln_prologue;
     auto ln_then_gemm = [&](const Linear& w, const tia::Epilogue& epi, int* defer, const uint16_t* g,
                             const uint16_t* beta, bool in_norm) {
       if (ln_prologue) return gemm(x, rows, w, epi, defer, g, beta, p32);
@@ -589,7 +607,7 @@ struct ti_llm_model {
       // finishes q, k, v itself (one launch fewer per layer).
       int qkv_splits = 0;
       int* defer_qkv = qlen == 1 && c_attn[l].bias ? &qkv_splits : nullptr;
-      if (fuse) ln_then_gemm(c_attn[l], e, defer_qkv, ln1_g[l], ln1_b[l], l == 0);
+      if (fuse) ln_then_gemm(c_attn[l], e, defer_qkv, ln1_g[l], ln1_b[l], l == 0 || split_residual);
       else gemm(norm, rows, c_attn[l], e, defer_qkv);
 
       tia::AttnArgs at;
@@ -632,6 +650,15 @@ struct ti_llm_model {
       gl.bias = c_fc[l].bias;
       gl.y = mlp;
       gl.ldy = 4 * H;
+      const bool final_layer = l + 1 == L;
+      if (split_residual) {
+        gl.p32 = p32;
+        residual_ln(attn, rows, c_proj[l], ln2_g[l], ln2_b[l], p32, kResidualSplitWorkgroups);
+        gemm(norm, rows, c_fc[l], gl, nullptr, nullptr, nullptr, p32);
+        residual_ln(mlp, rows, c_proj2[l], final_layer ? lnf_g : ln1_g[l + 1], final_layer ? lnf_b : ln1_b[l + 1],
+                    p32, kResidualSplitWorkgroups);
+        continue;
+      }
       if (fuse) {
         gl.p32 = p32;
         residual_add(attn, rows, c_proj[l], p32);
@@ -640,7 +667,6 @@ struct ti_llm_model {
         residual_ln(attn, rows, c_proj[l], ln2_g[l], ln2_b[l]);
         gemm(norm, rows, c_fc[l], gl);
       }
-      const bool final_layer = l + 1 == L;
       if (!fuse) {
         residual_ln(mlp, rows, c_proj2[l], final_layer ? lnf_g : ln1_g[l + 1], final_layer ? lnf_b : ln1_b[l + 1]);
         continue;

@@ -271,9 +271,10 @@ __global__ void gelu_kernel(const uint16_t* x, uint16_t* y, int64_t count, bool 
 // group order, then does the residual and the LayerNorm with lane owning
 // columns lane + 64 i.  NPL > 0 fixes cols = 64 * NPL so no load carries a
 // bounds predicate (predicated loads are issued one round trip at a time);
-// NPL = 0 is the predicated fallback for any cols <= 2048.
+// NPL = 0 is the predicated fallback for any cols <= 2048.  P32: x and norm are
+// fragment-packed decode matrices (common.hpp p32_off), the partials row-major.
 constexpr int kResLnMaxPerLane = 32;  // cols <= 2048
-template <int G, int NPL>
+template <int G, int NPL, bool P32 = false>
 __global__ __launch_bounds__(64 * G) void splitk_residual_ln_kernel(const float* partials, int splits, int rows,
                                                                     int cols, const uint16_t* bias, uint16_t* x,
                                                                     const uint16_t* g, const uint16_t* b,
@@ -284,6 +285,7 @@ __global__ __launch_bounds__(64 * G) void splitk_residual_ln_kernel(const float*
   const int row = blockIdx.x;
   const int64_t plane = int64_t(rows) * cols, base = int64_t(row) * cols;
   auto on = [&](int i) { return NPL > 0 || lane + 64 * i < cols; };
+  auto xat = [&](int c) { return P32 ? p32_off(row, c) : base + c; };
   // Operands that do not depend on the partials are requested first, in one batch.
   // (A null bias reads gamma instead and is scaled to zero, so no load sits
   // behind a per-element branch.)
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(64 * G) void splitk_residual_ln_kernel(const float*
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int c = on(i) ? lane + 64 * i : 0;
-      xv[i] = h2f(x[base + c]);
+      xv[i] = h2f(x[xat(c)]);
       gv[i] = h2f(g[c]);
       btv[i] = h2f(b[c]);
       bv[i] = h2f(bp[c]) * bscale;
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(64 * G) void splitk_residual_ln_kernel(const float*
       for (int w = 1; w < G; ++w) t += red[w * cols + c];
       const float h = rt16(t + bv[i]);
       v[i] = rt16(xv[i] + h);
-      x[base + c] = f2h(v[i]);
+      x[xat(c)] = f2h(v[i]);
       s += v[i];
     }
   }
@@ -337,7 +339,82 @@ __global__ __launch_bounds__(64 * G) void splitk_residual_ln_kernel(const float*
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const int c = lane + 64 * i;
-    if (on(i)) norm[base + c] = f2h((v[i] - mean) * inv * gv[i] + btv[i]);
+    if (on(i)) norm[xat(c)] = f2h((v[i] - mean) * inv * gv[i] + btv[i]);
+  }
+}
+
+// The same finisher with one wave per row and every load of the row in one
+// round (no LDS, no barrier): lane l owns columns 8 l + 512 i (i < NV, cols % 8
+// == 0); the S split partials are summed in split order, as the kernel above
+// sums them for S <= G, then bias, residual and LayerNorm as there.  Columns
+// past cols re-read the row's last 8 (clamped address) and are neither counted
+// nor stored.  P32: x and norm are fragment-packed, the partials row-major.
+template <int S, int NV, bool P32>
+__global__ __launch_bounds__(256) void residual_ln_wave(const float* partials, int rows, int cols,
+                                                        const uint16_t* bias, uint16_t* x, const uint16_t* g,
+                                                        const uint16_t* b, uint16_t* norm, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t plane = int64_t(rows) * cols, base = int64_t(row) * cols;
+  auto at = [&](int c) { return P32 ? p32_off(row, c) : base + c; };
+  const uint16_t* bp = bias ? bias : g;  // a null bias reads gamma, scaled to zero
+  const float bscale = bias ? 1.f : 0.f;
+  u32x4_t xr[NV], gr[NV], br[NV], hr[NV];
+  float4_t pr[S][NV][2];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = min(8 * lane + 512 * i, cols - 8);
+    xr[i] = *reinterpret_cast<const u32x4_t*>(x + at(c));
+    gr[i] = *reinterpret_cast<const u32x4_t*>(g + c);
+    br[i] = *reinterpret_cast<const u32x4_t*>(b + c);
+    hr[i] = *reinterpret_cast<const u32x4_t*>(bp + c);
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) {
+      const float4_t* pp = reinterpret_cast<const float4_t*>(partials + sp * plane + base + c);
+      pr[sp][i][0] = pp[0];
+      pr[sp][i][1] = pp[1];
+    }
+  }
+  auto half_at = [](const u32x4_t& u, int e) { return h2f(uint16_t(u[e >> 1] >> (16 * (e & 1)))); };
+  float v[NV][8];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const bool on = 8 * lane + 512 * i < cols;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float t = pr[0][i][e >> 2][e & 3];
+#pragma unroll
+      for (int sp = 1; sp < S; ++sp) t += pr[sp][i][e >> 2][e & 3];
+      const float h = rt16(t + half_at(hr[i], e) * bscale);
+      v[i][e] = rt16(half_at(xr[i], e) + h);
+      s += on ? v[i][e] : 0.f;
+    }
+  }
+  const float mean = wave_sum(s) / float(cols);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const bool on = 8 * lane + 512 * i < cols;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += on ? (v[i][e] - mean) * (v[i][e] - mean) : 0.f;
+  }
+  const float inv = rsqrtf(wave_sum(ss) / float(cols) + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = 8 * lane + 512 * i;
+    if (c >= cols) continue;
+    uint32_t xo[4], no[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float n0 = (v[i][e] - mean) * inv * half_at(gr[i], e) + half_at(br[i], e);
+      const float n1 = (v[i][e + 1] - mean) * inv * half_at(gr[i], e + 1) + half_at(br[i], e + 1);
+      xo[e >> 1] = uint32_t(f2h(v[i][e])) | (uint32_t(f2h(v[i][e + 1])) << 16);
+      no[e >> 1] = uint32_t(f2h(n0)) | (uint32_t(f2h(n1)) << 16);
+    }
+    *reinterpret_cast<u32x4_t*>(x + at(c)) = u32x4_t{xo[0], xo[1], xo[2], xo[3]};
+    *reinterpret_cast<u32x4_t*>(norm + at(c)) = u32x4_t{no[0], no[1], no[2], no[3]};
   }
 }
 
@@ -434,10 +511,42 @@ hipError_t layernorm_softmax_f32(const float* x, const float* g, const float* b,
 }
 hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows, int cols,
                                      const uint16_t* bias, uint16_t* x, const uint16_t* gamma,
-                                     const uint16_t* beta, uint16_t* norm, float eps, hipStream_t st) {
+                                     const uint16_t* beta, uint16_t* norm, float eps, hipStream_t st,
+                                     bool p32) {
   if (cols > 64 * kResLnMaxPerLane || splits < 1) return hipErrorInvalidValue;
+  if (p32 && (rows < 1 || rows > 32 || cols % 64 != 0)) return hipErrorInvalidValue;
+  // Up to 4 splits: one wave per row, all loads in one round.
+  if (splits <= 4 && cols % 8 == 0 && cols >= 8 && al16(partials) && al16(x) && al16(gamma) && al16(beta) && al16(norm) &&
+      (!bias || al16(bias))) {
+    const dim3 grid(unsigned((rows + 3) / 4)), block(256);
+#define TIA_RLW(S_, NV_)                                                                                   \
+  if (splits == S_) {                                                                                      \
+    if (p32) hipLaunchKernelGGL((residual_ln_wave<S_, NV_, true>), grid, block, 0, st, partials, rows, cols, \
+                                bias, x, gamma, beta, norm, eps);                                           \
+    else hipLaunchKernelGGL((residual_ln_wave<S_, NV_, false>), grid, block, 0, st, partials, rows, cols,    \
+                            bias, x, gamma, beta, norm, eps);                                               \
+    return hipGetLastError();                                                                              \
+  }
+    if (cols <= 1024) {
+      TIA_RLW(1, 2) TIA_RLW(2, 2) TIA_RLW(3, 2) TIA_RLW(4, 2)
+    } else {
+      TIA_RLW(1, 4) TIA_RLW(2, 4) TIA_RLW(3, 4) TIA_RLW(4, 4)
+    }
+#undef TIA_RLW
+  }
   // LDS holds G rows of partial sums: keep it within 64 KiB.
   const size_t lds16 = 16 * cols * sizeof(float), lds8 = 8 * cols * sizeof(float);
+  if (p32) {
+#define TIA_RLNP(G, NPL, LDS)                                                                     \
+  hipLaunchKernelGGL((splitk_residual_ln_kernel<G, NPL, true>), dim3(unsigned(rows)), dim3(64 * G), LDS, st, \
+                     partials, splits, rows, cols, bias, x, gamma, beta, norm, eps)
+    if (cols == 768) TIA_RLNP(16, 12, lds16);
+    else if (cols == 1600) TIA_RLNP(8, 25, lds8);
+    else if (cols <= 1024) TIA_RLNP(16, 0, lds16);
+    else TIA_RLNP(8, 0, lds8);
+#undef TIA_RLNP
+    return hipGetLastError();
+  }
 #define TIA_RLN(G, NPL, LDS)                                                                              \
   hipLaunchKernelGGL((splitk_residual_ln_kernel<G, NPL>), dim3(unsigned(rows)), dim3(64 * G), LDS, st, partials, \
                      splits, rows, cols, bias, x, gamma, beta, norm, eps)
