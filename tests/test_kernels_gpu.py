@@ -108,6 +108,18 @@ def test_gemm_split_k_and_tiled_paths(ops, m, n, k):
     gemm_case(ops, m, n, k, 0, True, seed=1)
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 768, 3072), (2, 3072, 768), (3, 1040, 1000), (5, 16, 17), (8, 2048, 4096),
+                                   (8, 48, 40)])
+@pytest.mark.parametrize("config", [0, 6])
+def test_gemm_rowmajor_gemv_shapes(ops, m, n, k, config):
+    """Row-major int8 W at M <= 8 through the reference ABI (fused config 0 and
+    separate-workspace config 6), the skinny split-K path: K not a multiple of
+    32 (a ragged last step), N across several 64-column tiles with a part-filled
+    last one, N = 16 and 48 (one tile), and K = 4096."""
+    say("gemm row-major gemv", m, n, k, "config", config)
+    gemm_case(ops, m, n, k, config, True, seed=3)
+
+
 @pytest.mark.parametrize("config", [0, 6])
 def test_gemm_tiled_split_k_fp16_weights(ops, config):
     """Row-major fp16 W over few tiles (M = 64, 3072 -> 768): K split over the
