@@ -222,13 +222,14 @@ def test_decode_graph_equals_eager(model):
     model.reset_all()
 
 
-@pytest.mark.parametrize("others", [1, 4, 15])
+@pytest.mark.parametrize("others", [1, 4, 15, 20, 31])
 def test_prefill_and_decode_are_batch_invariant(model, others):
     """A request's logits do not depend on the batch it runs in: its prompt
     prefilled alone or beside others of other lengths (rows of the prefill GEMMs
     and attention summed in one order whatever the batch), then decode steps of
-    1 to 16 rows.  The epoll server batches requests as they arrive and its
-    greedy output must equal direct greedy decoding."""
+    1 to 32 rows (the 32-row GEMVs and LM head sum K in the 16-row kernels'
+    order).  The epoll server batches requests as they arrive and its greedy
+    output must equal direct greedy decoding."""
     ids = token_ids(24, seed=11)
     rows = [token_ids(5 + 3 * i, seed=100 + i) for i in range(others)]
     say("batch invariance", others)

@@ -767,17 +767,24 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
     b.bias = bsrc[has_bias ? col : 0];
   };
   auto compute = [&](const Block& b, int i) {
-    float4_t acc[MT];
+    // Four sums, chunk c into sum c % 4, added in that order at the end: the
+    // K order of the 4-wave packed GEMV over the same KC (wave w takes chunks
+    // w, w + 4, ...; the waves are added in order), which serves 1..16 rows,
+    // so a row's logits do not depend on the batch size.
+    float4_t acc[4][MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[q][t] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const half8_t b0 = dequant8(b.w[c][0], b.w[c][1], b.scale);
       const half8_t b1 = dequant8(b.w[c][2], b.w[c][3], b.scale);
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * 2 + t) * 2) * 64 + lane], b0, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * 2 + t) * 2 + 1) * 64 + lane], b1, acc[t], 0, 0, 0);
+        float4_t& ac = acc[c % 4][t];
+        ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * 2 + t) * 2) * 64 + lane], b0, ac, 0, 0, 0);
+        ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * 2 + t) * 2 + 1) * 64 + lane], b1, ac, 0, 0, 0);
       }
       // One chunk's LDS reads and dequantisation at a time (hoisting all of
       // them would hold every A fragment of the block in registers).
@@ -793,7 +800,10 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * t + 4 * g + v;
-        const float val = acc[t][v] + bias;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sum += acc[q][t][v];
+        const float val = sum + bias;
         if (row < p.m) y[int64_t(row) * p.epi.ldy + col] = val;
         amax_merge(bv[t * 4 + v], bi[t * 4 + v], val, col);
       }
@@ -1297,36 +1307,33 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
 // decode shapes, M = 1 and 32, K = 768 .. 6400, N = 768 .. 50257):
 //  * W waves x CPW chunks per wave cover a split's K range with the fewest dead
 //    slots (a dead slot re-reads a chunk): 12 chunks -> 4 x 3, 16 -> 4 x 4,
-//    24 -> 8 x 3, 32 -> 8 x 4, 48 -> 16 x 3 (M <= 16);
-//  * at M > 16 every 16-column block re-reads A (4 KiB per chunk against 1 KiB
-//    of weights), so up to 16 chunks 4 waves suffice; longer ranges: 25
-//    chunks (K = 1600) over at least 200 column blocks as 16 x 2 with two
-//    blocks sharing each A fragment (1600 -> 4800 / 6400: 7.4 / 7.7 -> 6.4 /
-//    6.5 us), over fewer blocks 8 x 3 (1600 -> 1600: 4.9 -> 4.7 us); 48
-//    chunks (K = 3072) as 12 x 4 (3072 -> 768: 6.3 -> 6.0 us); more as
-//    rounds of 16 x 3 (6400 -> 1600: 10.6 -> 10.3 us);
-//  * at M > 16 two column blocks share each A fragment (CBG = 2) when that
-//    still leaves >= 512 workgroups (the LM head);
-//  * a deferred launch splits K to reach ~GemmArgs::defer_workgroups (192 by
-//    default) workgroups, keeping >= 4 chunks
-//    per split and the partials within the scratch; otherwise one split and
-//    the epilogue runs in the kernel;
+//    24 -> 8 x 3, 32 -> 8 x 4, 48 -> 16 x 3, more -> rounds of 16 x 4;
+//  * W x CPW follows the chunk count only, the same for 16- and 32-row
+//    launches: wave w sums chunks w, w + W, ... in order and the waves are
+//    added in wave order, so a row's sums do not depend on the batch size
+//    (decode batches of 1..32 give a request the same bits; 32-row-only shapes
+//    measured 2-5 % faster per launch: 3072 -> 768 as 12 x 4 6.0 against
+//    6.3 us, 1600 -> 6400 as 16 x 2 with block pairs 6.5 against 7.7 us);
+//  * at M > 16 two column blocks share each A fragment (CBG = 2: the same
+//    per-column order) over >= 200 column blocks at 8 waves, and when that
+//    still leaves >= 512 workgroups at 4 waves (the LM head);
+//  * a deferred launch splits K to reach ~192 workgroups, keeping >= 4 chunks
+//    per split and the partials within the scratch (the split count follows
+//    the shape only); otherwise one split and the epilogue runs in the kernel;
 //  * a LayerNorm-prologue launch is one split covered by one round.
 struct GemvShape {
   int w, cpw, cbg;
 };
 
 GemvShape gemv_shape(int mt, int chunks, bool one_round, int nb) {
-  if (chunks <= 12) return {4, 3, 1};
-  if (chunks <= 16) return {4, 4, 1};
-  if (one_round || mt == 1) {
-    if (chunks <= 24) return {8, 3, 1};
-    if (chunks <= 32) return {8, 4, 1};
-    if (mt == 1) return chunks <= 48 ? GemvShape{16, 3, 1} : GemvShape{16, 4, 1};
-  }
-  if (chunks <= 32) return nb >= 200 ? GemvShape{16, 2, 2} : GemvShape{8, 3, 1};
-  if (chunks <= 48) return {12, 4, 1};
-  return {16, 3, 1};
+  GemvShape s{16, 4, 1};
+  if (chunks <= 12) s = {4, 3, 1};
+  else if (chunks <= 16) s = {4, 4, 1};
+  else if (chunks <= 24) s = {8, 3, 1};
+  else if (chunks <= 32) s = {8, 4, 1};
+  else if (chunks <= 48) s = {16, 3, 1};
+  if (mt == 2 && !one_round && s.w == 8 && nb >= 200) s.cbg = 2;
+  return s;
 }
 
 template <int MT, bool LNA, bool PA>
@@ -1344,14 +1351,13 @@ hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipS
     TIA_GEMV(4, 3, 2)
     TIA_GEMV(4, 4, 2)
   }
-  if constexpr (MT == 1 && !LNA) {
+  if constexpr (!LNA) {
     TIA_GEMV(16, 3, 1)
     TIA_GEMV(16, 4, 1)
   }
   if constexpr (MT == 2 && !LNA) {
-    TIA_GEMV(16, 2, 2)
-    TIA_GEMV(12, 4, 1)
-    TIA_GEMV(16, 3, 1)
+    TIA_GEMV(8, 3, 2)
+    TIA_GEMV(8, 4, 2)
   }
 #undef TIA_GEMV
   return hipErrorInvalidValue;
