@@ -1,11 +1,21 @@
-"""ctypes wrapper of the v2 kernel ABI with the reference's Python signatures.
+"""Torch-facing ctypes binding of the v2 kernel ABI (libtinyinfer_backend.so).
 
-Mirrors reference llm/native_ops.py:33-210 (class ``NativeOps``): the same
-method names, argument meaning, tensor checks (CUDA/HIP device, dtype,
-contiguity, no grad, rank, extents), catalog check, ``record_stream`` on every
-tensor before the call, the current torch stream and device index appended to
-every native call, and ``RuntimeError`` carrying ``ti_v2_last_error()`` when a
-call returns a nonzero status.  Inference only; no CPU fallback exists.
+The public surface is the one reference llm/native_ops.py:33-210 gives its
+callers: ``NativeOps`` with ``gemm``, ``gemm_int8``, ``legacy_gemm``,
+``layernorm``, ``gelu_new``, ``softmax`` and ``attention``; the module constant
+``GEMM_CATALOG`` (reference :14-16) that the library's catalog JSON must equal;
+and the exception contract -- ``TypeError`` for an operand that is not a
+contiguous device tensor of the right dtype, ``ValueError`` for a bad rank,
+extent, device, integer argument or a tensor that requires grad,
+``RuntimeError`` carrying ``ti_v2_last_error()`` for a nonzero native status.
+
+How it is built here: every native symbol is described by a string of
+parameter codes (``_ABI``); each call goes through a ``_Call`` that validates
+the operands in argument order, allocates outputs on the operands' device,
+records every tensor on the current torch stream (the caller's allocator must
+not recycle them while the queued kernels run), and appends that stream and the
+device index as the ABI's last two arguments.  There is no CPU path: the
+library must be built, and the operands must already live on the GPU.
 """
 from __future__ import annotations
 
@@ -16,207 +26,276 @@ from pathlib import Path
 
 from . import BACKEND_LIB, require
 
-_I32_MAX = 2**31 - 1
-_TILES = ((32, 32, 16, 4), (64, 32, 32, 8), (64, 64, 32, 8))
-# The 12-entry allow-list the library must report (reference llm/native_ops.py:14-16).
-GEMM_CATALOG = tuple({"id": i, "tile": _TILES[i % 3],
-                      "stages": 1 if (3 <= i < 6 or i >= 9) else 2,
-                      "epilogue": "separate" if i >= 6 else "fused"} for i in range(12))
+INT32_MAX = 2**31 - 1
+INT64_MAX = 2**63 - 1
+
+# The 12 GEMM configurations the library must report, in order (the reference
+# catalog, kernels/src/cuda/tc/catalog.cuh:8-15): three CUDA tile hints, one or
+# two stages, fused bias epilogue for ids 0-5, a caller FP32 workspace for 6-11.
+_TILE_HINTS = ((32, 32, 16, 4), (64, 32, 32, 8), (64, 64, 32, 8))
+GEMM_CATALOG = tuple(
+    {"id": cid, "tile": _TILE_HINTS[cid % 3],
+     "stages": 2 if (cid % 6) < 3 else 1,
+     "epilogue": "fused" if cid < 6 else "separate"}
+    for cid in range(12))
+
+# Parameter codes of each entry point, before the implicit (stream, device)
+# trailer: p = pointer, i = int, f = float, q = int64.
+_ABI = {
+    "ti_v2_gemm_f16": "ppppiiiii",
+    "ti_v2_gemm_i8": "pppppiiiii",
+    "ti_v2_gemm_ex_f16": "pppppiiiii",
+    "ti_v2_gemm_ex_i8": "ppppppiiiii",
+    "ti_v2_legacy_gemm_f32": "pppiii",
+    "ti_v2_attention_f16": "pppppppiiiiiii",
+    "ti_v2_layernorm_f16": "ppppiif",
+    "ti_v2_gelu_new_f16": "ppq",
+    "ti_v2_softmax_f16": "ppii",
+}
+_CTYPE = {"p": ctypes.c_void_p, "i": ctypes.c_int, "f": ctypes.c_float, "q": ctypes.c_int64}
+_TRAILER = [ctypes.c_size_t, ctypes.c_int]   # hipStream_t as uintptr_t, device ordinal
 
 
-def _dim(value, name):
-    if type(value) is not int or value <= 0 or value > _I32_MAX:
-        raise ValueError(f"{name} must be an integer in [1, INT32_MAX]")
+def _count(value, name, low=1, high=INT32_MAX):
+    """An exact int (bool excluded) in [low, high], else ValueError."""
+    if type(value) is not int or value < low or value > high:
+        raise ValueError(f"{name} must be an integer in [{low}, {high}]")
     return value
 
 
-def _metadata(value, batch, default, maximum, name):
-    """Host-side per-request metadata: None, one int, or `batch` ints in [0, maximum]."""
+def _per_request(value, batch, default, upper, name):
+    """Host metadata for each of `batch` requests: None (every request gets
+    `default`), a single int for all, or a sequence of `batch` ints in [0, upper]."""
     if value is None:
-        values = [default] * batch
-    elif type(value) is int:
-        values = [value] * batch
-    else:
-        values = list(value)
-    if len(values) != batch or any(type(x) is not int or not 0 <= x <= maximum for x in values):
-        raise ValueError(f"{name} must contain {batch} integers in [0,{maximum}]")
-    return values
+        return [default] * batch
+    seq = [value] * batch if type(value) is int else list(value)
+    if len(seq) != batch:
+        raise ValueError(f"{name} must hold {batch} entries, got {len(seq)}")
+    for item in seq:
+        _count(item, name, 0, upper)
+    return seq
+
+
+class _Call:
+    """One native call being assembled: operands are checked and their
+    pointers appended in the ABI's argument order."""
+
+    def __init__(self, ops, symbol):
+        self.ops, self.symbol = ops, symbol
+        self.args, self.held = [], []
+        self.device = None
+
+    def operand(self, x, dtype, name, rank=None, shape=None):
+        torch = self.ops.torch
+        if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
+            raise TypeError(f"{name}: a GPU (torch 'cuda' device) tensor is required")
+        if x.dtype != dtype:
+            raise TypeError(f"{name}: dtype {x.dtype} given, {dtype} required")
+        if not x.is_contiguous():
+            raise TypeError(f"{name}: contiguous row-major storage required")
+        if x.requires_grad:
+            raise ValueError(f"{name}: tensors that require grad are not accepted (inference only)")
+        if rank is not None and x.dim() != rank:
+            raise ValueError(f"{name}: rank {rank} required, got {x.dim()}")
+        if x.dim() == 0 or x.numel() == 0:
+            raise ValueError(f"{name}: an empty or zero-rank tensor is not accepted")
+        for axis, extent in enumerate(x.shape):
+            _count(extent, f"{name}.shape[{axis}]")
+        if x.numel() * x.element_size() > INT64_MAX:
+            raise ValueError(f"{name}: byte extent beyond signed 64-bit indexing")
+        if self.device is None:
+            self.device = x.device
+        elif x.device != self.device:
+            raise ValueError(f"{name}: on {x.device}, the call's operands are on {self.device}")
+        if shape is not None and tuple(x.shape) != tuple(shape):
+            raise ValueError(f"{name}: shape {tuple(shape)} required, got {tuple(x.shape)}")
+        self.held.append(x)
+        self.args.append(x.data_ptr())
+        return x
+
+    def optional(self, x, dtype, name, shape):
+        if x is None:
+            self.args.append(None)
+            return None
+        return self.operand(x, dtype, name, shape=shape)
+
+    def output(self, shape, dtype):
+        y = self.ops.torch.empty(shape, dtype=dtype, device=self.device)
+        self.held.append(y)
+        self.args.append(y.data_ptr())
+        return y
+
+    def workspace(self, shape, needed):
+        if not needed:
+            self.args.append(None)
+            return None
+        return self.output(shape, self.ops.torch.float32)
+
+    def scalars(self, *values):
+        self.args.extend(values)
+
+    def run(self):
+        torch = self.ops.torch
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device)
+            for x in self.held:
+                x.record_stream(stream)
+            status = getattr(self.ops.lib, self.symbol)(*self.args, stream.cuda_stream, self.device.index)
+        if status != 0:
+            detail = self.ops.lib.ti_v2_last_error().decode("utf-8", errors="replace")
+            raise RuntimeError(f"{self.symbol} failed ({status}): {detail}")
 
 
 class NativeOps:
+    """Inference-only device ops over the v2 ABI; operands are torch GPU tensors,
+    work is queued on the current torch stream of their device."""
+
     def __init__(self, library_path=None):
         import torch
         self.torch = torch
-        path = require(BACKEND_LIB) if library_path is None else library_path
-        self.library_path = str(Path(path).expanduser().resolve(strict=True))
+        where = require(BACKEND_LIB) if library_path is None else library_path
+        self.library_path = str(Path(where).expanduser().resolve(strict=True))
         self.lib = ctypes.CDLL(self.library_path)
-        p, i, u = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
-        table = {
-            "ti_v2_gemm_f16": [p, p, p, p, i, i, i, i, i, u, i],
-            "ti_v2_gemm_i8": [p, p, p, p, p, i, i, i, i, i, u, i],
-            "ti_v2_gemm_ex_f16": [p, p, p, p, p, i, i, i, i, i, u, i],
-            "ti_v2_gemm_ex_i8": [p, p, p, p, p, p, i, i, i, i, i, u, i],
-            "ti_v2_legacy_gemm_f32": [p, p, p, i, i, i, u, i],
-            "ti_v2_attention_f16": [p, p, p, p, p, p, p, i, i, i, i, i, i, i, u, i],
-            "ti_v2_layernorm_f16": [p, p, p, p, i, i, ctypes.c_float, u, i],
-            "ti_v2_gelu_new_f16": [p, p, ctypes.c_int64, u, i],
-            "ti_v2_softmax_f16": [p, p, i, i, u, i],
-        }
-        self.lib.ti_v2_abi_version.argtypes, self.lib.ti_v2_abi_version.restype = [], i
-        self.lib.ti_v2_last_error.argtypes, self.lib.ti_v2_last_error.restype = [], ctypes.c_char_p
+        self._declare("ti_v2_abi_version", [], ctypes.c_int)
+        self._declare("ti_v2_last_error", [], ctypes.c_char_p)
+        self._declare("ti_v2_gemm_catalog_json", [], ctypes.c_char_p)
+        for symbol, codes in _ABI.items():
+            self._declare(symbol, [_CTYPE[c] for c in codes] + _TRAILER, ctypes.c_int)
         if self.lib.ti_v2_abi_version() != 2:
-            raise RuntimeError("native v2 ABI version mismatch")
-        self.lib.ti_v2_gemm_catalog_json.argtypes = []
-        self.lib.ti_v2_gemm_catalog_json.restype = ctypes.c_char_p
+            raise RuntimeError("native v2 ABI version mismatch: version 2 required")
         self.catalog = json.loads(self.lib.ti_v2_gemm_catalog_json())
-        reported = [dict(entry, tile=tuple(entry["tile"])) for entry in self.catalog["configs"]]
-        if reported != list(GEMM_CATALOG):
-            raise RuntimeError("native GEMM catalog does not match wrapper allow-list")
-        for name, args in table.items():
-            fn = getattr(self.lib, name)
-            fn.argtypes, fn.restype = args, i
+        listed = tuple({**entry, "tile": tuple(entry["tile"])} for entry in self.catalog["configs"])
+        if listed != GEMM_CATALOG:
+            raise RuntimeError("native GEMM catalog differs from the wrapper's GEMM_CATALOG")
 
-    # -- checks ---------------------------------------------------------------
-    def _tensor(self, tensor, dtype, name, ndim=None, device=None):
-        t = self.torch
-        if not isinstance(tensor, t.Tensor) or tensor.device.type != "cuda":
-            raise TypeError(f"{name} must be a CUDA Tensor")
-        if tensor.dtype != dtype or not tensor.is_contiguous():
-            raise TypeError(f"{name} must have dtype={dtype} and contiguous row-major storage")
-        if tensor.requires_grad:
-            raise ValueError(f"{name} requires_grad is unsupported by inference-only native ops")
-        if ndim is not None and tensor.ndim != ndim:
-            raise ValueError(f"{name} must have rank {ndim}")
-        if tensor.ndim == 0 or tensor.numel() == 0:
-            raise ValueError(f"{name} must have at least one nonempty dimension")
-        for axis, size in enumerate(tensor.shape):
-            _dim(size, f"{name}.shape[{axis}]")
-        if tensor.numel() > (2**63 - 1) // tensor.element_size():
-            raise ValueError(f"{name} byte extent exceeds signed 64-bit indexing")
-        if device is not None and tensor.device != device:
-            raise ValueError(f"{name} must be on {device}")
-        return tensor
+    def _declare(self, symbol, argtypes, restype):
+        fn = getattr(self.lib, symbol)
+        fn.argtypes, fn.restype = argtypes, restype
 
-    @staticmethod
-    def _ptr(tensor):
-        return None if tensor is None else tensor.data_ptr()
-
-    def _call(self, name, tensors, args):
-        device = tensors[0].device
-        with self.torch.cuda.device(device):
-            stream = self.torch.cuda.current_stream(device)
-            for tensor in tensors:
-                if tensor is not None:
-                    tensor.record_stream(stream)
-            status = getattr(self.lib, name)(*args, stream.cuda_stream, device.index)
-            if status:
-                reason = self.lib.ti_v2_last_error().decode("utf-8", errors="replace")
-                raise RuntimeError(f"{name} failed ({status}): {reason}")
-
-    def _gemm_args(self, a, b, bias, config, output_dtype, weight_dtype):
-        t = self.torch
-        self._tensor(a, t.float16, "a", 2)
-        self._tensor(b, weight_dtype, "b", 2, a.device)
+    # -- GEMMs --------------------------------------------------------------
+    def _linear(self, symbol, a, weight, weight_dtype, scales, bias, config, output_dtype):
+        torch = self.torch
+        call = _Call(self, symbol)
+        call.operand(a, torch.float16, "a", rank=2)
+        call.operand(weight, weight_dtype, "b", rank=2)
+        if scales is not None:
+            call.operand(scales, torch.float32, "scales", rank=1)
+            if scales.shape[0] != weight.shape[1]:
+                raise ValueError("scales must have shape [N], one scale per output column")
         m, k = a.shape
-        if b.shape[0] != k:
-            raise ValueError("GEMM a[M,K] and b[K,N] inner dimensions differ")
-        n = b.shape[1]
-        if type(config) is not int or not 0 <= config < len(GEMM_CATALOG):
-            raise ValueError("GEMM config must be allow-listed ID0..11")
-        only = getattr(self, "catalog", {}).get("only_config", -1)
-        if only != -1 and config != only:
-            raise ValueError("GEMM config is unavailable in this single-candidate build")
-        if (m - 1) // GEMM_CATALOG[config]["tile"][0] + 1 > 65535:
-            raise ValueError("GEMM M exceeds grid-y limit")
-        if bias is not None:
-            self._tensor(bias, t.float16, "bias", 1, a.device)
-            if bias.shape != (n,):
-                raise ValueError("bias must have shape [N]")
-        dtype = t.float16 if output_dtype is None else output_dtype
-        if dtype not in (t.float16, t.float32):
+        if weight.shape[0] != k:
+            raise ValueError(f"a is [{m}, {k}] but b has {weight.shape[0]} rows")
+        n = weight.shape[1]
+        if type(config) is not int or config not in range(len(GEMM_CATALOG)):
+            raise ValueError(f"GEMM config must be one of the catalog ids 0..{len(GEMM_CATALOG) - 1}")
+        only = self.catalog.get("only_config", -1)
+        if only not in (-1, config):
+            raise ValueError(f"this build compiles only GEMM config {only}")
+        rows_per_tile = GEMM_CATALOG[config]["tile"][0]
+        if (m + rows_per_tile - 1) // rows_per_tile > 65535:
+            raise ValueError("M needs more than 65535 row tiles")
+        call.optional(bias, torch.float16, "bias", shape=(n,))
+        out_dtype = torch.float16 if output_dtype is None else output_dtype
+        if out_dtype not in (torch.float16, torch.float32):
             raise TypeError("output_dtype must be torch.float16 or torch.float32")
-        out = t.empty((m, n), dtype=dtype, device=a.device)
-        return out, (m, n, k, int(dtype == t.float32), config)
+        y = call.output((m, n), out_dtype)
+        call.workspace((m, n), GEMM_CATALOG[config]["epilogue"] == "separate")
+        call.scalars(m, n, k, 1 if out_dtype == torch.float32 else 0, config)
+        call.run()
+        return y
 
-    # -- ops --------------------------------------------------------------------
     def gemm(self, a, b, *, bias=None, config=0, output_dtype=None):
-        out, dims = self._gemm_args(a, b, bias, config, output_dtype, self.torch.float16)
-        ws = self.torch.empty(out.shape, dtype=self.torch.float32, device=out.device) if config >= 6 else None
-        tensors = (a, b, bias, out, ws)
-        self._call("ti_v2_gemm_ex_f16", tensors, tuple(map(self._ptr, tensors)) + dims)
-        return out
+        """y = a[M,K] @ b[K,N] (+ bias), fp16 weights, fp32 accumulation."""
+        return self._linear("ti_v2_gemm_ex_f16", a, b, self.torch.float16, None, bias, config, output_dtype)
 
     def gemm_int8(self, a, b, scales, *, bias=None, config=0, output_dtype=None):
-        self._tensor(a, self.torch.float16, "a", 2)
-        self._tensor(b, self.torch.int8, "b", 2, a.device)
-        self._tensor(scales, self.torch.float32, "scales", 1, a.device)
-        if scales.shape != (b.shape[1],):
-            raise ValueError("scales must have shape [N], one scale per output channel")
-        out, dims = self._gemm_args(a, b, bias, config, output_dtype, self.torch.int8)
-        ws = self.torch.empty(out.shape, dtype=self.torch.float32, device=out.device) if config >= 6 else None
-        tensors = (a, b, scales, bias, out, ws)
-        self._call("ti_v2_gemm_ex_i8", tensors, tuple(map(self._ptr, tensors)) + dims)
-        return out
+        """W8A16: b int8 [K,N] with one fp32 scale per output column."""
+        if scales is None:
+            raise TypeError("scales: a GPU (torch 'cuda' device) tensor is required")
+        return self._linear("ti_v2_gemm_ex_i8", a, b, self.torch.int8, scales, bias, config, output_dtype)
 
     def legacy_gemm(self, a, b):
-        self._tensor(a, self.torch.float32, "a", 2)
-        self._tensor(b, self.torch.float32, "b", 2, a.device)
-        if a.shape[1] != b.shape[0] or (a.shape[0] - 1) // 64 + 1 > 65535:
-            raise ValueError("invalid FP32 GEMM dimensions")
-        out = self.torch.empty((a.shape[0], b.shape[1]), dtype=a.dtype, device=a.device)
-        tensors = (a, b, out)
-        self._call("ti_v2_legacy_gemm_f32", tensors,
-                   tuple(map(self._ptr, tensors)) + (a.shape[0], b.shape[1], a.shape[1]))
-        return out
+        """FP32 y = a @ b through ti_v2_legacy_gemm_f32."""
+        torch = self.torch
+        call = _Call(self, "ti_v2_legacy_gemm_f32")
+        call.operand(a, torch.float32, "a", rank=2)
+        call.operand(b, torch.float32, "b", rank=2)
+        (m, k), n = a.shape, b.shape[1]
+        if b.shape[0] != k or (m + 63) // 64 > 65535:
+            raise ValueError(f"FP32 GEMM: a [{m}, {k}] and b {list(b.shape)} do not multiply within the grid limit")
+        y = call.output((m, n), torch.float32)
+        call.scalars(m, n, k)
+        call.run()
+        return y
+
+    # -- row ops -------------------------------------------------------------
+    def _rows(self, x):
+        cols = x.shape[-1]
+        return _count(x.numel() // cols, "rows"), cols
 
     def layernorm(self, x, gamma, beta, *, eps=1e-5):
-        t = self.torch
-        self._tensor(x, t.float16, "x")
-        self._tensor(gamma, t.float16, "gamma", 1, x.device)
-        self._tensor(beta, t.float16, "beta", 1, x.device)
-        cols = x.shape[-1]
-        rows = _dim(x.numel() // cols, "rows")
-        if gamma.shape != (cols,) or beta.shape != (cols,) or not math.isfinite(eps) or eps <= 0:
-            raise ValueError("LayerNorm gamma/beta shape or eps invalid")
-        out = t.empty_like(x)
-        tensors = (x, gamma, beta, out)
-        self._call("ti_v2_layernorm_f16", tensors, tuple(map(self._ptr, tensors)) + (rows, cols, eps))
-        return out
+        """fp16 LayerNorm over the last axis, gamma/beta fp16 [cols]."""
+        torch = self.torch
+        call = _Call(self, "ti_v2_layernorm_f16")
+        call.operand(x, torch.float16, "x")
+        rows, cols = self._rows(x)
+        call.operand(gamma, torch.float16, "gamma", rank=1)
+        call.operand(beta, torch.float16, "beta", rank=1)
+        if gamma.shape[0] != cols or beta.shape[0] != cols:
+            raise ValueError(f"gamma and beta must have shape [{cols}]")
+        if not (isinstance(eps, (int, float)) and math.isfinite(eps) and eps > 0):
+            raise ValueError("eps must be finite and positive")
+        y = call.output(tuple(x.shape), torch.float16)
+        call.scalars(rows, cols, float(eps))
+        call.run()
+        return y
 
     def gelu_new(self, x):
-        self._tensor(x, self.torch.float16, "x")
-        out = self.torch.empty_like(x)
-        self._call("ti_v2_gelu_new_f16", (x, out), (x.data_ptr(), out.data_ptr(), x.numel()))
-        return out
+        """fp16 tanh-approximation GELU, elementwise."""
+        call = _Call(self, "ti_v2_gelu_new_f16")
+        call.operand(x, self.torch.float16, "x")
+        y = call.output(tuple(x.shape), self.torch.float16)
+        call.scalars(x.numel())
+        call.run()
+        return y
 
     def softmax(self, x):
-        self._tensor(x, self.torch.float16, "x")
-        cols = x.shape[-1]
-        rows = _dim(x.numel() // cols, "rows")
-        out = self.torch.empty_like(x)
-        self._call("ti_v2_softmax_f16", (x, out), (x.data_ptr(), out.data_ptr(), rows, cols))
-        return out
+        """fp16 softmax over the last axis."""
+        call = _Call(self, "ti_v2_softmax_f16")
+        call.operand(x, self.torch.float16, "x")
+        rows, cols = self._rows(x)
+        y = call.output(tuple(x.shape), self.torch.float16)
+        call.scalars(rows, cols)
+        call.run()
+        return y
 
+    # -- attention -------------------------------------------------------------
     def attention(self, q, k, v, *, q_lengths=None, kv_lengths=None, query_offsets=None,
                   causal=True, config=0):
-        t = self.torch
-        self._tensor(q, t.float16, "q", 4)
-        self._tensor(k, t.float16, "k", 4, q.device)
-        self._tensor(v, t.float16, "v", 4, q.device)
-        batch, heads, nq, d = q.shape
+        """q [B,H,Q,D], k/v [B,H,K,D] fp16, D in {64, 128}; per-request query
+        and key counts and absolute query offsets for the causal mask."""
+        torch = self.torch
+        call = _Call(self, "ti_v2_attention_f16")
+        call.operand(q, torch.float16, "q", rank=4)
+        batch, heads, nq, dim = q.shape
+        call.operand(k, torch.float16, "k", rank=4)
+        call.operand(v, torch.float16, "v", rank=4)
         nk = k.shape[2]
-        if k.shape != v.shape or k.shape[:2] != q.shape[:2] or k.shape[3] != d or d not in (64, 128):
-            raise ValueError("attention expects q[B,H,Q,D], k/v[B,H,K,D], D64/128")
-        if (batch > 65535 or heads > 65535 or type(causal) is not bool or type(config) is not int
-                or config not in (0, 1)):
-            raise ValueError("invalid attention grid, causal flag or config")
-        ql = _metadata(q_lengths, batch, nq, nq, "q_lengths")
-        kl = _metadata(kv_lengths, batch, nk, nk, "kv_lengths")
-        offsets = _metadata(query_offsets, batch, 0, _I32_MAX - nq, "query_offsets")
-        with t.cuda.device(q.device):
-            meta = tuple(t.tensor(vals, dtype=t.int32, device=q.device) for vals in (ql, kl, offsets))
-            out = t.empty_like(q)
-            tensors = (q, k, v, out) + meta
-            self._call("ti_v2_attention_f16", tensors,
-                       tuple(map(self._ptr, tensors)) + (batch, heads, nq, nk, d, int(causal), config))
-        return out
+        if (tuple(v.shape) != tuple(k.shape) or tuple(k.shape[:2]) != (batch, heads)
+                or k.shape[3] != dim or dim not in (64, 128)):
+            raise ValueError("attention takes q [B,H,Q,D] and k, v [B,H,K,D] with D 64 or 128")
+        if batch > 65535 or heads > 65535:
+            raise ValueError("batch and heads must each be at most 65535")
+        if type(causal) is not bool or type(config) is not int or config not in (0, 1):
+            raise ValueError("causal must be a bool and config 0 or 1")
+        meta = (_per_request(q_lengths, batch, nq, nq, "q_lengths"),
+                _per_request(kv_lengths, batch, nk, nk, "kv_lengths"),
+                _per_request(query_offsets, batch, 0, INT32_MAX - nq, "query_offsets"))
+        with torch.cuda.device(q.device):
+            y = call.output(tuple(q.shape), torch.float16)
+            for values in meta:
+                call.held.append(torch.tensor(values, dtype=torch.int32, device=q.device))
+                call.args.append(call.held[-1].data_ptr())
+        call.scalars(batch, heads, nq, nk, dim, int(causal), config)
+        call.run()
+        return y
