@@ -274,5 +274,9 @@ def test_greedy_tokens_match_oracle(model, cpu_model, batch):
         margins[b] = float(lg[0][cpu[b][i]] - lg[0][gpu[b][i]])
     print(f"greedy batch {batch}: {batch - len(diverged)}/{batch} identical over {NEW_TOKENS} tokens; "
           f"first divergence index {diverged}; oracle logit gap at divergence {margins}")
-    assert all(0 <= m <= 5e-2 for m in margins.values()), margins
+    # A divergence is accepted only at a near-tie: the oracle's own gap between
+    # the two picks at most 1e-2 (about twice the measured GPU-vs-oracle logit
+    # error, 0.004), and at most a quarter of the requests may diverge at all.
+    assert all(0 <= m <= 1e-2 for m in margins.values()), margins
+    assert len(diverged) <= batch // 4, diverged
     model.reset_all()
