@@ -19,6 +19,23 @@ int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const float* scales
                          const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m,
                          int n, int k, int epilogue, uintptr_t stream, int device);
 
+/* ti_amd_gemm_ex_i8_noalloc: no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): ti_v2_gemm_ex_i8 with the same
+ * arguments, validation, status codes and result bits, but its split-K fp32
+ * partials live in a fixed 8 MiB device array of the library (one per GPU,
+ * held until the process ends) instead of the per-(device, stream) scratch
+ * ti_v2_gemm_ex_i8 allocates on a stream's first call.  It calls no hipMalloc,
+ * hipFree or allocating library routine.  A shape whose split plan needs more
+ * than 8 MiB returns TI_V2_INVALID_ARGUMENT with the byte counts in
+ * ti_v2_last_error() (no shape under the current plans does: the largest
+ * needs at most 8 380 416 bytes).  Every call on one GPU shares that array: calls
+ * that overlap in time on one GPU (different streams, or threads) race;
+ * calls ordered on one stream do not. */
+int ti_amd_gemm_ex_i8_noalloc(const uint16_t* a, const int8_t* b, const float* scales,
+                              const uint16_t* bias, void* y, float* workspace, int m, int n, int k,
+                              int dtype, int config, uintptr_t stream, int device);
+
 /* Panel-packed int8 weights for the decode GEMV (M <= 32).  The reference keeps
  * q row-major [K,N] (reference kernels/src/cuda/tc/gemm.cu:21 reads
  * q[r*n + c]); the runtime packs every linear once at load so that each wave

@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <initializer_list>
 #include <limits>
+#include <mutex>
 
 #include "../../include/tinyinfer_amd_ext.h"
 #include "../../include/tinyinfer_backend_v2.h"
@@ -66,13 +67,15 @@ int check_workspace(const void* p, int m, int n, int config) {
   return TI_V2_OK;
 }
 
+// `split_scratch`: where split-K partials go (null: the library's
+// per-(device, stream) scratch, allocated on the stream's first call).
 int run_gemm(const uint16_t* a, const void* w, bool int8, const float* scales, const uint16_t* bias,
              void* y, float* workspace, int m, int n, int k, int dtype, int config, uintptr_t stream,
-             int device) {
+             int device, const tia::Scratch* split_scratch = nullptr) {
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t err = hipSuccess;
-  const tia::Scratch* scratch = tia::library_scratch(device, st, &err);
-  if (!scratch) return hip_status(err);
+  const tia::Scratch* lib_scratch = split_scratch ? split_scratch : tia::library_scratch(device, st, &err);
+  if (!lib_scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -92,7 +95,7 @@ int run_gemm(const uint16_t* a, const void* w, bool int8, const float* scales, c
     g.epi.y = y;
   }
   g.epi.ldy = n;
-  err = tia::gemm(g, scratch, st);
+  err = tia::gemm(g, lib_scratch, st);
   if (err == hipSuccess && separate) err = tia::bias_epilogue(workspace, bias, y, int64_t(m) * n, n, dtype, st);
   return hip_status(err);
 }
@@ -136,6 +139,69 @@ extern "C" int ti_v2_gemm_ex_i8(const uint16_t* a, const int8_t* b, const float*
   if (!aligned(scales, 4)) return fail(TI_V2_INVALID_ARGUMENT, "scales pointer must be nonnull aligned FP32[N]");
   if ((status = check_workspace(workspace, m, n, config))) return status;
   return run_gemm(a, b, true, scales, bias, y, workspace, m, n, k, dtype, config, stream, device);
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant of ti_v2_gemm_ex_i8.  Its split-K partials live in a
+// file-scope device array instead of the library's hipMalloc'd per-stream
+// scratch.  In host code `scratch` names a host-side stand-in, not device
+// memory: kernels get the per-device address hipGetSymbolAddress returns.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+constexpr size_t kNoAllocScratchFloats = kNoAllocScratchBytes / sizeof(float);
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex noalloc_mutex;
+float* noalloc_base[kNoAllocMaxDevices] = {};
+
+// Device address of `scratch` on `device` (the current device: begin() checked
+// it), looked up once per device and kept.
+float* noalloc_scratch(int device, hipError_t* err) {
+  if (device >= kNoAllocMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(noalloc_mutex);
+  if (!noalloc_base[device]) {
+    void* address = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !address) {
+      *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    noalloc_base[device] = static_cast<float*>(address);
+  }
+  return noalloc_base[device];
+}
+}  // namespace
+
+extern "C" int ti_amd_gemm_ex_i8_noalloc(const uint16_t* a, const int8_t* b, const float* scales,
+                                         const uint16_t* bias, void* y, float* workspace, int m, int n,
+                                         int k, int dtype, int config, uintptr_t stream, int device) {
+  int status = begin(device);
+  if (status) return status;
+  if ((status = check_gemm(a, b, bias, y, m, n, k, dtype, config, true))) return status;
+  if (!aligned(scales, 4)) return fail(TI_V2_INVALID_ARGUMENT, "scales pointer must be nonnull aligned FP32[N]");
+  if ((status = check_workspace(workspace, m, n, config))) return status;
+  // The split plan is the one ti_v2_gemm_ex_i8 takes with the library scratch,
+  // so both entry points return the same bits; a plan that needs more than the
+  // fixed array is refused rather than changed.
+  const size_t need = tia::row_major_gemm_scratch_floats(m, n, k, tia::kScratchPartialFloats);
+  if (need > kNoAllocScratchFloats) {
+    char text[200];
+    std::snprintf(text, sizeof(text),
+                  "no-allocation GEMM: this shape's split-K plan needs %zu bytes of scratch, above the fixed "
+                  "%zu-byte maximum; call ti_v2_gemm_ex_i8",
+                  need * sizeof(float), kNoAllocScratchBytes);
+    return fail(TI_V2_INVALID_ARGUMENT, text);
+  }
+  hipError_t err = hipSuccess;
+  float* base = noalloc_scratch(device, &err);
+  if (!base) return hip_status(err);
+  const tia::Scratch fixed{base, kNoAllocScratchFloats};
+  return run_gemm(a, b, true, scales, bias, y, workspace, m, n, k, dtype, config, stream, device, &fixed);
 }
 
 extern "C" int ti_v2_gemm_f16(const uint16_t* a, const uint16_t* b, const uint16_t* bias, void* y,
@@ -198,8 +264,8 @@ extern "C" int ti_v2_attention_f16(const uint16_t* q, const uint16_t* k, const u
   // capture) the one-pass kernel runs.
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t scratch_err = hipSuccess;
-  const tia::Scratch* scratch = tia::library_scratch(device, st, &scratch_err);
-  return hip_status(tia::attention(a, st, scratch));
+  const tia::Scratch* lib_scratch = tia::library_scratch(device, st, &scratch_err);
+  return hip_status(tia::attention(a, st, lib_scratch));
 }
 
 extern "C" int ti_v2_layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
@@ -241,8 +307,8 @@ extern "C" int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const fl
     return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t err = hipSuccess;
-  const tia::Scratch* scratch = tia::library_scratch(device, st, &err);
-  if (!scratch) return hip_status(err);
+  const tia::Scratch* lib_scratch = tia::library_scratch(device, st, &err);
+  if (!lib_scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -258,7 +324,7 @@ extern "C" int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const fl
   g.epi.ldy = n;
   g.epi.residual = residual;
   g.epi.ldr = n;
-  return hip_status(tia::gemm(g, scratch, st));
+  return hip_status(tia::gemm(g, lib_scratch, st));
 }
 
 extern "C" int64_t ti_amd_packed_w8_bytes(int k, int n) {
@@ -301,8 +367,8 @@ extern "C" int ti_amd_gemm_w16p_fused(const uint16_t* a, const void* packed16, c
     return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t err = hipSuccess;
-  const tia::Scratch* scratch = tia::library_scratch(device, st, &err);
-  if (!scratch) return hip_status(err);
+  const tia::Scratch* lib_scratch = tia::library_scratch(device, st, &err);
+  if (!lib_scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -317,7 +383,7 @@ extern "C" int ti_amd_gemm_w16p_fused(const uint16_t* a, const void* packed16, c
   g.epi.ldy = n;
   g.epi.residual = residual;
   g.epi.ldr = n;
-  return hip_status(tia::gemm(g, scratch, st));
+  return hip_status(tia::gemm(g, lib_scratch, st));
 }
 
 extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, const float* scales,
@@ -334,8 +400,8 @@ extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, cons
     return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t err = hipSuccess;
-  const tia::Scratch* scratch = tia::library_scratch(device, st, &err);
-  if (!scratch) return hip_status(err);
+  const tia::Scratch* lib_scratch = tia::library_scratch(device, st, &err);
+  if (!lib_scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -352,7 +418,7 @@ extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, cons
   g.epi.ldy = n;
   g.epi.residual = residual;
   g.epi.ldr = n;
-  return hip_status(tia::gemm(g, scratch, st));
+  return hip_status(tia::gemm(g, lib_scratch, st));
 }
 
 extern "C" int ti_amd_gemm_w8p_ln_fused(const uint16_t* a, const uint16_t* gamma, const uint16_t* beta, float eps,

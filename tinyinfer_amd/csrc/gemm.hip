@@ -1256,6 +1256,24 @@ __global__ __launch_bounds__(256) void legacy_f32_kernel(const float* a, const f
 // ---------------------------------------------------------------------------
 // Host-side dispatch
 // ---------------------------------------------------------------------------
+// Number of K splits of the row-major M <= 32 kernel: aim for ~2 workgroups
+// per CU (a 2.4 MB GEMV is latency-bound, so every CU should have loads in
+// flight), with the fp32 partials (splits * M * N * 4 bytes, L2/MALL traffic)
+// at most twice the weight bytes and within `capacity` floats (0: no scratch,
+// one split).  Returns the split count after rounding to whole step ranges.
+int skinny_splits(int m, int n, int k, size_t capacity) {
+  const int ntile = (n + 63) / 64, steps = (k + 31) / 32;
+  int splits = 1;
+  if (capacity > 0) {
+    const int target = (2 * 256 + ntile - 1) / ntile;
+    const int max_by_traffic = std::max(1, k / (2 * std::max(1, m)));
+    splits = std::max(1, std::min(target, std::min(steps, max_by_traffic)));
+    while (splits > 1 && size_t(splits) * m * n > capacity) --splits;
+  }
+  const int spb = (steps + splits - 1) / splits;
+  return (steps + spb - 1) / spb;
+}
+
 template <bool INT8, int MT>
 hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch* s,
                          hipStream_t stream, int* deferred) {
@@ -1265,19 +1283,8 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   p.ldw = g.ldw > 0 ? g.ldw : g.n;
   p.ntile = (g.n + 63) / 64;
   p.steps = (g.k + 31) / 32;
-  // Number of K splits: aim for ~2 workgroups per CU (a 2.4 MB GEMV is
-  // latency-bound, so every CU should have loads in flight), with the fp32
-  // partials (splits * M * N * 4 bytes, L2/MALL traffic) at most twice the
-  // weight bytes and within the scratch.
-  int splits = 1;
-  if (s && s->partials) {
-    const int target = (2 * 256 + p.ntile - 1) / p.ntile;
-    const int max_by_traffic = std::max(1, g.k / (2 * std::max(1, g.m)));
-    splits = std::max(1, std::min(target, std::min(p.steps, max_by_traffic)));
-    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
-  }
+  int splits = skinny_splits(g.m, g.n, g.k, (s && s->partials) ? s->partial_floats : 0);
   const int spb = (p.steps + splits - 1) / splits;
-  splits = (p.steps + spb - 1) / spb;
   p.steps_per_block = spb;
   p.splits = splits;
   p.defer = deferred != nullptr;
@@ -1736,6 +1743,20 @@ hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, i
 // workgroups run (at least 4 steps each), then splitk_epilogue_kernel sums the
 // splits in a fixed order and applies the epilogue.  Canonical (batch-invariant)
 // calls stay unsplit: their K order must not depend on M.
+// Split count of the row-major M > 32 kernel (0 capacity or a canonical call:
+// one split), after rounding to whole step ranges.
+int tiled_splits(int m, int n, int k, bool canonical, size_t capacity) {
+  const int steps = (k + TBK - 1) / TBK;
+  const int64_t tiles = int64_t((n + TBN - 1) / TBN) * ((m + TBM - 1) / TBM);
+  int splits = 1;
+  if (!canonical && capacity > 0 && tiles < 256) {
+    splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, steps / 4)));
+    while (splits > 1 && size_t(splits) * m * n > capacity) --splits;
+  }
+  const int per = (steps + splits - 1) / splits;
+  return (steps + per - 1) / per;
+}
+
 template <bool INT8>
 hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, const Scratch* s, hipStream_t stream) {
   TiledParams p{};
@@ -1743,14 +1764,8 @@ hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, const Scratch* 
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.ldw = g.ldw > 0 ? g.ldw : g.n;
   const int steps = (g.k + TBK - 1) / TBK;
-  const int64_t tiles = int64_t((g.n + TBN - 1) / TBN) * ((g.m + TBM - 1) / TBM);
-  int splits = 1;
-  if (!g.canonical && s && s->partials && tiles < 256) {
-    splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, steps / 4)));
-    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
-  }
+  int splits = tiled_splits(g.m, g.n, g.k, g.canonical, (s && s->partials) ? s->partial_floats : 0);
   p.steps_per_split = (steps + splits - 1) / splits;
-  splits = (steps + p.steps_per_split - 1) / p.steps_per_split;
   p.partials = splits > 1 ? s->partials : nullptr;
   const dim3 grid(unsigned((g.n + TBN - 1) / TBN), unsigned((g.m + TBM - 1) / TBM), unsigned(splits));
 #define TIA_TILED(WV, AV) hipLaunchKernelGGL((tiled_kernel<INT8, WV, AV>), grid, dim3(256), 0, stream, p)
@@ -1821,6 +1836,12 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   if (g.m <= 32) return g.w_int8 ? launch_skinny<true, 2>(g, wvec, avec, s, stream, deferred)
                                  : launch_skinny<false, 2>(g, wvec, avec, s, stream, deferred);
   return g.w_int8 ? launch_tiled<true>(g, wvec, avec, s, stream) : launch_tiled<false>(g, wvec, avec, s, stream);
+}
+
+size_t row_major_gemm_scratch_floats(int m, int n, int k, size_t capacity) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  const int splits = m <= 32 ? skinny_splits(m, n, k, capacity) : tiled_splits(m, n, k, false, capacity);
+  return splits > 1 ? size_t(splits) * size_t(m) * size_t(n) : 0;
 }
 
 hipError_t argmax_partials(const float* vals, const int32_t* idx, int groups, int rows, int32_t* out,

@@ -131,6 +131,11 @@ hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows
                                      const uint16_t* bias, uint16_t* x, const uint16_t* gamma,
                                      const uint16_t* beta, uint16_t* norm, float eps,
                                      hipStream_t stream, bool p32 = false);
+// Floats of split-K partials that gemm() keeps in a scratch of `capacity`
+// floats for row-major weights without packing, LayerNorm or P32 operands (the
+// v2 ABI's GEMMs); 0 when the call runs unsplit.
+size_t row_major_gemm_scratch_floats(int m, int n, int k, size_t capacity);
+
 // Per-(device, stream) scratch owned by the library, created on the first call
 // on that stream (never under graph capture).  Returns nullptr and sets *err if
 // it cannot be created.
