@@ -1,6 +1,6 @@
-// libtinyinfer_diag.so: machine-limit probes for bench.py (no reference
-// counterpart, not used by any product path).  They measure what the roofline
-// figures are compared against on this MI355X:
+// benchlib/liblimits.so: machine-limit probes for bench.py only (not part of
+// the product libraries or headers; no reference counterpart).  They measure
+// what the roofline figures are compared against on this MI355X:
 //  * tia_diag_empty: an empty kernel; back-to-back graph replays of it give the
 //    per-launch floor that every kernel of the path pays.
 //  * tia_diag_stream: a pure streaming read, `wgs` workgroups each reading
@@ -10,7 +10,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/tinyinfer_amd_diag.h"
+
+// Entry points (C ABI, loaded by bench.py through ctypes):
+//   int tia_diag_empty(uintptr_t stream): enqueue one empty kernel.
+//   int tia_diag_stream(const void* src, unsigned* out, int64_t per_wg, int wgs,
+//                       int threads, uintptr_t stream): enqueue a streaming read
+//     of wgs * per_wg bytes from 16-byte aligned `src`, workgroup w reading
+//     [w * per_wg, (w + 1) * per_wg) with `threads` threads (a multiple of 64, at
+//     most 1024); `out` receives wgs * threads dwords; per_wg a positive multiple
+//     of 1024.  Both return 0, or 1 on invalid arguments or a launch error.
 
 namespace {
 

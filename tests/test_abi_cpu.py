@@ -11,12 +11,11 @@ import pytest
 
 import oracle
 from tests.conftest import GOLDEN, ROOT
-from tinyinfer_amd import BACKEND_LIB, CODEC_LIB, DIAG_LIB, LLM_LIB
+from tinyinfer_amd import BACKEND_LIB, CODEC_LIB, LLM_LIB
 
 HEADERS = {"tinyinfer_backend_v2.h": BACKEND_LIB, "tinyinfer_backend.h": BACKEND_LIB,
            "tinyinfer_amd_ext.h": BACKEND_LIB,
-           "tinyinfer_host_codec.h": CODEC_LIB, "tinyinfer_llm.h": LLM_LIB,
-           "tinyinfer_amd_diag.h": DIAG_LIB}
+           "tinyinfer_host_codec.h": CODEC_LIB, "tinyinfer_llm.h": LLM_LIB}
 
 
 def declared(header):

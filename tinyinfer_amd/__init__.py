@@ -21,7 +21,6 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 BACKEND_LIB = PACKAGE_DIR / "libtinyinfer_backend.so"
 LLM_LIB = PACKAGE_DIR / "libtinyinfer_llm.so"
 CODEC_LIB = PACKAGE_DIR / "libtinyinfer_host_codec.so"
-DIAG_LIB = PACKAGE_DIR / "libtinyinfer_diag.so"
 
 
 def require(path: Path) -> str:

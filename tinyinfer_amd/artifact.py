@@ -15,10 +15,13 @@ native loader accepts exactly these two identities.
 """
 from __future__ import annotations
 
+import collections
+import concurrent.futures as cf
 import ctypes
 import hashlib
 import json
 import math
+import os
 from pathlib import Path
 
 import numpy as np
@@ -92,8 +95,8 @@ def quantize_numpy(w_bits: np.ndarray):
     w = np.ascontiguousarray(w_bits, np.uint16).view(np.float16).astype(np.float64)
     mx = np.abs(w).max(axis=0)
     scales = np.where(mx > 0, (mx / 127.0).astype(np.float32), np.float32(1.0)).astype(np.float32)
-    q = np.clip(np.rint(w / scales.astype(np.float64)), -127, 127).astype(np.int8)
-    return q, scales
+    r = np.rint(w / scales.astype(np.float64))
+    return np.clip(r, -127, 127, out=r).astype(np.int8), scales
 
 
 # -- synthetic weights -------------------------------------------------------------
@@ -101,66 +104,109 @@ def _normal_f16(rng, shape, mean, std):
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std) + np.float32(mean)).astype(np.float16)
 
 
+def _quantized(codec, name, bits):
+    """INT8 bytes and scales of fp16 `bits` [K, N]; the native codec and the
+    numpy quantizer must agree byte for byte (reference export_weights.py:146-151)."""
+    q, sc = codec.quantize(bits)
+    q2, sc2 = quantize_numpy(bits)
+    if not (np.array_equal(q, q2) and np.array_equal(sc.view(np.uint32), sc2.view(np.uint32))):
+        raise ValueError(f"native/numpy INT8 bytes differ for {name}")
+    return q, sc
+
+
+def _record(name, dtype, arr):
+    raw = np.ascontiguousarray(arr)
+    return name, dtype, list(arr.shape), raw, hashlib.sha256(memoryview(raw).cast("B")).hexdigest()
+
+
+def _writer_threads():
+    # Generation, quantization and hashing release the GIL; a GPU box gives a
+    # process 16 cores whatever os.cpu_count() reports.
+    return max(1, min(16, os.cpu_count() or 1))
+
+
 def write_synthetic(dest, arch=None, seed=42, precision="int8", std=0.02, progress=None):
     """Write a random-init GPT-2 artifact: every weight matrix, embedding and bias
-    ~ N(0, std), LayerNorm gamma ~ N(1, std), beta ~ N(0, std) (numpy PCG64 from
-    ``seed``), stored fp16; linears and the tied head INT8-quantized.  Returns the
-    manifest path.  Quantized bytes must agree between the native codec and the
-    numpy quantizer, as the reference exporter requires (export_weights.py:146-151).
-    ``progress``, if given, is called with each tensor name as it is written."""
+    ~ N(0, std), LayerNorm gamma ~ N(1, std), beta ~ N(0, std), stored fp16;
+    linears and the tied head INT8-quantized (``precision="int8"``) or kept fp16
+    (``"float16"``).  Tensor i of the manifest order draws from its own numpy
+    PCG64 stream, ``SeedSequence(seed).spawn(count)[i]``, so worker threads build
+    tensors concurrently and the bytes do not depend on their scheduling.
+    Returns the manifest path.  ``progress``, if given, is called with each
+    tensor name as it is written."""
     arch = dict(GPT2_SMALL if arch is None else arch)
+    if precision not in ("int8", "float16"):
+        raise ValueError("precision must be 'int8' or 'float16'")
     dest = Path(dest)
     dest.mkdir(parents=True, exist_ok=True)
     codec = HostCodec() if precision == "int8" else None
-    rng = np.random.Generator(np.random.PCG64(seed))
-    spec = {"generator": "numpy.PCG64", "seed": seed, "std": std, "precision": precision,
+    shapes = list(tensor_shapes(arch).items())
+    streams = np.random.SeedSequence(seed).spawn(len(shapes))
+    spec = {"generator": "numpy.PCG64, tensor i from SeedSequence(seed).spawn(count)[i] in manifest order",
+            "seed": seed, "std": std, "precision": precision,
             "distribution": "matrices/embeddings/biases N(0,std); ln gamma N(1,std); ln beta N(0,std)",
             "architecture": arch}
+
+    def build(index):
+        name, shape = shapes[index]
+        mean = 1.0 if (".ln_" in name or "ln_f" in name) and name.endswith(".weight") else 0.0
+        vals = _normal_f16(np.random.Generator(np.random.PCG64(streams[index])), shape, mean, std)
+        bits = vals.view(np.uint16)
+        if precision == "int8" and len(shape) == 2 and ".h." in name and name.endswith(".weight"):
+            q, sc = _quantized(codec, name, bits)
+            return [_record(name, "int8", q), _record(name + ".scales", "float32", sc)], None
+        return [_record(name, "float16", bits)], (bits if name == "transformer.wte.weight" else None)
+
+    # The tied head is the transposed fp16 wte [hidden, vocab].  Quantization is
+    # per output column, so column blocks are quantized as independent jobs.
+    head_block_cols = 8192
+
+    def head_block(wte_bits, c0):
+        t = np.ascontiguousarray(wte_bits[c0:c0 + head_block_cols].T)
+        return _quantized(codec, "lm_head.weight", t) if precision == "int8" else (t, None)
+
+    def head_records(blocks):
+        mat = np.concatenate([b[0] for b in blocks], axis=1)
+        if precision == "int8":
+            scales = np.concatenate([b[1] for b in blocks])
+            return [_record("lm_head.weight", "int8", mat), _record("lm_head.weight.scales", "float32", scales)]
+        return [_record("lm_head.weight", "float16", mat)]
+
     entries = []
     binary = dest / "weights.bin"
-    sha = hashlib.sha256()
-    with binary.open("wb") as f:
-        def write(name, dtype, shape, arr):
-            raw = np.ascontiguousarray(arr).tobytes()
-            pad = (-f.tell()) % ALIGNMENT
-            if pad:
-                f.write(bytes(pad))
-                sha.update(bytes(pad))
-            off = f.tell()
-            f.write(raw)
-            sha.update(raw)
-            entries.append({"name": name, "dtype": dtype, "shape": list(shape), "offset": off,
-                            "nbytes": len(raw), "sha256": hashlib.sha256(raw).hexdigest()})
+    digest = hashlib.sha256()
+    with binary.open("wb") as f, cf.ThreadPoolExecutor(_writer_threads()) as pool:
+        def emit(records):
+            for name, dtype, shape, raw, sha in records:
+                pad = (-f.tell()) % ALIGNMENT
+                if pad:
+                    f.write(bytes(pad))
+                    digest.update(bytes(pad))
+                off = f.tell()
+                view = memoryview(raw).cast("B")
+                f.write(view)
+                digest.update(view)
+                entries.append({"name": name, "dtype": dtype, "shape": shape, "offset": off,
+                                "nbytes": raw.nbytes, "sha256": sha})
+                if progress:
+                    progress(name)
 
-        wte = None
-        for name, shape in tensor_shapes(arch).items():
-            mean = 1.0 if (".ln_" in name or "ln_f" in name) and name.endswith(".weight") else 0.0
-            vals = _normal_f16(rng, shape, mean, std)
-            if name == "transformer.wte.weight":
-                wte = vals
-            is_linear = len(shape) == 2 and ".h." in name and name.endswith(".weight")
-            if precision == "int8" and is_linear:
-                q, sc = codec.quantize(vals.view(np.uint16))
-                q2, sc2 = quantize_numpy(vals.view(np.uint16))
-                if not (np.array_equal(q, q2) and np.array_equal(sc.view(np.uint32), sc2.view(np.uint32))):
-                    raise ValueError(f"native/numpy INT8 bytes differ for {name}")
-                write(name, "int8", shape, q)
-                write(name + ".scales", "float32", [shape[1]], sc)
-            else:
-                write(name, "float16", shape, vals.view(np.uint16))
-            if progress:
-                progress(name)
-        head = np.ascontiguousarray(wte.T)  # [hidden, vocab]
-        if precision == "int8":
-            q, sc = codec.quantize(head.view(np.uint16))
-            write("lm_head.weight", "int8", list(head.shape), q)
-            write("lm_head.weight.scales", "float32", [head.shape[1]], sc)
-        else:
-            write("lm_head.weight", "float16", list(head.shape), head.view(np.uint16))
+        window = 2 * _writer_threads()
+        pending = collections.deque()
+        head_jobs = []
+        for index in range(len(shapes)):
+            pending.append(pool.submit(build, index))
+            while len(pending) > window or (index == len(shapes) - 1 and pending):
+                records, wte_bits = pending.popleft().result()
+                if wte_bits is not None:
+                    head_jobs = [pool.submit(head_block, wte_bits, c0)
+                                 for c0 in range(0, wte_bits.shape[0], head_block_cols)]
+                emit(records)
+        emit(head_records([job.result() for job in head_jobs]))
     manifest = {"schema_version": 1, "model_id": SYNTHETIC_ID, "revision": f"seed-{seed}",
                 "source_sha256": canonical_hash(spec), "synthetic": spec, "precision": precision,
                 "architecture": arch, "binary": "weights.bin", "binary_bytes": binary.stat().st_size,
-                "binary_sha256": sha.hexdigest(), "alignment": ALIGNMENT,
+                "binary_sha256": digest.hexdigest(), "alignment": ALIGNMENT,
                 "quantization": {"axis": "output", "range": [-127, 127], "rounding": "ties_to_even",
                                  "zero_channel_scale": 1, "reference": "fp16",
                                  "dequantize": "fp32_then_fp16"},

@@ -5,7 +5,6 @@ Outputs, next to this file:
   libtinyinfer_llm.so         GPT-2 runtime C ABI (include/tinyinfer_llm.h)
   libtinyinfer_host_codec.so  host INT8 codec (include/tinyinfer_host_codec.h)
   ikernels<ext>               pybind11 module, next to libtinyinfer_backend.so
-  libtinyinfer_diag.so        machine-limit probes for bench.py (include/tinyinfer_amd_diag.h)
 Usage: python -m tinyinfer_amd.build  (or __graft_entry__.build()).
 """
 from __future__ import annotations
@@ -35,7 +34,6 @@ HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-march=x86-64-v3", "-ffp-contract=f
 
 BACKEND_HIP = ["gemm.hip", "attention.hip", "rowops.hip", "backend_v2.hip", "backend_legacy.hip"]
 LLM_HIP = ["llm_runtime.hip"]
-DIAG_HIP = ["diag.hip"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -70,7 +68,7 @@ def ikernels_name() -> str:
 
 def build(verbose: bool = True) -> None:
     OBJ.mkdir(exist_ok=True)
-    hip_sources = BACKEND_HIP + [s for s in LLM_HIP + DIAG_HIP if (CSRC / s).exists()]
+    hip_sources = BACKEND_HIP + [s for s in LLM_HIP if (CSRC / s).exists()]
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as pool:
         hip_jobs = {s: pool.submit(_hip_obj, s) for s in hip_sources}
         cpu_job = pool.submit(_host_obj, "cpu_ops.cpp", ["-fopenmp"])
@@ -85,8 +83,6 @@ def build(verbose: bool = True) -> None:
     if "llm_runtime.hip" in objs:
         _link(PKG / "libtinyinfer_llm.so", [objs["llm_runtime.hip"]],
               ["-L", str(PKG), "-ltinyinfer_backend", *rpath])
-    if "diag.hip" in objs:
-        _link(PKG / "libtinyinfer_diag.so", [objs["diag.hip"]], [])
     if (CSRC / "ikernels.cpp").exists():
         import pybind11
         inc = sysconfig.get_paths()["include"]
