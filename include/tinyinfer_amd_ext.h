@@ -19,6 +19,15 @@ int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const float* scales
                          const uint16_t* bias, uint16_t* y, const uint16_t* residual, int m,
                          int n, int k, int epilogue, uintptr_t stream, int device);
 
+/* ti_amd_legacy_gemm_f32_variant: the three FP32 GEMM variants behind
+ * ikernels.cuda_bench_matmul(variant, ...) (reference
+ * kernels/src/cuda/bench_api.cu:43-51 over kernels/src/cuda/matmul.cu:7-80):
+ * 0 naive, 1 LDS-tiled, 2 register-tiled (what ti_cuda_gemm and
+ * ti_v2_legacy_gemm_f32 run).  y[M,N] = a[M,K] @ b[K,N] in fp32, device
+ * pointers, v2 status codes (3 for an unknown variant). */
+int ti_amd_legacy_gemm_f32_variant(int variant, const float* a, const float* b, float* y, int m, int n, int k,
+                                   uintptr_t stream, int device);
+
 /* ti_amd_gemm_ex_i8_noalloc: no counterpart in the reference.  For callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): ti_v2_gemm_ex_i8 with the same

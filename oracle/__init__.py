@@ -196,15 +196,17 @@ class _Weights(C.Structure):
                 ("lnf_b", C.c_void_p), ("ln1_g", C.c_void_p), ("ln1_b", C.c_void_p),
                 ("ln2_g", C.c_void_p), ("ln2_b", C.c_void_p), ("w", C.c_void_p * 4),
                 ("s", C.c_void_p * 4), ("bias", C.c_void_p * 4), ("head_q", C.c_void_p),
-                ("head_s", C.c_void_p)]
+                ("head_s", C.c_void_p), ("w16", C.c_void_p * 4), ("head16", C.c_void_p)]
 
 
 _LINEARS = ("attn.c_attn", "attn.c_proj", "mlp.c_fc", "mlp.c_proj")
 
 
 class Gpt2:
-    """CPU GPT-2 (INT8 weight-only) restating reference llm/src/runtime.cu, fed from
-    a dict of numpy arrays keyed by the artifact's tensor names."""
+    """CPU GPT-2 restating reference llm/src/runtime.cu, fed from a dict of numpy
+    arrays keyed by the artifact's tensor names: INT8 weight-only linears
+    (dequantised fp16_rn(q * scale)) or, for fp16-precision artifacts, fp16
+    linears used as stored (reference runtime.cu:97-113)."""
 
     def __init__(self, tensors, arch, slots, capacity):
         L = arch["layers"]
@@ -230,12 +232,20 @@ class Gpt2:
         for field, ln, part in (("ln1_g", "ln_1", "weight"), ("ln1_b", "ln_1", "bias"),
                                 ("ln2_g", "ln_2", "weight"), ("ln2_b", "ln_2", "bias")):
             setattr(w, field, table([ptr(f"transformer.h.{l}.{ln}.{part}", np.uint16) for l in range(L)]))
+        # fp16-precision artifacts keep the linears and the head as fp16 bits.
+        fp16 = tensors["lm_head.weight"].dtype == np.uint16
         for i, lin in enumerate(_LINEARS):
-            w.w[i] = table([ptr(f"transformer.h.{l}.{lin}.weight", np.int8) for l in range(L)])
-            w.s[i] = table([ptr(f"transformer.h.{l}.{lin}.weight.scales", np.float32) for l in range(L)])
+            if fp16:
+                w.w16[i] = table([ptr(f"transformer.h.{l}.{lin}.weight", np.uint16) for l in range(L)])
+            else:
+                w.w[i] = table([ptr(f"transformer.h.{l}.{lin}.weight", np.int8) for l in range(L)])
+                w.s[i] = table([ptr(f"transformer.h.{l}.{lin}.weight.scales", np.float32) for l in range(L)])
             w.bias[i] = table([ptr(f"transformer.h.{l}.{lin}.bias", np.uint16) for l in range(L)])
-        w.head_q = ptr("lm_head.weight", np.int8)
-        w.head_s = ptr("lm_head.weight.scales", np.float32)
+        if fp16:
+            w.head16 = ptr("lm_head.weight", np.uint16)
+        else:
+            w.head_q = ptr("lm_head.weight", np.int8)
+            w.head_s = ptr("lm_head.weight.scales", np.float32)
         lib().or_gpt2_create.restype = C.c_void_p
         self._h = C.c_void_p(lib().or_gpt2_create(C.byref(w), C.c_int(slots), C.c_int(capacity)))
         self.vocab = arch["vocab"]

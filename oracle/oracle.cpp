@@ -26,7 +26,7 @@
 namespace {
 
 // ---- IEEE binary16 <-> binary32, round-to-nearest-even (bit exact) ----------
-float h2f(uint16_t h) {
+float h2f_compute(uint16_t h) {
   const uint32_t sign = uint32_t(h & 0x8000u) << 16;
   const uint32_t exp = (h >> 10) & 31u, man = h & 0x3ffu;
   uint32_t bits;
@@ -43,6 +43,17 @@ float h2f(uint16_t h) {
   std::memcpy(&out, &bits, 4);
   return out;
 }
+
+// binary16 -> binary32 through a table of all 65 536 patterns, each computed by
+// h2f_compute (the same values, without the branches per element).
+struct HalfTable {
+  float v[65536];
+  HalfTable() {
+    for (uint32_t i = 0; i < 65536; ++i) v[i] = h2f_compute(uint16_t(i));
+  }
+};
+const HalfTable kHalf;
+inline float h2f(uint16_t h) { return kHalf.v[h]; }
 
 uint16_t f2h(float f) {
   uint32_t x;
@@ -360,6 +371,11 @@ struct or_gpt2_weights {
   const uint16_t* const* bias[4];
   const int8_t* head_q;  // [hidden, vocab]
   const float* head_s;   // [vocab]
+  // fp16-precision artifacts (reference runtime.cu:97-113, ti_v2_gemm_ex_f16):
+  // when w16[0] is set the linears and the head are fp16 [K,N] bits, used as
+  // they are (no scales) in place of w/s/head_q/head_s.
+  const uint16_t* const* w16[4];
+  const uint16_t* head16;
 };
 }  // extern "C"
 
@@ -379,36 +395,65 @@ struct Gpt2 {
 
   // fp32-accumulated linear over pre-dequantized weights; fp16 rounding of the
   // result as the reference's TI_V2_FP16 output (runtime.cu:143,148,150,152).
+  // `active` lists the rows to compute (null: all); the others stay 0 (the
+  // padding rows of a ragged prefill, which no real row reads).
   static void linear(const std::vector<float>& x, int rows, int K, const std::vector<float>& W,
-                     int N, const uint16_t* bias, std::vector<float>& out, bool round16) {
+                     int N, const uint16_t* bias, std::vector<float>& out, bool round16,
+                     const std::vector<int>* active = nullptr) {
     out.assign(size_t(rows) * N, 0.f);
-#pragma omp parallel for schedule(static)
+    std::vector<int> all;
+    if (!active) {
+      all.resize(rows);
+      for (int r = 0; r < rows; ++r) all[r] = r;
+      active = &all;
+    }
+    const int count = int(active->size());
+    // Rows in blocks of 16 share each loaded weight row (a 128-column slice of W
+    // is read once per 16 rows instead of once per row); every output still
+    // sums k in increasing order, one fma per k.
+    constexpr int RB = 16;
+#pragma omp parallel for schedule(dynamic) collapse(2)
     for (int n0 = 0; n0 < N; n0 += 128) {
-      const int n1 = std::min(N, n0 + 128);
-      for (int r = 0; r < rows; ++r) {
-        float* o = &out[size_t(r) * N];
-        const float* xr = &x[size_t(r) * K];
+      for (int i0 = 0; i0 < count; i0 += RB) {
+        const int n1 = std::min(N, n0 + 128), i1 = std::min(count, i0 + RB);
         for (int k = 0; k < K; ++k) {
-          const float av = xr[k];
           const float* wr = &W[size_t(k) * N];
+          for (int i = i0; i < i1; ++i) {
+            const int r = (*active)[i];
+            const float av = x[size_t(r) * K + k];
+            float* o = &out[size_t(r) * N];
 #pragma omp simd
-          for (int n = n0; n < n1; ++n) o[n] += av * wr[n];
+            for (int n = n0; n < n1; ++n) o[n] += av * wr[n];
+          }
         }
-        for (int n = n0; n < n1; ++n) {
-          const float v = o[n] + (bias ? h2f(bias[n]) : 0.f);
-          o[n] = round16 ? rt16(v) : v;
+        for (int i = i0; i < i1; ++i) {
+          float* o = &out[size_t((*active)[i]) * N];
+          for (int n = n0; n < n1; ++n) {
+            const float v = o[n] + (bias ? h2f(bias[n]) : 0.f);
+            o[n] = round16 ? rt16(v) : v;
+          }
         }
       }
     }
   }
 
+  // x = fp16_rn(x + proj), elementwise.
+  static void residual(std::vector<float>& x, const std::vector<float>& proj) {
+    const int64_t n = int64_t(x.size());
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) x[i] = rt16(x[i] + proj[i]);
+  }
+
   void layernorm(const std::vector<float>& x, int rows, const std::vector<uint16_t>& g,
                  const std::vector<uint16_t>& b, std::vector<float>& y) const {
     std::vector<uint16_t> xin(x.size()), yo(x.size());
-    for (size_t i = 0; i < x.size(); ++i) xin[i] = f2h(x[i]);
+    const int64_t n = int64_t(x.size());
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) xin[i] = f2h(x[i]);
     or_layernorm_f16(xin.data(), g.data(), b.data(), yo.data(), rows, Hd, 1e-5f);
     y.resize(x.size());
-    for (size_t i = 0; i < x.size(); ++i) y[i] = h2f(yo[i]);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) y[i] = h2f(yo[i]);
   }
 
   // One forward over rows [b, qlen] of new tokens; returns the fp16 ln_f output of
@@ -417,8 +462,10 @@ struct Gpt2 {
                  const std::vector<int>& lens, int B, int Q, std::vector<float>& xout) {
     const int rows = B * Q, H3 = 3 * Hd, H4 = 4 * Hd;
     std::vector<float> x(size_t(rows) * Hd, 0.f), norm, qkv, attn(size_t(rows) * Hd, 0.f), proj, mlp;
-    std::vector<int> offs(B);
+    std::vector<int> offs(B), real;
     for (int b = 0; b < B; ++b) offs[b] = lengths[slot[b]];
+    for (int b = 0; b < B; ++b)
+      for (int t = 0; t < lens[b]; ++t) real.push_back(b * Q + t);
     for (int b = 0; b < B; ++b)  // embed: fp16(wte[id] + wpe[off + t]), padded rows 0 (:25-30)
       for (int t = 0; t < lens[b]; ++t) {
         const int id = tokens[size_t(b) * Q + t], pos = offs[b] + t;
@@ -427,7 +474,7 @@ struct Gpt2 {
       }
     for (int l = 0; l < L; ++l) {
       layernorm(x, rows, ln1_g[l], ln1_b[l], norm);
-      linear(norm, rows, Hd, w[0][l], H3, bias[0][l].data(), qkv, true);
+      linear(norm, rows, Hd, w[0][l], H3, bias[0][l].data(), qkv, true, &real);
       // split_scatter (:34-42): q | k | v thirds, head h at columns h*64..h*64+63
       for (int b = 0; b < B; ++b)
         for (int t = 0; t < lens[b]; ++t)
@@ -452,13 +499,17 @@ struct Gpt2 {
             for (int d = 0; d < 64; ++d) attn[(size_t(b) * Q + t) * Hd + h * 64 + d] = h2f(oh[d]);
           }
         }
-      linear(attn, rows, Hd, w[1][l], Hd, bias[1][l].data(), proj, true);
-      for (size_t i = 0; i < x.size(); ++i) x[i] = rt16(x[i] + proj[i]);  // res = x + proj (:149)
+      linear(attn, rows, Hd, w[1][l], Hd, bias[1][l].data(), proj, true, &real);
+      residual(x, proj);  // res = x + proj (:149)
       layernorm(x, rows, ln2_g[l], ln2_b[l], norm);
-      linear(norm, rows, Hd, w[2][l], H4, bias[2][l].data(), mlp, true);
-      for (auto& v : mlp) v = rt16(gelu_tanh(v));  // gelu_new over the fp16 c_fc output (:151)
-      linear(mlp, rows, H4, w[3][l], Hd, bias[3][l].data(), proj, true);
-      for (size_t i = 0; i < x.size(); ++i) x[i] = rt16(x[i] + proj[i]);  // x = res + proj (:153)
+      linear(norm, rows, Hd, w[2][l], H4, bias[2][l].data(), mlp, true, &real);
+      {  // gelu_new over the fp16 c_fc output (:151)
+        const int64_t n = int64_t(mlp.size());
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) mlp[i] = rt16(gelu_tanh(mlp[i]));
+      }
+      linear(mlp, rows, H4, w[3][l], Hd, bias[3][l].data(), proj, true, &real);
+      residual(x, proj);  // x = res + proj (:153)
     }
     layernorm(x, rows, lnf_g, lnf_b, xout);  // ln_f (:155)
   }
@@ -493,6 +544,12 @@ struct Gpt2 {
 };
 
 std::vector<uint16_t> copy16(const uint16_t* p, size_t n) { return std::vector<uint16_t>(p, p + n); }
+std::vector<float> widen16(const uint16_t* w, size_t n) {
+  std::vector<float> out(n);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < int64_t(n); ++i) out[i] = h2f(w[i]);
+  return out;
+}
 std::vector<float> dequant_f32(const int8_t* q, const float* s, int K, int N) {
   std::vector<float> out(size_t(K) * N);
 #pragma omp parallel for schedule(static)
@@ -517,11 +574,12 @@ void* or_gpt2_create(const or_gpt2_weights* w, int slots, int capacity) {
     m->ln1_g.push_back(copy16(w->ln1_g[l], H)); m->ln1_b.push_back(copy16(w->ln1_b[l], H));
     m->ln2_g.push_back(copy16(w->ln2_g[l], H)); m->ln2_b.push_back(copy16(w->ln2_b[l], H));
     for (int i = 0; i < 4; ++i) {
-      m->w[i].push_back(dequant_f32(w->w[i][l], w->s[i][l], KN[i][0], KN[i][1]));
+      m->w[i].push_back(w->w16[0] ? widen16(w->w16[i][l], size_t(KN[i][0]) * KN[i][1])
+                                  : dequant_f32(w->w[i][l], w->s[i][l], KN[i][0], KN[i][1]));
       m->bias[i].push_back(copy16(w->bias[i][l], KN[i][1]));
     }
   }
-  m->head = dequant_f32(w->head_q, w->head_s, H, w->vocab);
+  m->head = w->w16[0] ? widen16(w->head16, size_t(H) * w->vocab) : dequant_f32(w->head_q, w->head_s, H, w->vocab);
   const size_t cache = size_t(slots) * w->layers * w->heads * capacity * 64;
   m->kc.assign(cache, 0);
   m->vc.assign(cache, 0);

@@ -276,6 +276,12 @@ def tiny_tensors(tiny_artifact):
     return load_tensors(tiny_artifact)[1]
 
 
+@pytest.fixture(scope="module")
+def tiny_f16_tensors(tmp_path_factory):
+    from tinyinfer_amd.artifact import load_tensors, write_synthetic
+    return load_tensors(write_synthetic(tmp_path_factory.mktemp("tiny16"), TINY, seed=11, precision="fp16"))[1]
+
+
 def test_gpt2_self_consistency(tiny_tensors):
     m = oracle.Gpt2(tiny_tensors, TINY, slots=4, capacity=64)
     rng = np.random.default_rng(9)
@@ -309,18 +315,24 @@ def test_gpt2_mixed_greedy_lengths(tiny_tensors, golden):
         assert m.greedy([2], [prompt], n)[0] == gen
 
 
-def test_gpt2_matches_independent_transformers_model(tiny_tensors):
+@pytest.mark.parametrize("precision", ["int8", "fp16"])
+def test_gpt2_matches_independent_transformers_model(precision, request):
     """Cross-check against HF transformers' GPT-2 (float32, CPU) loaded with the same
-    dequantized weights: an independent implementation of the architecture."""
+    weights (dequantized INT8, or the fp16 linears of a float16 artifact as
+    stored): an independent implementation of the architecture."""
     torch = pytest.importorskip("torch")
     tr = pytest.importorskip("transformers")
     cfg = tr.GPT2Config(vocab_size=300, n_positions=64, n_embd=128, n_layer=2, n_head=2,
                         activation_function="gelu_new", layer_norm_epsilon=1e-5,
                         resid_pdrop=0, embd_pdrop=0, attn_pdrop=0, tie_word_embeddings=False)
     model = tr.GPT2LMHeadModel(cfg).eval()
-    t = tiny_tensors
+    t = tiny_tensors = request.getfixturevalue("tiny_tensors" if precision == "int8" else "tiny_f16_tensors")
     f = lambda bits: torch.tensor(h(bits), dtype=torch.float32)
-    deq = lambda name: torch.tensor(_deq(t[name], t[name + ".scales"]), dtype=torch.float32)
+    if precision == "int8":
+        deq = lambda name: torch.tensor(_deq(t[name], t[name + ".scales"]), dtype=torch.float32)
+    else:
+        assert t["lm_head.weight"].dtype == np.uint16 and "lm_head.weight.scales" not in t
+        deq = lambda name: f(t[name])
     sd = {"transformer.wte.weight": f(t["transformer.wte.weight"]),
           "transformer.wpe.weight": f(t["transformer.wpe.weight"]),
           "transformer.ln_f.weight": f(t["transformer.ln_f.weight"]),

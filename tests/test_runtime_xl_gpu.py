@@ -1,13 +1,18 @@
-"""GPT-2 XL shapes through libtinyinfer_llm.so (BASELINE configs[4] architecture:
-hidden 1600, 25 heads x 64, MLP 6400, vocab 50257) on a 2-layer synthetic INT8
-artifact, against the CPU oracle (restating reference llm/src/runtime.cu).
+"""GPT-2 XL through libtinyinfer_llm.so (BASELINE configs[4] architecture:
+hidden 1600, 25 heads x 64, MLP 6400, vocab 50257).
 
-The two layers exercise every XL-specific shape of the path: K = 1600 and 6400
-(25 and 100 chunks of the packed GEMV/GEMM), N = 4800 / 1600 / 6400 / 50257,
-25-head attention over ragged prompts up to 300 tokens, and the fused
-residual+LayerNorm finisher at 1600 columns.  Tolerances as the small model:
-logits within atol 5e-2, greedy tokens identical or diverging only at
-near-ties (oracle logit gap within 5e-2), first divergence reported.
+Against the CPU oracle (restating reference llm/src/runtime.cu), on a 2-layer
+synthetic INT8 artifact with XL's shapes: K = 1600 and 6400 (25 and 100 chunks
+of the packed GEMV/GEMM), N = 4800 / 1600 / 6400 / 50257, 25-head attention,
+and the fused residual+LayerNorm finisher at 1600 columns.  Tolerances as the
+small model: logits within atol 5e-2; greedy tokens identical, or diverging only
+at near-ties (the oracle's own logit gap between the two picks at most 1e-2),
+with the first divergence per request reported.  configs[4]'s own workload (64
+requests, prompts U[128,512], KV capacity 640) runs here against the oracle.
+
+On the full 48-layer artifact, where the oracle would take hours, the checks are
+properties: a request's logits are bit-identical alone and inside the
+64-request run, and the captured decode graph equals the eager path.
 """
 import numpy as np
 import pytest
@@ -99,7 +104,7 @@ def test_xl_greedy_matches_oracle(model, cpu_model):
         margins[b] = float(lg[0][cpu[b][i]] - lg[0][gpu[b][i]])
     print(f"xl greedy: {len(prompts) - len(diverged)}/{len(prompts)} identical over {NEW_TOKENS} tokens; "
           f"first divergence index {diverged}; oracle logit gap at divergence {margins}")
-    assert all(0 <= m <= 5e-2 for m in margins.values()), margins
+    assert all(0 <= m <= 1e-2 for m in margins.values()), margins
     model.reset_all()
 
 
@@ -133,3 +138,125 @@ def test_xl_decode_batch_sizes_match_oracle(artifact, batch):
                 assert np.abs(gpu - ref).max() <= 5e-2
     finally:
         cpu.close()
+
+
+# ---------------------------------------------------------------- configs[4] workload
+# configs[4]'s 128 greedy tokens per request.
+WORKLOAD_TOKENS = 128
+
+
+def configs4_prompts():
+    """64 requests, prompt lengths U[128,512] and ids U[0,50257) from seed 42
+    (the bench's configs[4] workload)."""
+    rng = np.random.default_rng(42)
+    lens = rng.integers(128, 513, 64)
+    return [rng.integers(0, 50257, int(n)).tolist() for n in lens]
+
+
+HALVES = (list(range(0, 32)), list(range(32, 64)))  # max_batch slices, as the server batches
+
+
+def test_xl_configs4_workload_vs_oracle(artifact):
+    from tinyinfer_amd import LLM_LIB
+    from tinyinfer_amd.artifact import load_tensors
+    from tinyinfer_amd.runtime import NativeModel
+    prompts = configs4_prompts()
+    say("configs[4] workload on the 2-layer XL-shaped artifact: GPU side")
+    with NativeModel(LLM_LIB, artifact, max_batch=32, cache_slots=64, capacity=640) as m:
+        gpu_prefill = np.concatenate([logits_of(m.forward(sl, [prompts[i] for i in sl])) for sl in HALVES])
+        manifest, tensors = load_tensors(artifact)
+        cpu = oracle.Gpt2(tensors, manifest["architecture"], slots=64, capacity=640)
+        try:
+            say("configs[4] workload: oracle prefill of 64 prompts")
+            cpu_prefill, first = [], []
+            for sl in HALVES:
+                lg, nxt = cpu.forward(sl, [prompts[i] for i in sl])
+                cpu_prefill.append(lg)
+                first += [int(t) for t in nxt]
+            cpu_prefill = np.concatenate(cpu_prefill)
+            err = np.abs(gpu_prefill - cpu_prefill).max()
+            print(f"configs[4] prefill of 64 requests: max |logit diff| {err:.3g}")
+            assert err <= 5e-2
+            # One decode step on both sides from the oracle's first token.
+            gpu_step = np.concatenate([logits_of(m.forward(sl, [[first[i]] for i in sl])) for sl in HALVES])
+            cpu_step, second = [], []
+            for sl in HALVES:
+                lg, nxt = cpu.forward(sl, [[first[i]] for i in sl])
+                cpu_step.append(lg)
+                second += [int(t) for t in nxt]
+            err = np.abs(gpu_step - np.concatenate(cpu_step)).max()
+            print(f"configs[4] first decode step of 64 requests: max |logit diff| {err:.3g}")
+            assert err <= 5e-2
+            say("configs[4] workload: GPU greedy")
+            m.reset_all()
+            gpu_tokens = []
+            for sl in HALVES:
+                gpu_tokens += m.greedy([prompts[i] for i in sl], WORKLOAD_TOKENS, slots=sl)["tokens"]
+            say("configs[4] workload: oracle greedy continues")
+            cpu_tokens = [[first[b], second[b]] for b in range(64)]
+            gaps = {}
+
+            def note(step, lg_by_request):
+                for b, lg in lg_by_request:
+                    if b in gaps:
+                        continue
+                    c, g = cpu_tokens[b][step], gpu_tokens[b][step]
+                    if c != g:
+                        gaps[b] = (step, float(lg[c] - lg[g]))
+
+            note(0, zip(range(64), cpu_prefill))
+            note(1, zip(range(64), np.concatenate(cpu_step)))
+            for step in range(2, WORKLOAD_TOKENS):
+                for sl in HALVES:
+                    lg, nxt = cpu.forward(sl, [[cpu_tokens[i][-1]] for i in sl])
+                    for i, t in zip(sl, nxt):
+                        cpu_tokens[i].append(int(t))
+                    note(step, zip(sl, lg))
+        finally:
+            cpu.close()
+    print(f"configs[4] greedy, 64 requests x {WORKLOAD_TOKENS} tokens: {64 - len(gaps)}/64 identical; "
+          f"first divergence (request: index, oracle gap) {gaps}")
+    assert all(0 <= gap <= 1e-2 for _, gap in gaps.values()), gaps
+    assert len(gaps) <= 16, gaps
+
+
+# ---------------------------------------------------------------- 48 layers: properties
+@pytest.fixture(scope="module")
+def xl48_artifact(tmp_path_factory):
+    from tinyinfer_amd.artifact import GPT2_XL, write_synthetic
+    say("writing the 48-layer GPT-2 XL synthetic artifact (1.7 GB)")
+    return write_synthetic(tmp_path_factory.mktemp("gpt2xl48"), GPT2_XL, seed=42)
+
+
+def test_xl48_batch_invariance_and_graph_equals_eager(xl48_artifact):
+    """Full GPT-2 XL, configs[4]'s 64 requests in two max_batch slices: requests
+    alone give the same logits bits as inside the batched run, at prefill and at
+    a decode step; the captured decode graph gives the eager path's bits."""
+    from tinyinfer_amd import LLM_LIB
+    from tinyinfer_amd.runtime import NativeModel
+    prompts = configs4_prompts()
+    picks = (3, 40, 63)
+    with NativeModel(LLM_LIB, xl48_artifact, max_batch=32, cache_slots=64, capacity=640) as m:
+        say("xl48: batched prefill and graph decode step of 64 requests")
+        pre, dec = {}, {}
+        for sl in HALVES:
+            lg = logits_of(m.forward(sl, [prompts[i] for i in sl]))
+            for j, i in enumerate(sl):
+                pre[i] = lg[j]
+            step = logits_of(m.forward(sl, [[7] for _ in sl], return_next=True))  # graph path
+            for j, i in enumerate(sl):
+                dec[i] = step[j]
+        say("xl48: the same requests alone")
+        for i in picks:
+            m.reset(i)
+            alone = logits_of(m.forward([i], [prompts[i]]))[0]
+            assert np.array_equal(alone, pre[i]), f"request {i}: prefill alone differs from the batched run"
+            alone = logits_of(m.forward([i], [[7]], return_next=True))[0]
+            assert np.array_equal(alone, dec[i]), f"request {i}: decode step alone differs from the batched run"
+        say("xl48: graph vs eager decode")
+        m.reset_all()
+        m.forward([0, 1], [prompts[5], prompts[5]], return_logits=False, return_next=False)
+        for tok in (11, 50000, 7):
+            graph = logits_of(m.forward([0], [[tok]], return_next=True))
+            eager = logits_of(m.forward([1], [[tok]], return_next=False))
+            assert np.array_equal(graph, eager)

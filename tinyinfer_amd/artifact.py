@@ -129,14 +129,14 @@ def write_synthetic(dest, arch=None, seed=42, precision="int8", std=0.02, progre
     """Write a random-init GPT-2 artifact: every weight matrix, embedding and bias
     ~ N(0, std), LayerNorm gamma ~ N(1, std), beta ~ N(0, std), stored fp16;
     linears and the tied head INT8-quantized (``precision="int8"``) or kept fp16
-    (``"float16"``).  Tensor i of the manifest order draws from its own numpy
+    (``"fp16"``, the format's two precisions, reference export_weights.py:142).  Tensor i of the manifest order draws from its own numpy
     PCG64 stream, ``SeedSequence(seed).spawn(count)[i]``, so worker threads build
     tensors concurrently and the bytes do not depend on their scheduling.
     Returns the manifest path.  ``progress``, if given, is called with each
     tensor name as it is written."""
     arch = dict(GPT2_SMALL if arch is None else arch)
-    if precision not in ("int8", "float16"):
-        raise ValueError("precision must be 'int8' or 'float16'")
+    if precision not in ("int8", "fp16"):
+        raise ValueError("precision must be 'int8' or 'fp16'")
     dest = Path(dest)
     dest.mkdir(parents=True, exist_ok=True)
     codec = HostCodec() if precision == "int8" else None

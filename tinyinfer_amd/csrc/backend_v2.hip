@@ -225,6 +225,17 @@ extern "C" int ti_v2_legacy_gemm_f32(const float* a, const float* b, float* y, i
   return hip_status(tia::legacy_gemm_f32(a, b, y, m, n, k, reinterpret_cast<hipStream_t>(stream)));
 }
 
+extern "C" int ti_amd_legacy_gemm_f32_variant(int variant, const float* a, const float* b, float* y, int m, int n,
+                                              int k, uintptr_t stream, int device) {
+  int status = begin(device);
+  if (status) return status;
+  if (variant < 0 || variant > 2) return fail(TI_V2_UNSUPPORTED_CONFIG, "FP32 GEMM variant must be 0, 1 or 2");
+  if (!aligned(a, 4) || !aligned(b, 4) || !aligned(y, 4) || !shape_fits({m, k}, 4) || !shape_fits({k, n}, 4) ||
+      !shape_fits({m, n}, 4) || (m - 1) / 16 + 1 > 65535)
+    return fail(TI_V2_INVALID_ARGUMENT, "invalid FP32 GEMM arguments");
+  return hip_status(tia::legacy_gemm_f32_variant(variant, a, b, y, m, n, k, reinterpret_cast<hipStream_t>(stream)));
+}
+
 extern "C" int ti_v2_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* y,
                                    const int32_t* ql, const int32_t* kl, const int32_t* offsets, int b,
                                    int h, int nq, int nk, int d, int causal, int config,

@@ -1209,8 +1209,43 @@ __global__ void bias_epilogue_kernel(const float* ws, const uint16_t* bias, void
   }
 }
 
-// 64x64 output tile per 256-thread block, 4x4 outputs per thread, K in 16-wide
-// LDS slabs.
+// The three FP32 GEMM variants of the legacy ABI's benchmark hook (the
+// reference's naive / shared-memory tiled / register-tiled kernels,
+// kernels/src/cuda/matmul.cu:7-80, chosen by bench_api.cu:43-51's variant).
+// Every variant sums k in increasing order for each output.
+// Variant 0: one thread per output, operands straight from global memory.
+__global__ __launch_bounds__(256) void legacy_f32_naive_kernel(const float* a, const float* b, float* c, int m,
+                                                               int n, int k) {
+  const int64_t col = int64_t(blockIdx.x) * 16 + (threadIdx.x & 15);
+  const int64_t row = int64_t(blockIdx.y) * 16 + (threadIdx.x >> 4);
+  if (row >= m || col >= n) return;
+  float acc = 0.f;
+  for (int64_t kk = 0; kk < k; ++kk) acc += a[row * k + kk] * b[kk * n + col];
+  c[row * n + col] = acc;
+}
+
+// Variant 1: 16x16 output tile per 256-thread block, one output per thread,
+// A and B staged through LDS in 16-wide K slabs.
+__global__ __launch_bounds__(256) void legacy_f32_tiled_kernel(const float* a, const float* b, float* c, int m,
+                                                               int n, int k) {
+  __shared__ float As[16][17];
+  __shared__ float Bs[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t row = int64_t(blockIdx.y) * 16 + ty, col = int64_t(blockIdx.x) * 16 + tx;
+  float acc = 0.f;
+  for (int64_t k0 = 0; k0 < k; k0 += 16) {
+    As[ty][tx] = (row < m && k0 + tx < k) ? a[row * k + k0 + tx] : 0.f;
+    Bs[ty][tx] = (k0 + ty < k && col < n) ? b[(k0 + ty) * n + col] : 0.f;
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) acc += As[ty][kk] * Bs[kk][tx];
+    __syncthreads();
+  }
+  if (row < m && col < n) c[row * n + col] = acc;
+}
+
+// Variant 2 (ti_cuda_gemm, ti_v2_legacy_gemm_f32): 64x64 output tile per
+// 256-thread block, 4x4 outputs per thread, K in 16-wide LDS slabs.
 __global__ __launch_bounds__(256) void legacy_f32_kernel(const float* a, const float* b, float* c,
                                                          int m, int n, int k) {
   __shared__ float As[16][64 + 4];
@@ -1918,8 +1953,24 @@ hipError_t bias_epilogue(const float* ws, const uint16_t* bias, void* y, int64_t
 
 hipError_t legacy_gemm_f32(const float* a, const float* b, float* c, int m, int n, int k,
                            hipStream_t stream) {
-  hipLaunchKernelGGL(legacy_f32_kernel, dim3(unsigned((n + 63) / 64), unsigned((m + 63) / 64)),
-                     dim3(256), 0, stream, a, b, c, m, n, k);
+  return legacy_gemm_f32_variant(2, a, b, c, m, n, k, stream);
+}
+
+hipError_t legacy_gemm_f32_variant(int variant, const float* a, const float* b, float* c, int m, int n, int k,
+                                   hipStream_t stream) {
+  if (m <= 0 || n <= 0 || k <= 0) return hipErrorInvalidValue;
+  if (variant == 2) {
+    if ((m + 63) / 64 > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(legacy_f32_kernel, dim3(unsigned((n + 63) / 64), unsigned((m + 63) / 64)), dim3(256), 0,
+                       stream, a, b, c, m, n, k);
+  } else if (variant == 0 || variant == 1) {
+    if ((m + 15) / 16 > 65535) return hipErrorInvalidValue;
+    const dim3 grid(unsigned((n + 15) / 16), unsigned((m + 15) / 16));
+    if (variant == 0) hipLaunchKernelGGL(legacy_f32_naive_kernel, grid, dim3(256), 0, stream, a, b, c, m, n, k);
+    else hipLaunchKernelGGL(legacy_f32_tiled_kernel, grid, dim3(256), 0, stream, a, b, c, m, n, k);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

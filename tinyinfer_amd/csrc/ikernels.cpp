@@ -147,7 +147,7 @@ double time_ms(F&& launch, int iters) {
 double bench_matmul(int variant, int m, int n, int k, int iters) {
   if (variant < 0 || variant > 2) throw std::invalid_argument("variant must be 0, 1 or 2");
   DeviceBuffer A(size_t(m) * k, 1), B(size_t(k) * n, 2), C(size_t(m) * n, 3);
-  return time_ms([&] { return tia::legacy_gemm_f32(A.p, B.p, C.p, m, n, k, nullptr); }, iters);
+  return time_ms([&] { return tia::legacy_gemm_f32_variant(variant, A.p, B.p, C.p, m, n, k, nullptr); }, iters);
 }
 double bench_softmax(int rows, int cols, int iters) {
   DeviceBuffer x(size_t(rows) * cols, 3), y(size_t(rows) * cols, 4);
@@ -170,7 +170,8 @@ PYBIND11_MODULE(ikernels, m) {
   m.attr("has_cuda") = true;
   m.def("cuda_device_available", &device_available);
   m.def("cuda_bench_matmul", &bench_matmul, py::arg("variant"), py::arg("M"), py::arg("N"), py::arg("K"),
-        py::arg("iters") = 20, "HIP-event ms per launch of the FP32 GEMM");
+        py::arg("iters") = 20,
+        "HIP-event ms per launch of FP32 GEMM variant 0 (naive), 1 (LDS-tiled) or 2 (register-tiled)");
   m.def("cuda_bench_softmax", &bench_softmax, py::arg("rows"), py::arg("cols"), py::arg("iters") = 50);
   m.def("cuda_bench_layernorm", &bench_layernorm, py::arg("rows"), py::arg("cols"), py::arg("iters") = 50);
 }

@@ -145,6 +145,9 @@ hipError_t bias_epilogue(const float* ws, const uint16_t* bias, void* y, int64_t
                          int dtype, hipStream_t stream);
 hipError_t legacy_gemm_f32(const float* a, const float* b, float* c, int m, int n, int k,
                            hipStream_t stream);
+// Variant 0 naive, 1 LDS-tiled, 2 register-tiled (legacy_gemm_f32).
+hipError_t legacy_gemm_f32_variant(int variant, const float* a, const float* b, float* c, int m, int n, int k,
+                                   hipStream_t stream);
 
 // Attention with generic strides (elements).  K/V of (b, h) start at
 // k + slot(b) * kv_sb + h * kv_sh with consecutive keys D elements apart, where
