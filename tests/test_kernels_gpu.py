@@ -208,7 +208,8 @@ def test_pack_w8_layout_bit_exact(ops, k, n):
 
 
 @pytest.mark.parametrize("m", [1, 8, 17, 32])
-@pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (768, 2304), (128, 100), (64, 50257)])
+@pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (768, 2304), (128, 100), (64, 50257), (768, 50257),
+                                 (1024, 16400)])
 def test_packed_gemv_against_oracle(ops, m, k, n):
     """Decode GEMV over panel-packed weights: bias, bias+GELU and in-place residual
     epilogues against the oracle's fp32-accumulate linear."""
@@ -549,6 +550,29 @@ def test_split_decode_attention_ragged(ops, d, nk, causal):
     got = h(hbits(out))
     close(got, h(oracle.attention_f16(q, k, v, ql, kl, off, bool(causal))))
     assert not got[2].any() and not got[4].any()
+
+
+def test_split_decode_attention_large_batch(ops):
+    """The key-split kernel plus its merge pass over a large batch (260
+    requests, 520 (b, h) rows): ragged lengths, ties, empty rows and a request
+    with no query, against the oracle."""
+    t = torch()
+    rng = np.random.default_rng(260)
+    B, H, D, nk = 260, 2, 64, 600
+    kl = rng.integers(0, nk + 1, B)
+    kl[:8] = [nk, nk, 1, 0, 517, 517, 512, 128]
+    ql = np.ones(B, np.int64)
+    ql[9] = 0
+    off = np.maximum(kl - 1, 0)
+    q = f16(rng.standard_normal((B, H, 1, D)) * 0.5)
+    k = f16(rng.standard_normal((B, H, nk, D)) * 0.5)
+    v = f16(rng.standard_normal((B, H, nk, D)))
+    say("split decode attention, batch", B)
+    out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql.tolist(),
+                        kv_lengths=kl.tolist(), query_offsets=off.tolist(), causal=True)
+    got = h(hbits(out))
+    close(got, h(oracle.attention_f16(q, k, v, ql, kl, off, True)))
+    assert not got[3].any() and not got[9].any()
 
 
 @pytest.mark.parametrize("nq,nk", [(64, 64), (300, 300), (1, 2000), (3, 700)])

@@ -380,13 +380,14 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
 // rows with no visible key, and padded queries, are exactly zero.
 template <int D, int KS>
 __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma_kernel(AttnParams p) {
-  constexpr int BQ = 64, BT = 64, KP = D + 8, VP = BT + 8;
+  constexpr int BQ = 64, BT = 64, KP = D + 8;
   constexpr int SEGS = D / 8;                 // 16-byte pieces per key row
   constexpr int PIECES = BT * SEGS / 256;     // per thread per tile (2 or 4)
-  // Dynamic LDS: [2 buffers][KS tiles] of K rows, then of transposed V.
+  // Dynamic LDS: [2 buffers][KS tiles] of K rows, then of V rows (row-major;
+  // the PV operand is read transposed by ds_read_b64_tr_b16).
   extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
   auto ks = reinterpret_cast<f16(*)[KS][BT][KP]>(lds_raw);
-  auto vt = reinterpret_cast<f16(*)[KS][D][VP]>(lds_raw + 2 * KS * BT * KP * sizeof(f16));
+  auto vs = reinterpret_cast<f16(*)[KS][BT][KP]>(lds_raw + 2 * KS * BT * KP * sizeof(f16));
   const AttnArgs& a = p.a;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // KS = 2: waves 4..7 are a second key group taking the odd tiles of each
@@ -462,8 +463,7 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
     for (int r = 0; r < PIECES; ++r) {
       const int piece = gt + 256 * r, key = piece % BT, seg = piece / BT;
       *reinterpret_cast<half8_t*>(&ks[buf][grp][key][8 * seg]) = r_.k[r];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vt[buf][grp][8 * seg + e][key] = r_.v[r][e];
+      *reinterpret_cast<half8_t*>(&vs[buf][grp][key][8 * seg]) = r_.v[r];
     }
   };
 
@@ -545,12 +545,20 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
       // l = sum of the fp16 probabilities, in fp32, with no cross-lane step.
       // V^T fragments of a key pair: the first pair's LDS reads complete while
       // the exponentials run, the second's during the first pair's MFMAs.
+      // ds_read_b64_tr_b16 on 16-lane groups: value k of lane r comes from the
+      // address of lane 4k + r/4 of its group, element r % 4.  Lane (j, g)
+      // therefore points at row 4g + j/4 (+ 32c, + 16 for the second run),
+      // dims 16d + 4 (j % 4) .. + 3, so that lane (j, g) receives V[32c + 4g +
+      // k][16d + j], k < 4: the A operand V^T of the key runs described above.
       auto vfrag = [&](half8_t (&vf)[D / 16], int c) {
 #pragma unroll
         for (int d = 0; d < D / 16; ++d) {
-          const f16* vrow = &vt[buf][grp][16 * d + j][32 * c + 4 * g];
-          const half4_t lo = *reinterpret_cast<const half4_t*>(vrow);
-          const half4_t hi = *reinterpret_cast<const half4_t*>(vrow + 16);
+          typedef __fp16 tr_vec __attribute__((vector_size(8)));
+          typedef __attribute__((address_space(3))) tr_vec lds_tr_vec;
+          const f16* vrow = &vs[buf][grp][32 * c + 4 * g + (j >> 2)][16 * d + 4 * (j & 3)];
+          const half4_t lo = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_vec*)(vrow)));
+          const half4_t hi =
+              __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_vec*)(vrow + 16 * KP)));
           vf[d] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
       };
@@ -681,7 +689,7 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
       // batch_invariant (the runtime's prefill) always takes the key-split
       // kernel, so a query's sums never depend on the grid.
       const int64_t wgs = int64_t(grid.x) * grid.y * grid.z;
-      constexpr size_t lds1 = 2 * 64 * (D + 8) * 2 + 2 * D * (64 + 8) * 2;
+      constexpr size_t lds1 = 2 * 2 * 64 * (D + 8) * 2;  // K and V rows, two buffers
       if (wgs <= 512 || a.batch_invariant) {
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, 2>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, int(2 * lds1));

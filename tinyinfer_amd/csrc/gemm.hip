@@ -713,7 +713,8 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
 // instead re-reads all of A for every one or two column blocks (1571
 // workgroups x 48 KiB for the 38.6 MB GPT-2 head at M = 32).
 struct WideParams {
-  const uint16_t* a;    // P32 fragment-packed [32][K]
+  const uint16_t* a;    // P32 fragment-packed [32][K], or row-major [M][lda] (AP32 false)
+  int64_t lda;
   const u32x4_t* w;     // panel-packed records
   const float* scales;  // fp32 [N]
   int m, n, nb, per;    // rows, columns, column blocks, blocks per workgroup
@@ -731,15 +732,17 @@ __device__ __forceinline__ void amax_merge(float& bv, int& bi, float v, int i) {
   }
 }
 
-template <int MT, int KC, int W>
+template <int MT, int KC, int W, bool AP32>
 __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
-  __shared__ half8_t a_lds[KC * 256];  // P32 fragments ((c * 2 + t) * 2 + s) * 64 + lane
+  // A as MFMA fragments ((c * MT + t) * 2 + s) * 64 + lane: rows 16t + (lane & 15),
+  // columns 64c + 32s + 8 (lane >> 4) .. + 7 (for MT = 2, the P32 layout).
+  __shared__ half8_t a_lds[KC * MT * 2 * 64];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const half8_t* asrc = reinterpret_cast<const half8_t*>(p.a);
-  static_assert((KC * 256) % (W * 64) == 0, "A copy must divide evenly");
+  static_assert((KC * MT * 2 * 64) % (W * 64) == 0, "A copy must divide evenly");
   static_assert(W >= 8, "the blocks of a wave are not overlapped: at least 8 waves per workgroup");
-  constexpr int kACopy = KC * 256 / (W * 64);
+  static_assert(AP32 ? MT == 2 : true, "P32 A holds 32 rows");
+  constexpr int kACopy = KC * MT * 2 * 64 / (W * 64);
   const int cb_first = blockIdx.x * p.per + wave, cb_end = min(p.nb, (blockIdx.x + 1) * p.per);
   const int count = cb_first < cb_end ? (cb_end - cb_first + W - 1) / W : 0;  // this wave's blocks
   const bool has_bias = p.epi.kind != EPI_RAW_F32 && p.epi.bias;
@@ -783,18 +786,16 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
         float4_t& ac = acc[c % 4][t];
-        ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * 2 + t) * 2) * 64 + lane], b0, ac, 0, 0, 0);
-        ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * 2 + t) * 2 + 1) * 64 + lane], b1, ac, 0, 0, 0);
+        ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * MT + t) * 2) * 64 + lane], b0, ac, 0, 0, 0);
+        ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * MT + t) * 2 + 1) * 64 + lane], b1, ac, 0, 0, 0);
       }
       // One chunk's LDS reads and dequantisation at a time (hoisting all of
       // them would hold every A fragment of the block in registers).
       __builtin_amdgcn_sched_barrier(0);
     }
-    // EPI_F32 (fp32 logits + bias), the only epilogue this kernel is launched with.
     const int col = (cb_first + W * i) * 16 + j;
     if (col >= p.n) return;
     const float bias = has_bias ? h2f(b.bias) : 0.f;
-    float* y = static_cast<float*>(p.epi.y);
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -803,9 +804,14 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
         float sum = 0.f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) sum += acc[q][t][v];
-        const float val = sum + bias;
-        if (row < p.m) y[int64_t(row) * p.epi.ldy + col] = val;
-        amax_merge(bv[t * 4 + v], bi[t * 4 + v], val, col);
+        if (p.epi.kind == EPI_F32) {
+          // fp32 logits + bias, with this lane's running argmax.
+          const float val = sum + bias;
+          if (row < p.m) static_cast<float*>(p.epi.y)[int64_t(row) * p.epi.ldy + col] = val;
+          amax_merge(bv[t * 4 + v], bi[t * 4 + v], val, col);
+        } else if (row < p.m) {
+          apply_epilogue(p.epi, row, col, sum, bias);
+        }
       }
   };
   Block x;
@@ -814,7 +820,16 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
     // to overlap them; issuing the first blocks' weight loads ahead of the A
     // copy measured slower).
 #pragma unroll
-    for (int i = 0; i < kACopy; ++i) a_lds[i * W * 64 + threadIdx.x] = asrc[i * W * 64 + threadIdx.x];
+    for (int i = 0; i < kACopy; ++i) {
+      const int f = i * W * 64 + threadIdx.x;  // fragment f / 64, lane f % 64
+      if constexpr (AP32) {
+        a_lds[f] = reinterpret_cast<const half8_t*>(p.a)[f];
+      } else {
+        const int fl = f & 63, frag = f >> 6, s2 = frag & 1, t = (frag >> 1) % MT, c = (frag >> 1) / MT;
+        const int row = 16 * t + (fl & 15), col = 64 * c + 32 * s2 + 8 * (fl >> 4);
+        a_lds[f] = row < p.m ? *reinterpret_cast<const half8_t*>(p.a + int64_t(row) * p.lda + col) : half8_t{};
+      }
+    }
     __syncthreads();
     for (int i = 0; i < count; ++i) {
       load(x, i);
@@ -1452,24 +1467,40 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   if (ln) {
     p.ln_gamma = g.ln_gamma; p.ln_beta = g.ln_beta; p.ln_eps = g.ln_eps;
   }
-  if constexpr (MT == 2) {
-    // The LM head: whole column blocks per wave over an LDS copy of A.
-    if (g.a_p32 && !ln && !deferred && p.epi.kind == EPI_F32 && p.nb >= 1024 && (p.kc == 12 || p.kc == 16)) {
-      // 16 column blocks per workgroup of 8 waves (two per wave): timed
-      // against 8 / 16 / 32 blocks and 4 / 8 / 16 waves on the GPT-2 head.
-      WideParams wp{};
-      wp.a = g.a; wp.w = p.w; wp.scales = p.scales; wp.m = p.m; wp.n = p.n; wp.nb = p.nb; wp.epi = p.epi;
-      wp.per = 16;
-      const int grid = (p.nb + wp.per - 1) / wp.per;
-      if (g.amax_v && g.amax_i && g.amax_groups && size_t(grid) * 32 <= g.amax_capacity) {
-        wp.amax_v = g.amax_v;
-        wp.amax_i = g.amax_i;
-        *g.amax_groups = grid;
-      }
-      if (p.kc == 12) hipLaunchKernelGGL((gemv_wide_kernel<2, 12, 8>), dim3(unsigned(grid)), dim3(512), 0, stream, wp);
-      else hipLaunchKernelGGL((gemv_wide_kernel<2, 16, 8>), dim3(unsigned(grid)), dim3(512), 0, stream, wp);
-      return hipGetLastError();
+  // Wide N (the LM head shape, >= 1024 column blocks) at 17..32 rows: whole
+  // column blocks per wave over an LDS copy of A, no cross-wave reduction and
+  // A read once per workgroup instead of once per column block pair.  The
+  // runtime's decode head (P32 A, fp32 logits) and the ABI's row-major calls
+  // take it (768 -> 50257 at M = 32 through the ABI: 18.9 against 20.8 us for
+  // the packed GEMV; at M = 1 the packed GEMV is faster, 10.0 against 11.6 us);
+  // 16 column blocks per workgroup of 8 waves (two per wave): timed against
+  // 8 / 16 / 32 blocks and 4 / 8 / 16 waves on the GPT-2 head.
+  const bool wide_epi = p.epi.kind == EPI_F32 || ((p.epi.kind == EPI_F16 || p.epi.kind == EPI_GELU ||
+                                                    p.epi.kind == EPI_RESIDUAL) && !p.epi.p32);
+  if (MT == 2 && !ln && !deferred && p.nb >= 1024 && (p.kc == 12 || p.kc == 16) && wide_epi &&
+      (!g.a_p32 || p.epi.kind == EPI_F32)) {
+    WideParams wp{};
+    wp.a = g.a; wp.lda = g.lda; wp.w = p.w; wp.scales = p.scales; wp.m = p.m; wp.n = p.n; wp.nb = p.nb;
+    wp.epi = p.epi;
+    wp.per = 16;
+    const int grid = (p.nb + wp.per - 1) / wp.per;
+    if (p.epi.kind == EPI_F32 && g.amax_v && g.amax_i && g.amax_groups && size_t(grid) * 32 <= g.amax_capacity) {
+      wp.amax_v = g.amax_v;
+      wp.amax_i = g.amax_i;
+      *g.amax_groups = grid;
     }
+    const dim3 gd{unsigned(grid)}, bd{512u};
+    if constexpr (MT == 2) {
+      if (g.a_p32) {
+        if (p.kc == 12) hipLaunchKernelGGL((gemv_wide_kernel<2, 12, 8, true>), gd, bd, 0, stream, wp);
+        else hipLaunchKernelGGL((gemv_wide_kernel<2, 16, 8, true>), gd, bd, 0, stream, wp);
+      } else if (p.kc == 12) {
+        hipLaunchKernelGGL((gemv_wide_kernel<2, 12, 8, false>), gd, bd, 0, stream, wp);
+      } else {
+        hipLaunchKernelGGL((gemv_wide_kernel<2, 16, 8, false>), gd, bd, 0, stream, wp);
+      }
+    }
+    return hipGetLastError();
   }
   int splits = 1;
   if (deferred && !ln && s && s->partials) {
