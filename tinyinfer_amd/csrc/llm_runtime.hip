@@ -21,7 +21,17 @@
 //  * a decode step (every request appends one token) is captured once per
 //    batch size into a hipGraph whose kernels read all lengths, offsets and slots
 //    from device memory, so later steps are one graph launch between a pinned
-//    H2D copy of the step metadata and a D2H copy of the next tokens.
+//    H2D copy of the step metadata and a D2H copy of the next tokens;
+//  * the captured step ends with a feed kernel (its greedy ids become the next
+//    step's input ids, positions advance by one), so ti_llm_greedy_batch queues
+//    each run of decode steps over an unchanged set of requests back to back,
+//    with the ids copied to pinned memory as they come, and waits once per run;
+//  * such a run of more than 16 requests splits into two lanes of at most 16,
+//    each with its own stream, activations, scratch and captured graph over the
+//    shared weights and KV cache, queued side by side: one lane's chain of 64
+//    dependent launches leaves most CUs idle, and two free-running chains fill
+//    them.  A request's logits are the same bits in either lane, since the
+//    decode kernels sum every row in one K order at every batch size.
 #include <algorithm>
 #include <chrono>
 #include <climits>
@@ -51,6 +61,8 @@ constexpr int kHeadDim = 64;
 // 64 requests: 192 -> 12.06 K tok/s, 384 -> 11.66 K (unsplit with a separate
 // LayerNorm row kernel: 11.4 K).
 constexpr int kResidualSplitWorkgroups = 192;
+// Decode steps of more than this many requests run as two concurrent lanes.
+constexpr int kLaneRows = 16;
 
 struct GpuError : std::runtime_error {
   using std::runtime_error::runtime_error;
@@ -231,6 +243,26 @@ __global__ __launch_bounds__(256) void sum_kernel(const double* v, double* out, 
   if (threadIdx.x == 0) *out = s[0] + s[1] + s[2] + s[3];
 }
 
+// End of a captured decode step: the step's greedy ids become the next step's
+// input ids and every request's position advances by one, so a run of decode
+// steps needs no host round trip between steps.
+// Step t of a run also lands in run[t * b + i] (t counted in *run_step, which
+// the run's caller clears; steps past run_steps are not recorded).  One
+// workgroup of 64 threads, b <= 32.
+__global__ void feed_kernel(const int32_t* next, int32_t* ids, int32_t* offsets, int32_t* run, uint32_t* run_step,
+                            uint32_t run_steps, int b) {
+  const int i = threadIdx.x;
+  const uint32_t t = *run_step;
+  __syncthreads();  // every thread has read the step before thread 0 advances it
+  if (i < b) {
+    const int32_t v = next[i];
+    ids[i] = v;
+    offsets[i] += 1;
+    if (t < run_steps) run[size_t(t) * b + i] = v;
+  }
+  if (i == 0) *run_step = t + 1;
+}
+
 __global__ void zero_f64_kernel(double* p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0.0;
@@ -284,7 +316,71 @@ struct ti_llm_model {
   tia::Scratch scratch;
   std::vector<int32_t> lengths;
   ti_llm_trace trace{};
-  std::map<int, hipGraphExec_t> decode_graphs;
+  bool norm_p32 = false;  // the last layers() pass left x and norm P32-packed
+
+  // Per-lane state of a decode step: the members above (stream, activations,
+  // step metadata, head outputs, scratch) are the active lane's copy;
+  // select_lane() swaps them.  Lane 0 also serves prefill, eager passes and
+  // scoring, with buffers sized for max_batch x capacity rows; lane 1 only
+  // decodes, with buffers for 32 rows.
+  struct Lane {
+    hipStream_t stream = nullptr;
+    uint16_t *x = nullptr, *norm = nullptr, *qkv = nullptr, *attn = nullptr, *mlp = nullptr, *last = nullptr;
+    float* logits = nullptr;
+    int32_t *d_meta = nullptr, *d_next = nullptr;
+    float* d_amax_v = nullptr;
+    int32_t* d_amax_i = nullptr;
+    int32_t *h_meta = nullptr, *h_next = nullptr;
+    tia::Scratch scratch;
+    bool norm_p32 = false;
+    std::map<int, hipGraphExec_t> decode_graphs;
+    // Greedy ids of a run of decode steps: device [capacity][rows] with its
+    // step counter, and the pinned host copy.
+    int32_t* d_run = nullptr;
+    uint32_t* d_run_step = nullptr;
+    int32_t* h_run = nullptr;
+  };
+  Lane lanes[2];
+  int lane = 0;
+  bool two_lanes = false;
+  void* pinned_lane1 = nullptr;
+  void* pinned_runs[2] = {nullptr, nullptr};
+
+  void save_lane() {
+    Lane& l = lanes[lane];
+    l.stream = stream;
+    l.x = x; l.norm = norm; l.qkv = qkv; l.attn = attn; l.mlp = mlp; l.last = last;
+    l.logits = logits;
+    l.d_meta = d_meta; l.d_next = d_next;
+    l.d_amax_v = d_amax_v; l.d_amax_i = d_amax_i;
+    l.h_meta = h_meta; l.h_next = h_next;
+    l.scratch = scratch;
+    l.norm_p32 = norm_p32;
+  }
+  void select_lane(int i) {
+    save_lane();
+    lane = i;
+    const Lane& l = lanes[i];
+    stream = l.stream;
+    x = l.x; norm = l.norm; qkv = l.qkv; attn = l.attn; mlp = l.mlp; last = l.last;
+    logits = l.logits;
+    d_meta = l.d_meta; d_next = l.d_next;
+    d_amax_v = l.d_amax_v; d_amax_i = l.d_amax_i;
+    h_meta = l.h_meta; h_next = l.h_next;
+    scratch = l.scratch;
+    norm_p32 = l.norm_p32;
+    // The metadata layout ids[rows] | slots[B] | qlens[B] | offsets[B] of each
+    // lane, B = max_batch.
+    const size_t rows = i == 0 ? std::max<size_t>(size_t(opt.max_batch) * opt.capacity, 32) : 32;
+    d_ids = d_meta;
+    d_slots = d_ids + rows;
+    d_qlens = d_slots + opt.max_batch;
+    d_offsets = d_qlens + opt.max_batch;
+    h_ids = h_meta;
+    h_slots = h_ids + rows;
+    h_qlens = h_slots + opt.max_batch;
+    h_offsets = h_qlens + opt.max_batch;
+  }
 
   template <class T>
   T* alloc(size_t count) {
@@ -298,11 +394,18 @@ struct ti_llm_model {
     int previous = -1;
     (void)hipGetDevice(&previous);
     (void)hipSetDevice(opt.device);
-    if (stream) (void)hipStreamSynchronize(stream);
-    for (auto& g : decode_graphs) (void)hipGraphExecDestroy(g.second);
+    if (stream) save_lane();
+    for (Lane& l : lanes) {
+      if (l.stream) (void)hipStreamSynchronize(l.stream);
+      for (auto& g : l.decode_graphs) (void)hipGraphExecDestroy(g.second);
+    }
     for (void* p : allocations) (void)hipFree(p);
     if (pinned) (void)hipHostFree(pinned);
-    if (stream) (void)hipStreamDestroy(stream);
+    if (pinned_lane1) (void)hipHostFree(pinned_lane1);
+    for (void* p : pinned_runs)
+      if (p) (void)hipHostFree(p);
+    for (Lane& l : lanes)
+      if (l.stream) (void)hipStreamDestroy(l.stream);
     if (previous >= 0) (void)hipSetDevice(previous);
   }
 
@@ -457,6 +560,40 @@ struct ti_llm_model {
     scratch.partials = alloc<float>(tia::kScratchPartialFloats);
     scratch.partial_floats = tia::kScratchPartialFloats;
     lengths.assign(opt.cache_slots + 1, 0);
+    save_lane();
+    // Lane 1 (decode steps of more than kLaneRows requests over the packed
+    // INT8 weights): its own stream, 32-row activations, metadata, head
+    // outputs and scratch.
+    two_lanes = opt.max_batch > kLaneRows && quantized && head.packed && H % 64 == 0;
+    if (two_lanes) {
+      Lane& l = lanes[1];
+      ck(hipStreamCreateWithFlags(&l.stream, hipStreamNonBlocking));
+      l.x = alloc<uint16_t>(32 * size_t(H));
+      l.norm = alloc<uint16_t>(32 * size_t(H));
+      l.qkv = alloc<uint16_t>(32 * 3 * size_t(H));
+      l.attn = alloc<uint16_t>(32 * size_t(H));
+      l.mlp = alloc<uint16_t>(32 * 4 * size_t(H));
+      l.last = alloc<uint16_t>(32 * size_t(H));
+      l.logits = alloc<float>(size_t(kLaneRows) * size_t(head.ldw));
+      const size_t ints = 32 + 3 * size_t(opt.max_batch);
+      l.d_meta = alloc<int32_t>(ints);
+      l.d_next = alloc<int32_t>(opt.max_batch);
+      l.d_amax_v = alloc<float>(kAmaxEntries);
+      l.d_amax_i = alloc<int32_t>(kAmaxEntries);
+      ck(hipHostMalloc(&pinned_lane1, (ints + opt.max_batch) * sizeof(int32_t), hipHostMallocDefault));
+      l.h_meta = static_cast<int32_t*>(pinned_lane1);
+      l.h_next = l.h_meta + ints;
+      l.scratch.partials = alloc<float>(tia::kScratchPartialFloats);
+      l.scratch.partial_floats = tia::kScratchPartialFloats;
+    }
+    for (int i = 0; i < (two_lanes ? 2 : 1); ++i) {
+      Lane& l = lanes[i];
+      const size_t ids = size_t(opt.capacity) * size_t(i == 0 ? opt.max_batch : kLaneRows);
+      l.d_run = alloc<int32_t>(ids);
+      l.d_run_step = alloc<uint32_t>(1);
+      ck(hipHostMalloc(&pinned_runs[i], ids * sizeof(int32_t), hipHostMallocDefault));
+      l.h_run = static_cast<int32_t*>(pinned_runs[i]);
+    }
     ck(hipStreamSynchronize(stream));
   }
 
@@ -549,8 +686,6 @@ struct ti_llm_model {
     return qlen == 1 && quantized && head.packed && c_attn[0].packed &&
            tia::gemm_ln_supported(b, H, H);
   }
-
-  bool norm_p32 = false;  // the last layers() pass left x and norm P32-packed
 
   // One pass of the transformer over rows [b, qlen] whose metadata is already on
   // the device; leaves the residual stream in x and ln_f(x) of every row in norm
@@ -735,6 +870,7 @@ struct ti_llm_model {
   }
 
   void decode_step_graph(int b) {
+    auto& decode_graphs = lanes[lane].decode_graphs;
     auto it = decode_graphs.find(b);
     if (it == decode_graphs.end()) {
       hipGraph_t graph = nullptr;
@@ -742,6 +878,9 @@ struct ti_llm_model {
       try {
         layers(b, 1);
         head_and_argmax(b, 1, true);
+        feed_kernel<<<1, 64, 0, stream>>>(d_next, d_ids, d_offsets, lanes[lane].d_run, lanes[lane].d_run_step,
+                                          uint32_t(opt.capacity), b);
+        ck(hipGetLastError());
       } catch (...) {
         hipGraph_t dropped = nullptr;
         (void)hipStreamEndCapture(stream, &dropped);
@@ -797,6 +936,52 @@ struct ti_llm_model {
     ck(hipStreamSynchronize(stream));
     if (greedy) std::copy(h_next, h_next + b, greedy);
     for (int i = 0; i < b; ++i) lengths[s[i]] += lens[i];
+  }
+
+  // Greedy-decode `steps` tokens for each of b requests (slots s, last ids
+  // `ids`) as one run: the steps are queued back to back (the captured step
+  // feeds its own ids forward) and the host waits once, at the end.  More
+  // than kLaneRows requests split into two lanes queued side by side.
+  // tokens[t * b + i] is request i's token after step t.
+  void decode_run(const int32_t* s, const int32_t* ids, int b, int steps, int32_t* tokens) {
+    check();
+    if (b < 1 || b > opt.max_batch || steps < 1) throw Invalid("invalid decode run");
+    for (int i = 0; i < b; ++i)
+      if (lengths[s[i]] + steps > opt.capacity) throw Invalid("decode run exceeds the cache capacity");
+    const bool split = two_lanes && b > kLaneRows && ln_fused(kLaneRows, 1);
+    const int parts = split ? 2 : 1;
+    const int first[2] = {0, split ? (b + 1) / 2 : b};
+    const int count[2] = {first[1], b - first[1]};
+    for (int l = 0; l < parts; ++l) {
+      select_lane(l);
+      for (int j = 0; j < count[l]; ++j) {
+        const int i = first[l] + j;
+        h_ids[j] = ids[i];
+        h_slots[j] = s[i];
+        h_qlens[j] = 1;
+        h_offsets[j] = lengths[s[i]];
+      }
+      upload_meta(count[l], 1);
+      ck(hipMemsetAsync(lanes[l].d_run_step, 0, sizeof(uint32_t), stream));
+    }
+    for (int t = 0; t < steps; ++t)
+      for (int l = 0; l < parts; ++l) {
+        select_lane(l);
+        decode_step_graph(count[l]);
+      }
+    for (int l = 0; l < parts; ++l) {
+      select_lane(l);
+      ck(hipMemcpyAsync(lanes[l].h_run, lanes[l].d_run, size_t(steps) * count[l] * sizeof(int32_t),
+                        hipMemcpyDeviceToHost, stream));
+    }
+    select_lane(0);
+    for (int l = 0; l < parts; ++l) ck(hipStreamSynchronize(lanes[l].stream));
+    for (int l = 0; l < parts; ++l)
+      for (int t = 0; t < steps; ++t)
+        std::copy(lanes[l].h_run + size_t(t) * count[l], lanes[l].h_run + size_t(t + 1) * count[l],
+                  tokens + size_t(t) * b + first[l]);
+    for (int t = 0; t < steps; ++t) count_forward(true, true);
+    for (int i = 0; i < b; ++i) lengths[s[i]] += steps;
   }
 
   // reference runtime.cu:204-211
@@ -993,25 +1178,30 @@ extern "C" int ti_llm_greedy_batch(ti_llm_model* m, const int32_t* slots, const 
       if (ttft) ttft[i] = first;
       if (total && requested[i] == 1) total[i] = first;
     }
+    // Decode in runs: each run advances every unfinished request by the
+    // fewest tokens any of them still needs, so the active set is fixed
+    // within a run and at least one request finishes at its end.
     for (;;) {
-      std::vector<int32_t> active, ids, ones;
+      std::vector<int32_t> active, ids;
       std::vector<int> owner;
+      int steps = 0;
       for (int i = 0; i < batch; ++i)
         if (done[i] < requested[i]) {
           active.push_back(slots[i]);
           ids.push_back(next[i]);
-          ones.push_back(1);
           owner.push_back(i);
+          steps = steps ? std::min(steps, requested[i] - done[i]) : requested[i] - done[i];
         }
       if (active.empty()) break;
-      std::vector<int32_t> generated(active.size());
-      m->forward(active.data(), ids.data(), ones.data(), int(active.size()), 1, nullptr, generated.data());
+      const int n = int(active.size());
+      std::vector<int32_t> generated(size_t(steps) * n);
+      m->decode_run(active.data(), ids.data(), n, steps, generated.data());
       const double elapsed = ms_since(start);
-      for (size_t j = 0; j < owner.size(); ++j) {
+      for (int j = 0; j < n; ++j) {
         const int i = owner[j];
-        next[i] = generated[j];
-        output[int64_t(i) * out_stride + done[i]] = next[i];
-        ++done[i];
+        for (int t = 0; t < steps; ++t) output[int64_t(i) * out_stride + done[i] + t] = generated[size_t(t) * n + j];
+        done[i] += steps;
+        next[i] = generated[size_t(steps - 1) * n + j];
         if (total && done[i] == requested[i]) total[i] = elapsed;
       }
     }
