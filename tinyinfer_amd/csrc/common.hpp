@@ -56,6 +56,15 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Running argmax step: largest value, lowest index on ties; NaN never wins
+// (reference llm/src/runtime.cu:59-66).
+__device__ __forceinline__ void amax_merge(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
 // Butterfly reductions across the 64 lanes of a wave.  Every lane ends with the
 // full result.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -357,7 +357,12 @@ struct PackedParams {
   const uint16_t* ln_gamma;  // A = LayerNorm(a rows; gamma, beta, eps) when set
   const uint16_t* ln_beta;
   float ln_eps;
+  // MT = 1, one split, fp32 epilogue: when set, per (workgroup, row) best
+  // output and its column, as the wide GEMV leaves them for greedy decoding.
+  float* amax_v;
+  int32_t* amax_i;
 };
+
 
 // fp16_rn(float(q) * scale) of the 8 bytes in (lo, hi): one MFMA B operand.
 __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scale) {
@@ -458,10 +463,13 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     u32x4_t wf[CPW][CBG];
     half8_t af[CPW][2][MT];
     half8_t gbv;
+    // Plain (cached) loads: two decode lanes stream the same records
+    // microseconds apart, and the second finds them in cache (b = 32 decode as
+    // two 16-row lanes: 102 K against 92 K tok/s with nontemporal loads).
     auto load_w = [&](int i) {
       const int c = min(c0 + i * W, c_end - 1);
 #pragma unroll
-      for (int r = 0; r < CBG; ++r) wf[i][r] = __builtin_nontemporal_load(wb[r] + int64_t(c) * 64);
+      for (int r = 0; r < CBG; ++r) wf[i][r] = wb[r][int64_t(c) * 64];
     };
     auto load_a = [&](int i) {
       const int c = min(c0 + i * W, c_end - 1);
@@ -611,6 +619,8 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   // the main loop).
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
+  float amax_val = -__builtin_huge_valf();  // MT = 1: this thread's (single) output
+  int amax_col = INT_MAX;
 #pragma unroll
   for (int it = 0; it < kOutIters; ++it) {
     const int o = tid + it * W * 64, r = o / per_block, rem = o - r * per_block;
@@ -625,6 +635,24 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     const float bias = has_bias ? h2f(braw) : 0.f;
     if (epi_now) apply_epilogue(p.epi, row, n, s, bias, has_res ? h2f(res_raw[it]) : 0.f);
     else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
+    if (MT == 1) {
+      amax_val = s + bias;  // the EPI_F32 value
+      amax_col = n;
+    }
+  }
+  if constexpr (MT == 1) {
+    // Argmax partials: thread o holds row o / 16, column o % 16 of the single
+    // block (CBG = 1, one output per thread), so a row's 16 columns are 16
+    // consecutive lanes of one wave.
+    static_assert(MT != 1 || (CBG == 1 && kOutIters == 1), "one output per thread");
+    if (!p.amax_v) return;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1)
+      amax_merge(amax_val, amax_col, __shfl_xor(amax_val, o, 64), __shfl_xor(amax_col, o, 64));
+    if ((tid & 15) == 0 && tid < per_block) {
+      p.amax_v[(tid >> 4) * groups + grp] = amax_val;
+      p.amax_i[(tid >> 4) * groups + grp] = amax_col;
+    }
   }
 }
 
@@ -723,15 +751,6 @@ struct WideParams {
   int32_t* amax_i;
 };
 
-// Largest value, lowest index on ties; NaN never wins (reference
-// llm/src/runtime.cu:59-66).
-__device__ __forceinline__ void amax_merge(float& bv, int& bi, float v, int i) {
-  if (v > bv || (v == bv && i < bi)) {
-    bv = v;
-    bi = i;
-  }
-}
-
 template <int MT, int KC, int W, bool AP32>
 __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
   // A as MFMA fragments ((c * MT + t) * 2 + s) * 64 + lane: rows 16t + (lane & 15),
@@ -765,7 +784,7 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
   auto load = [&](Block& b, int i) {
     const int cb = min(cb_first + W * i, p.nb - 1), col = min(cb * 16 + j, p.n - 1);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) b.w[c] = __builtin_nontemporal_load(p.w + (int64_t(cb) * KC + c) * 64 + lane);
+    for (int c = 0; c < KC; ++c) b.w[c] = p.w[(int64_t(cb) * KC + c) * 64 + lane];  // cached, as the packed GEMV
     b.scale = p.scales[col];
     b.bias = bsrc[has_bias ? col : 0];
   };
@@ -856,8 +875,8 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
       int i = si[0][threadIdx.x];
 #pragma unroll
       for (int w = 1; w < W; ++w) amax_merge(v, i, sv[w][threadIdx.x], si[w][threadIdx.x]);
-      p.amax_v[blockIdx.x * 32 + threadIdx.x] = v;
-      p.amax_i[blockIdx.x * 32 + threadIdx.x] = i;
+      p.amax_v[threadIdx.x * gridDim.x + blockIdx.x] = v;
+      p.amax_i[threadIdx.x * gridDim.x + blockIdx.x] = i;
     }
   }
 }
@@ -869,7 +888,7 @@ __global__ __launch_bounds__(64) void argmax_partials_kernel(const float* vals, 
   const int row = blockIdx.x, lane = threadIdx.x;
   float v = -__builtin_huge_valf();
   int i = INT_MAX;
-  for (int gi = lane; gi < groups; gi += 64) amax_merge(v, i, vals[gi * 32 + row], idx[gi * 32 + row]);
+  for (int gi = lane; gi < groups; gi += 64) amax_merge(v, i, vals[row * groups + gi], idx[row * groups + gi]);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) amax_merge(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
   if (lane == 0) out[row] = i;
@@ -1518,6 +1537,12 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   if (MT == 2 && !p.defer && sh.w == 4 && (p.nb + 1) / 2 >= 512) sh.cbg = 2;
   const int grid = (p.nb + sh.cbg - 1) / sh.cbg * splits;
   if (deferred) *deferred = splits;
+  if (MT == 1 && splits == 1 && !p.defer && p.epi.kind == EPI_F32 && g.amax_v && g.amax_i && g.amax_groups &&
+      size_t(grid) * 32 <= g.amax_capacity) {
+    p.amax_v = g.amax_v;
+    p.amax_i = g.amax_i;
+    *g.amax_groups = grid;
+  }
   if (g.a_p32)
     return ln ? launch_gemv_shape<MT, true, true>(p, sh, grid, stream)
               : launch_gemv_shape<MT, false, true>(p, sh, grid, stream);

@@ -64,10 +64,12 @@ struct GemmArgs {
   const void* w_f16p = nullptr;
   // A is P32 fragment-packed (M <= 32, packed W; lda ignored).
   bool a_p32 = false;
-  // Optional greedy partials (EPI_F32 logits): when the wide LM-head GEMV runs
-  // it also writes each workgroup's best (value, column) per row to
-  // amax_v/amax_i[group * 32 + row] (capacity entries) and sets *amax_groups;
-  // otherwise *amax_groups = 0.  argmax_partials finishes them.
+  // Optional greedy partials (EPI_F32 logits): when the wide LM-head GEMV or a
+  // one-split packed GEMV of up to 16 rows runs, it also writes each
+  // workgroup's best (value, column) per row to amax_v/amax_i[row * groups +
+  // group] (at most 32 * groups <= capacity entries; a row's partials are
+  // contiguous) and sets *amax_groups = groups; otherwise *amax_groups = 0.
+  // argmax_partials finishes them.
   float* amax_v = nullptr;
   int32_t* amax_i = nullptr;
   size_t amax_capacity = 0;

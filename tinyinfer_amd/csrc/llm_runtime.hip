@@ -25,13 +25,14 @@
 //  * the captured step ends with a feed kernel (its greedy ids become the next
 //    step's input ids, positions advance by one), so ti_llm_greedy_batch queues
 //    each run of decode steps over an unchanged set of requests back to back,
-//    with the ids copied to pinned memory as they come, and waits once per run;
-//  * such a run of more than 16 requests splits into two lanes of at most 16,
-//    each with its own stream, activations, scratch and captured graph over the
-//    shared weights and KV cache, queued side by side: one lane's chain of 64
-//    dependent launches leaves most CUs idle, and two free-running chains fill
-//    them.  A request's logits are the same bits in either lane, since the
-//    decode kernels sum every row in one K order at every batch size.
+//    records every step's ids on the device, and waits once per run;
+//  * such a run of more than kLaneRows requests splits evenly over lanes of at
+//    most kLaneRows, each with its own stream, activations, scratch and
+//    captured graph over the shared weights and KV cache, queued side by side:
+//    one lane's chain of 64 dependent launches leaves most CUs idle, and
+//    free-running chains fill them.  A request's logits are the same bits in
+//    any lane, since the decode kernels sum every row in one K order at every
+//    batch size.
 #include <algorithm>
 #include <chrono>
 #include <climits>
@@ -62,7 +63,8 @@ constexpr int kHeadDim = 64;
 // LayerNorm row kernel: 11.4 K).
 constexpr int kResidualSplitWorkgroups = 192;
 // Decode steps of more than this many requests run as two concurrent lanes.
-constexpr int kLaneRows = 16;
+constexpr int kLanes = 2, kLaneRows = 16;
+static_assert(kLanes * kLaneRows >= 32, "the lanes must hold a full decode batch");
 
 struct GpuError : std::runtime_error {
   using std::runtime_error::runtime_error;
@@ -98,20 +100,16 @@ __global__ void gather_last_kernel(const uint16_t* x, uint16_t* out, const int32
       *reinterpret_cast<const tia::half8_t*>(x + (int64_t(b) * qlen + qlens[b] - 1) * hidden + c);
 }
 
-// x[row] = fp16(wte[id] + wpe[offset + t]) for t < qlens[b], else 0 (reference
-// runtime.cu:25-30), fused with the first layer's LayerNorm of that row: one
-// wave per row, lane owns the 8-wide column groups lane + 64 i (hidden <= 2048).
-// p32: x and norm are written P32 fragment-packed (rows <= 32, hidden % 64 == 0).
-__global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const int32_t* qlens,
-                                                       const int32_t* offsets, const uint16_t* wte,
-                                                       const uint16_t* wpe, const uint16_t* g, const uint16_t* bt,
-                                                       uint16_t* x, uint16_t* norm, int rows, int qlen, int hidden,
-                                                       bool p32) {
+// One embedding row, x = fp16(wte[id] + wpe[pos]) (zeros when !valid;
+// reference runtime.cu:25-30), and the first layer's LayerNorm of it into
+// norm: one wave, lane owns the 8-wide column groups lane + 64 i (hidden <=
+// 2048).  p32: x and norm are written P32 fragment-packed (rows <= 32, hidden
+// % 64 == 0).
+__device__ __forceinline__ void embed_ln_row(int lane, bool valid, int id, int pos, const uint16_t* wte,
+                                             const uint16_t* wpe, const uint16_t* g, const uint16_t* bt,
+                                             uint16_t* x, uint16_t* norm, int row, int hidden, bool p32) {
   constexpr int NV = 4;
-  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int b = row / qlen, t = row - b * qlen, groups = hidden / 8;
-  const bool valid = t < qlens[b];
+  const int groups = hidden / 8;
   float v[NV][8];
   float s = 0.f;
 #pragma unroll
@@ -121,9 +119,8 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const
     for (int k = 0; k < 8; ++k) v[i][k] = 0.f;
     if (gi < groups) {
       if (valid) {
-        const tia::half8_t e = *reinterpret_cast<const tia::half8_t*>(wte + int64_t(ids[row]) * hidden + 8 * gi);
-        const tia::half8_t p =
-            *reinterpret_cast<const tia::half8_t*>(wpe + int64_t(offsets[b] + t) * hidden + 8 * gi);
+        const tia::half8_t e = *reinterpret_cast<const tia::half8_t*>(wte + int64_t(id) * hidden + 8 * gi);
+        const tia::half8_t p = *reinterpret_cast<const tia::half8_t*>(wpe + int64_t(pos) * hidden + 8 * gi);
 #pragma unroll
         for (int k = 0; k < 8; ++k) v[i][k] = float(tia::f16r(float(e[k]) + float(p[k])));
       }
@@ -159,6 +156,21 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const
   }
 }
 
+// Embedding rows of a pass, row = b * qlen + t, position offsets[b] + t, zero
+// for t >= qlens[b]: one wave per row.
+__global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const int32_t* qlens,
+                                                       const int32_t* offsets, const uint16_t* wte,
+                                                       const uint16_t* wpe, const uint16_t* g, const uint16_t* bt,
+                                                       uint16_t* x, uint16_t* norm, int rows, int qlen, int hidden,
+                                                       bool p32) {
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int b = row / qlen, t = row - b * qlen;
+  const bool valid = t < qlens[b];
+  const int id = valid ? ids[row] : 0, pos = valid ? offsets[b] + t : 0;
+  embed_ln_row(lane, valid, id, pos, wte, wpe, g, bt, x, norm, row, hidden, p32);
+}
+
 // Greedy id per row: largest logit, lowest id on ties (reference runtime.cu:59-66).
 // One 1024-thread block per row, 16-byte loads over a row pitch `ld` (a multiple
 // of 4 floats).
@@ -169,15 +181,22 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int32
   float best = -__builtin_huge_valf();
   int idx = INT_MAX;
   const int vec = vocab / 4;
-  for (int j4 = threadIdx.x; j4 < vec; j4 += 1024) {
-    const float4 v = *reinterpret_cast<const float4*>(row + 4 * j4);
-    const float e[4] = {v.x, v.y, v.z, v.w};
+  // Four 16-byte loads per thread in flight at a time.
+  for (int j0 = threadIdx.x; j0 < vec; j0 += 4 * 1024) {
+    float4 v[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (e[k] > best) {  // ids visited in increasing order: equality keeps the lower id
-        best = e[k];
-        idx = 4 * j4 + k;
-      }
+    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4*>(row + 4 * min(j0 + u * 1024, vec - 1));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j4 = j0 + u * 1024;
+      const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (j4 < vec && e[k] > best) {  // ids visited in increasing order: equality keeps the lower id
+          best = e[k];
+          idx = 4 * j4 + k;
+        }
+    }
   }
   for (int j = 4 * vec + threadIdx.x; j < vocab; j += 1024)
     if (row[j] > best) {
@@ -243,24 +262,80 @@ __global__ __launch_bounds__(256) void sum_kernel(const double* v, double* out, 
   if (threadIdx.x == 0) *out = s[0] + s[1] + s[2] + s[3];
 }
 
-// End of a captured decode step: the step's greedy ids become the next step's
-// input ids and every request's position advances by one, so a run of decode
-// steps needs no host round trip between steps.
-// Step t of a run also lands in run[t * b + i] (t counted in *run_step, which
-// the run's caller clears; steps past run_steps are not recorded).  One
-// workgroup of 64 threads, b <= 32.
-__global__ void feed_kernel(const int32_t* next, int32_t* ids, int32_t* offsets, int32_t* run, uint32_t* run_step,
-                            uint32_t run_steps, int b) {
-  const int i = threadIdx.x;
-  const uint32_t t = *run_step;
-  __syncthreads();  // every thread has read the step before thread 0 advances it
-  if (i < b) {
-    const int32_t v = next[i];
-    ids[i] = v;
-    offsets[i] += 1;
-    if (t < run_steps) run[size_t(t) * b + i] = v;
+// End of a captured decode step, one workgroup per request row (1024 threads
+// over partials, else 64):
+//  * the row's greedy id: from the head GEMV's per-workgroup partials (largest
+//    value, lowest id on ties: the same id in any merge order), or already in
+//    next[row] when groups == 0;
+//  * next[row] = id and run[pos * b + row] = id, pos = offsets[row] the
+//    position of the step's input token, so a run of steps leaves every id on
+//    the device;
+//  * the id is the next step's input: ids[row] = id, offsets[row] = pos + 1,
+//    and its embedding row with the first LayerNorm is written now (the
+//    embedding kernel's work), so the next step starts at layer 0.  An id
+//    outside the vocabulary (non-finite logits) is recorded as is for the host
+//    to reject and embedded as 0; no embedding is written past the last
+//    position.
+struct FeedArgs {
+  const float* vals;
+  const int32_t* idx;
+  int groups;
+  int32_t *next, *ids, *offsets, *run;
+  int b, vocab, positions, hidden;
+  const uint16_t *wte, *wpe, *g, *bt;
+  uint16_t *x, *norm;
+  bool p32;
+};
+
+__global__ __launch_bounds__(1024) void greedy_feed_kernel(FeedArgs a) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nt = blockDim.x;
+  int id;
+  if (a.groups > 0) {
+    // Four partials per thread in flight at a time.
+    float v = -__builtin_huge_valf();
+    int i = INT_MAX;
+    for (int g0 = threadIdx.x; g0 < a.groups; g0 += 4 * nt) {
+      float pv[4];
+      int pi[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int gi = min(g0 + u * nt, a.groups - 1);
+        pv[u] = a.vals[row * a.groups + gi];
+        pi[u] = a.idx[row * a.groups + gi];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (g0 + u * nt < a.groups) tia::amax_merge(v, i, pv[u], pi[u]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) tia::amax_merge(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
+    if (lane == 0) {
+      sv[wave] = v;
+      si[wave] = i;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    v = sv[0];
+    i = si[0];
+    for (int w = 1; w < nt / 64; ++w) tia::amax_merge(v, i, sv[w], si[w]);
+    id = i;
+  } else {
+    if (wave != 0) return;
+    id = a.next[row];
   }
-  if (i == 0) *run_step = t + 1;
+  const int pos = a.offsets[row];
+  if (lane == 0) {
+    a.next[row] = id;
+    a.run[int64_t(pos) * a.b + row] = id;
+    a.ids[row] = id;
+    a.offsets[row] = pos + 1;
+  }
+  if (pos + 1 < a.positions) {
+    const bool ok = id >= 0 && id < a.vocab;
+    embed_ln_row(lane, true, ok ? id : 0, pos + 1, a.wte, a.wpe, a.g, a.bt, a.x, a.norm, row, a.hidden, a.p32);
+  }
 }
 
 __global__ void zero_f64_kernel(double* p, int n) {
@@ -334,17 +409,16 @@ struct ti_llm_model {
     tia::Scratch scratch;
     bool norm_p32 = false;
     std::map<int, hipGraphExec_t> decode_graphs;
-    // Greedy ids of a run of decode steps: device [capacity][rows] with its
-    // step counter, and the pinned host copy.
+    // Greedy ids of a run of decode steps: device [position][rows] (the
+    // position of the step's input token) and the pinned host copy.
     int32_t* d_run = nullptr;
-    uint32_t* d_run_step = nullptr;
     int32_t* h_run = nullptr;
   };
-  Lane lanes[2];
+  Lane lanes[kLanes];
   int lane = 0;
-  bool two_lanes = false;
-  void* pinned_lane1 = nullptr;
-  void* pinned_runs[2] = {nullptr, nullptr};
+  int lane_count = 1;
+  void* pinned_lanes[kLanes] = {};
+  void* pinned_runs[kLanes] = {};
 
   void save_lane() {
     Lane& l = lanes[lane];
@@ -401,7 +475,8 @@ struct ti_llm_model {
     }
     for (void* p : allocations) (void)hipFree(p);
     if (pinned) (void)hipHostFree(pinned);
-    if (pinned_lane1) (void)hipHostFree(pinned_lane1);
+    for (void* p : pinned_lanes)
+      if (p) (void)hipHostFree(p);
     for (void* p : pinned_runs)
       if (p) (void)hipHostFree(p);
     for (Lane& l : lanes)
@@ -561,12 +636,13 @@ struct ti_llm_model {
     scratch.partial_floats = tia::kScratchPartialFloats;
     lengths.assign(opt.cache_slots + 1, 0);
     save_lane();
-    // Lane 1 (decode steps of more than kLaneRows requests over the packed
-    // INT8 weights): its own stream, 32-row activations, metadata, head
-    // outputs and scratch.
-    two_lanes = opt.max_batch > kLaneRows && quantized && head.packed && H % 64 == 0;
-    if (two_lanes) {
-      Lane& l = lanes[1];
+    // Lanes 1.. (decode runs of more than kLaneRows requests over the packed
+    // INT8 weights): own stream, 32-row activations, metadata, head outputs
+    // and scratch.
+    if (opt.max_batch > kLaneRows && quantized && head.packed && H % 64 == 0)
+      lane_count = std::min(kLanes, (opt.max_batch + kLaneRows - 1) / kLaneRows);
+    for (int i = 1; i < lane_count; ++i) {
+      Lane& l = lanes[i];
       ck(hipStreamCreateWithFlags(&l.stream, hipStreamNonBlocking));
       l.x = alloc<uint16_t>(32 * size_t(H));
       l.norm = alloc<uint16_t>(32 * size_t(H));
@@ -580,17 +656,16 @@ struct ti_llm_model {
       l.d_next = alloc<int32_t>(opt.max_batch);
       l.d_amax_v = alloc<float>(kAmaxEntries);
       l.d_amax_i = alloc<int32_t>(kAmaxEntries);
-      ck(hipHostMalloc(&pinned_lane1, (ints + opt.max_batch) * sizeof(int32_t), hipHostMallocDefault));
-      l.h_meta = static_cast<int32_t*>(pinned_lane1);
+      ck(hipHostMalloc(&pinned_lanes[i], (ints + opt.max_batch) * sizeof(int32_t), hipHostMallocDefault));
+      l.h_meta = static_cast<int32_t*>(pinned_lanes[i]);
       l.h_next = l.h_meta + ints;
       l.scratch.partials = alloc<float>(tia::kScratchPartialFloats);
       l.scratch.partial_floats = tia::kScratchPartialFloats;
     }
-    for (int i = 0; i < (two_lanes ? 2 : 1); ++i) {
+    for (int i = 0; i < lane_count; ++i) {
       Lane& l = lanes[i];
       const size_t ids = size_t(opt.capacity) * size_t(i == 0 ? opt.max_batch : kLaneRows);
       l.d_run = alloc<int32_t>(ids);
-      l.d_run_step = alloc<uint32_t>(1);
       ck(hipHostMalloc(&pinned_runs[i], ids * sizeof(int32_t), hipHostMallocDefault));
       l.h_run = static_cast<int32_t*>(pinned_runs[i]);
     }
@@ -690,18 +765,28 @@ struct ti_llm_model {
   // One pass of the transformer over rows [b, qlen] whose metadata is already on
   // the device; leaves the residual stream in x and ln_f(x) of every row in norm
   // (both P32 fragment-packed after an ln_fused pass, row-major otherwise).
-  void layers(int b, int qlen) {
+  // Fragment-packed activations from two rows up: a single row reads one
+  // cache line per A fragment either way, and its row-major output writes are
+  // contiguous.
+  bool p32_pass(int b, int qlen) const { return ln_fused(b, qlen) && b * qlen > 1; }
+
+  // Embedding rows and layer 0's ln_1 of a pass whose metadata is on the device.
+  void embed(int b, int qlen) {
+    const int rows = b * qlen;
+    embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, ln1_g[0],
+                                                             ln1_b[0], x, norm, rows, qlen, H, p32_pass(b, qlen));
+    ck(hipGetLastError());
+  }
+
+  // `embedded`: x and norm already hold the embedding rows (the previous
+  // decode step's greedy_feed_kernel, or embed()).
+  void layers(int b, int qlen, bool embedded = false) {
     const int rows = b * qlen;
     prefill_pass = qlen > 1;
     const bool fuse = ln_fused(b, qlen);
-    // Fragment-packed activations from two rows up: a single row reads one
-    // cache line per A fragment either way, and its row-major output writes
-    // are contiguous.
-    const bool p32 = fuse && rows > 1;
+    const bool p32 = p32_pass(b, qlen);
     norm_p32 = p32;
-    embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, ln1_g[0],
-                                                             ln1_b[0], x, norm, rows, qlen, H, p32);
-    ck(hipGetLastError());
+    if (!embedded) embed(b, qlen);
     // The LayerNorm before c_attn / c_fc: in the GEMV's prologue up to hidden
     // 1024; above, every one of the GEMV's workgroups normalising all rows
     // costs more VALU time than a row kernel (measured at GPT-2 XL's 1600).
@@ -817,7 +902,8 @@ struct ti_llm_model {
 
   // Logits of each request's last row (norm already holds ln_f), fp32 without
   // bias over the padded row pitch head.ldw, then the greedy argmax.
-  void head_and_argmax(int b, int qlen, bool greedy) {
+  // `feed` (a captured decode step): greedy_feed_kernel ends the step.
+  void head_and_argmax(int b, int qlen, bool greedy, bool feed = false) {
     const uint16_t* rows_in = norm;
     if (qlen > 1) {
       gather_last_kernel<<<blocks_for(int64_t(b) * H / 8), 256, 0, stream>>>(norm, last, d_qlens, b, qlen, H);
@@ -832,11 +918,34 @@ struct ti_llm_model {
     // finishing kernel replaces the pass over all logits.
     int groups = 0;
     gemm(rows_in, b, head, e, nullptr, nullptr, nullptr, norm_p32 && qlen == 1, greedy ? &groups : nullptr);
-    if (greedy && groups > 0) {
-      ck(tia::argmax_partials(d_amax_v, d_amax_i, groups, b, d_next, stream));
-    } else if (greedy) {
+    if (greedy && groups == 0) {
       argmax_kernel<<<b, 1024, 0, stream>>>(logits, d_next, V, head.ldw);
       ck(hipGetLastError());
+    }
+    if (feed) {
+      FeedArgs f;
+      f.vals = d_amax_v;
+      f.idx = d_amax_i;
+      f.groups = groups;
+      f.next = d_next;
+      f.ids = d_ids;
+      f.offsets = d_offsets;
+      f.run = lanes[lane].d_run;
+      f.b = b;
+      f.vocab = V;
+      f.positions = opt.capacity;
+      f.hidden = H;
+      f.wte = wte;
+      f.wpe = wpe;
+      f.g = ln1_g[0];
+      f.bt = ln1_b[0];
+      f.x = x;
+      f.norm = norm;
+      f.p32 = p32_pass(b, 1);
+      greedy_feed_kernel<<<b, groups > 0 ? 1024 : 64, 0, stream>>>(f);
+      ck(hipGetLastError());
+    } else if (greedy && groups > 0) {
+      ck(tia::argmax_partials(d_amax_v, d_amax_i, groups, b, d_next, stream));
     }
   }
 
@@ -869,6 +978,8 @@ struct ti_llm_model {
     (void)rows;
   }
 
+  // One greedy decode step of b rows as a graph launch: layers over the
+  // embedding rows already in x / norm, head, greedy_feed_kernel.
   void decode_step_graph(int b) {
     auto& decode_graphs = lanes[lane].decode_graphs;
     auto it = decode_graphs.find(b);
@@ -876,11 +987,8 @@ struct ti_llm_model {
       hipGraph_t graph = nullptr;
       ck(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
       try {
-        layers(b, 1);
-        head_and_argmax(b, 1, true);
-        feed_kernel<<<1, 64, 0, stream>>>(d_next, d_ids, d_offsets, lanes[lane].d_run, lanes[lane].d_run_step,
-                                          uint32_t(opt.capacity), b);
-        ck(hipGetLastError());
+        layers(b, 1, true);
+        head_and_argmax(b, 1, true, true);
       } catch (...) {
         hipGraph_t dropped = nullptr;
         (void)hipStreamEndCapture(stream, &dropped);
@@ -923,6 +1031,7 @@ struct ti_llm_model {
     const bool need_head = out || greedy;
     upload_meta(b, qlen);
     if (qlen == 1 && greedy) {
+      embed(b, 1);
       decode_step_graph(b);
     } else {
       layers(b, qlen);
@@ -941,17 +1050,19 @@ struct ti_llm_model {
   // Greedy-decode `steps` tokens for each of b requests (slots s, last ids
   // `ids`) as one run: the steps are queued back to back (the captured step
   // feeds its own ids forward) and the host waits once, at the end.  More
-  // than kLaneRows requests split into two lanes queued side by side.
-  // tokens[t * b + i] is request i's token after step t.
+  // than kLaneRows requests split evenly over ceil(b / kLaneRows) lanes,
+  // queued side by side.  tokens[t * b + i] is request i's token after step t.
   void decode_run(const int32_t* s, const int32_t* ids, int b, int steps, int32_t* tokens) {
     check();
     if (b < 1 || b > opt.max_batch || steps < 1) throw Invalid("invalid decode run");
     for (int i = 0; i < b; ++i)
       if (lengths[s[i]] + steps > opt.capacity) throw Invalid("decode run exceeds the cache capacity");
-    const bool split = two_lanes && b > kLaneRows && ln_fused(kLaneRows, 1);
-    const int parts = split ? 2 : 1;
-    const int first[2] = {0, split ? (b + 1) / 2 : b};
-    const int count[2] = {first[1], b - first[1]};
+    const int parts = lane_count > 1 && b > kLaneRows && ln_fused(kLaneRows, 1) ? (b + kLaneRows - 1) / kLaneRows : 1;
+    int first[kLanes] = {}, count[kLanes] = {};
+    for (int l = 0; l < parts; ++l) {
+      count[l] = b / parts + (l < b % parts ? 1 : 0);
+      first[l] = l ? first[l - 1] + count[l - 1] : 0;
+    }
     for (int l = 0; l < parts; ++l) {
       select_lane(l);
       for (int j = 0; j < count[l]; ++j) {
@@ -962,24 +1073,37 @@ struct ti_llm_model {
         h_offsets[j] = lengths[s[i]];
       }
       upload_meta(count[l], 1);
-      ck(hipMemsetAsync(lanes[l].d_run_step, 0, sizeof(uint32_t), stream));
+      embed(count[l], 1);
     }
     for (int t = 0; t < steps; ++t)
       for (int l = 0; l < parts; ++l) {
         select_lane(l);
         decode_step_graph(count[l]);
       }
+    // Lane l's ids sit at run[position][row], positions lengths .. lengths +
+    // steps - 1 of its requests.
+    int lo[kLanes] = {}, hi[kLanes] = {};
     for (int l = 0; l < parts; ++l) {
+      lo[l] = INT_MAX;
+      for (int j = 0; j < count[l]; ++j) {
+        lo[l] = std::min(lo[l], lengths[s[first[l] + j]]);
+        hi[l] = std::max(hi[l], lengths[s[first[l] + j]] + steps);
+      }
       select_lane(l);
-      ck(hipMemcpyAsync(lanes[l].h_run, lanes[l].d_run, size_t(steps) * count[l] * sizeof(int32_t),
-                        hipMemcpyDeviceToHost, stream));
+      ck(hipMemcpyAsync(lanes[l].h_run, lanes[l].d_run + size_t(lo[l]) * count[l],
+                        size_t(hi[l] - lo[l]) * count[l] * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
     }
     select_lane(0);
     for (int l = 0; l < parts; ++l) ck(hipStreamSynchronize(lanes[l].stream));
     for (int l = 0; l < parts; ++l)
-      for (int t = 0; t < steps; ++t)
-        std::copy(lanes[l].h_run + size_t(t) * count[l], lanes[l].h_run + size_t(t + 1) * count[l],
-                  tokens + size_t(t) * b + first[l]);
+      for (int j = 0; j < count[l]; ++j) {
+        const int i = first[l] + j, base = lengths[s[i]] - lo[l];
+        for (int t = 0; t < steps; ++t) {
+          const int32_t id = lanes[l].h_run[size_t(base + t) * count[l] + j];
+          if (id < 0 || id >= V) throw GpuError("greedy id outside the vocabulary (non-finite logits)");
+          tokens[size_t(t) * b + i] = id;
+        }
+      }
     for (int t = 0; t < steps; ++t) count_forward(true, true);
     for (int i = 0; i < b; ++i) lengths[s[i]] += steps;
   }
