@@ -612,6 +612,29 @@ def test_attention_prefill_many_tiles(ops, causal):
     close(h(hbits(out)), h(oracle.attention_f16(q, k, v, ql, kl, off, bool(causal))))
 
 
+@pytest.mark.parametrize("causal", [0, 1])
+def test_attention_prefill_two_query_blocks(ops, causal):
+    """At least 768 workgroups of 128 queries (4 x 12 x 16): the 4-wave kernel
+    with two 16-query blocks per wave.  Ragged lengths put a block boundary
+    inside a wave (a request of 17 queries, one of 130), a request with no
+    query, and queries past a request's length that must come out zero."""
+    t = torch()
+    rng = np.random.default_rng(31 + causal)
+    B, H, D, nq, nk = 16, 12, 64, 512, 530
+    ql = [512, 17, 130, 0, 511, 128, 1, 300, 512, 64, 96, 200, 255, 257, 33, 480]
+    kl = [530, 17, 140, 9, 520, 128, 1, 310, 512, 100, 96, 210, 255, 300, 40, 500]
+    off = [max(0, kv - qv) for qv, kv in zip(ql, kl)]
+    q = f16(rng.standard_normal((B, H, nq, D)) * 0.5)
+    k = f16(rng.standard_normal((B, H, nk, D)) * 0.5)
+    v = f16(rng.standard_normal((B, H, nk, D)))
+    say("attention prefill two query blocks", causal)
+    out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
+                        kv_lengths=kl, query_offsets=off, causal=bool(causal))
+    got = h(hbits(out))
+    close(got, h(oracle.attention_f16(q, k, v, ql, kl, off, bool(causal))))
+    assert not got[3].any() and not got[1, :, 17:].any()
+
+
 # ---------------------------------------------------------------- row ops fp16
 @pytest.mark.parametrize("cols", [1, 7, 257, 768, 3072, 5000])
 def test_layernorm_gelu_softmax_f16(ops, cols):

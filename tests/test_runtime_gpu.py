@@ -244,6 +244,22 @@ def test_prefill_and_decode_are_batch_invariant(model, others):
     model.reset_all()
 
 
+def test_long_prefill_batch_invariant(model):
+    """32 prompts of 150..255 ids prefill with two 16-query blocks per attention
+    wave (>= 512 workgroups of 128 queries), a prompt alone with one: the same
+    logits bits (a query's attention sums do not depend on the blocking)."""
+    rng = np.random.default_rng(12)
+    rows = [rng.integers(0, 50257, int(n)).tolist() for n in rng.integers(150, 256, 32)]
+    say("long prefill batch invariance")
+    model.reset_all()
+    batched = logits_of(model.forward(list(range(32)), rows))
+    for i in (0, 17, 31):
+        model.reset(33)
+        alone = logits_of(model.forward([33], [rows[i]]))[0]
+        assert np.array_equal(alone, batched[i]), f"request {i}"
+    model.reset_all()
+
+
 def first_divergence(a, b):
     for i, (x, y) in enumerate(zip(a, b)):
         if x != y:

@@ -362,25 +362,36 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
 //   P^T = exp(S^T - m) rounded to fp16: two 16-key blocks of it side by side
 //                 are exactly the B operand of
 //   O^T += V^T P^T  v_mfma_f32_16x16x32_f16, A = 16 dims x (two 4-key runs per
-//                 lane) of V^T (LDS, V is staged transposed), lane (j, g)
-//                 accumulates query j's dims 16db + 4g + v;
+//                 lane) of V^T (read from row-major V in LDS by the transposing
+//                 ds_read_b64_tr_b16), lane (j, g) accumulates query j's dims
+//                 16db + 4g + v;
 //   l   += 1 P^T  the same MFMA with an A of ones: the row sums, in every lane.
 // So a query's running max, sum and rescale stay in the four lanes (j, g) that
-// hold it (cross-lane steps only on tiles that raise the maximum).  A workgroup of 4
-// waves takes 64 queries (16 per wave) and walks 64-key tiles of K and V through
-// double-buffered LDS, stopping at the last key any of its queries may see.
-// The global loads of the next two tiles are in flight during a tile's MFMAs
-// (one tile ahead left every tile waiting a full memory round trip).  Staging
-// gives each wave instruction 64 consecutive keys of one 8-dim segment, so the
-// transposed V stores fill whole LDS rows (8 dims per lane over 8 keys made
-// them 8-way bank conflicts, two thirds of the kernel's LDS cycles).
+// hold it (cross-lane steps only on tiles that raise the maximum).  A wave
+// takes QB blocks of 16 queries; every K and V^T fragment it reads from LDS
+// feeds the MFMAs of all QB blocks (LDS reads per MFMA fall by QB: at QB = 1
+// the K and V reads of a tile take more LDS cycles than its MFMAs).  A
+// workgroup of 4 waves per key group takes 64 QB queries and walks 64-key
+// tiles of K and V through double-buffered LDS, stopping at the last key any
+// of its queries may see.  The global loads of the next two tiles are in
+// flight during a tile's MFMAs (one tile ahead left every tile waiting a full
+// memory round trip).  Staging gives each wave instruction 64 consecutive keys
+// of one 8-dim segment (16-byte K and V row stores).
 // Numerics: scores, max, sum and accumulation in fp32 (exponentials in base 2
 // of the log2(e)-scaled scores), probabilities rounded to fp16 for the PV
 // product and its row sum (numerator and denominator weigh each key alike);
-// rows with no visible key, and padded queries, are exactly zero.
-template <int D, int KS>
-__global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma_kernel(AttnParams p) {
-  constexpr int BQ = 64, BT = 64, KP = D + 8;
+// rows with no visible key, and padded queries, are exactly zero.  A query's
+// sums do not depend on QB (each block's MFMAs see the same operands in the
+// same order); they depend on KS (two key groups merge at the end).
+// Waves per SIMD the register budget is sized for (two query blocks need
+// about 1.5x the registers of one).
+constexpr int prefill_waves_per_simd(int d, int ks, int qb) {
+  return (d == 64 ? 4 : 2) / ks / qb > 0 ? (d == 64 ? 4 : 2) / ks / qb : 1;
+}
+
+template <int D, int KS, int QB = 1>
+__global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void prefill_mfma_kernel(AttnParams p) {
+  constexpr int BQ = 64 * QB, BT = 64, KP = D + 8;
   constexpr int SEGS = D / 8;                 // 16-byte pieces per key row
   constexpr int PIECES = BT * SEGS / 256;     // per thread per tile (2 or 4)
   // Dynamic LDS: [2 buffers][KS tiles] of K rows, then of V rows (row-major;
@@ -416,7 +427,6 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
   const int q_valid = max(0, min(a.q_len, a.q_lengths[b]));
   const int64_t off = a.offsets ? int64_t(a.offsets[b]) : 0;
   const int kvv = int(a.kv_from_offsets ? off + q_valid : max(0, min(a.kv_len, a.kv_lengths[b])));
-  const int my_q = q0 + 16 * qw + j;
   const int last_q = min(q0 + BQ, q_valid) - 1;
   const int key_end = last_q < q0 ? 0 : int(min<int64_t>(kvv, a.causal ? off + last_q + 1 : kvv));
   const int ntiles = (key_end + BT - 1) / BT;
@@ -424,19 +434,30 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
   const int64_t slot = a.kv_slot ? int64_t(a.kv_slot[b]) : int64_t(b);
   const uint16_t* kbase = a.k + slot * a.kv_sb + int64_t(h) * a.kv_sh;
   const uint16_t* vbase = a.v + slot * a.kv_sb + int64_t(h) * a.kv_sh;
-  // Query my_q sees keys [0, my_end); every valid query of this wave sees at
-  // least [0, my_end_min) (its first query's range), so tiles below that need no mask.
-  const int my_end = my_q < q_valid ? int(min<int64_t>(kvv, a.causal ? off + my_q + 1 : kvv)) : 0;
-  const int wq0 = q0 + 16 * qw;
-  const int my_end_min = (wq0 + 15 < q_valid) ? int(min<int64_t>(kvv, a.causal ? off + wq0 + 1 : kvv)) : 0;
+  // This wave's queries are wq0 .. wq0 + 16 QB - 1, block u holding wq0 + 16 u
+  // + j in lane (j, g).  Query my_q[u] sees keys [0, my_end[u]); every valid
+  // query of the wave sees at least [0, my_end_min) (its first query's range),
+  // so tiles below that need no mask.
+  const int wq0 = q0 + 16 * QB * qw;
+  int my_q[QB], my_end[QB];
+#pragma unroll
+  for (int u = 0; u < QB; ++u) {
+    my_q[u] = wq0 + 16 * u + j;
+    my_end[u] = my_q[u] < q_valid ? int(min<int64_t>(kvv, a.causal ? off + my_q[u] + 1 : kvv)) : 0;
+  }
+  const int my_end_min = (wq0 + 16 * QB - 1 < q_valid) ? int(min<int64_t>(kvv, a.causal ? off + wq0 + 1 : kvv)) : 0;
+  const int wave_end =
+      wq0 < q_valid ? int(min<int64_t>(kvv, a.causal ? off + min(wq0 + 16 * QB - 1, q_valid - 1) + 1 : kvv)) : 0;
 
-  half8_t qf[D / 32];
-  {
-    const uint16_t* qp = a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(min(my_q, max(q_valid, 1) - 1)) * a.q_sq;
+  half8_t qf[QB][D / 32];
+#pragma unroll
+  for (int u = 0; u < QB; ++u) {
+    const uint16_t* qp =
+        a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(min(my_q[u], max(q_valid, 1) - 1)) * a.q_sq;
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) {
-      qf[s] = *reinterpret_cast<const half8_t*>(qp + 32 * s + 8 * g);
-      if (my_q >= q_valid) qf[s] = half8_t{};
+      qf[u][s] = *reinterpret_cast<const half8_t*>(qp + 32 * s + 8 * g);
+      if (my_q[u] >= q_valid) qf[u][s] = half8_t{};
     }
   }
 
@@ -467,11 +488,16 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
     }
   };
 
-  float m = kNegInf;
-  float4_t accl = {0.f, 0.f, 0.f, 0.f};  // every entry: the running sum l of this lane's query
-  float4_t acc[D / 16];
+  float m[QB];
+  float4_t accl[QB];  // every entry: the running sum l of this lane's query
+  float4_t acc[QB][D / 16];
 #pragma unroll
-  for (int d = 0; d < D / 16; ++d) acc[d] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < QB; ++u) {
+    m[u] = kNegInf;
+    accl[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < D / 16; ++d) acc[u][d] = float4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
   // Step s (tiles s * KS + group) sits in LDS buffer s & 1; its registers were
   // set s & 1 (st0 / st1).
@@ -488,16 +514,17 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
   auto step = [&](int s_, Staged& next) {
     const int buf = s_ & 1, t = s_ * KS + grp;
     // This wave's queries see nothing of this tile: skip the math, keep the barriers.
-    const int wave_end = int(min<int64_t>(kvv, a.causal ? off + min(q0 + 16 * qw + 15, q_valid - 1) + 1 : kvv));
-    if (t < ntiles && q0 + 16 * qw < q_valid && t * BT < wave_end) {
-      float4_t sc[4];
+    if (t < ntiles && wq0 < q_valid && t * BT < wave_end) {
+      float4_t sc[QB][4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        sc[kb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < QB; ++u) sc[u][kb] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < D / 32; ++s) {
           const half8_t kf = *reinterpret_cast<const half8_t*>(&ks[buf][grp][16 * kb + j][32 * s + 8 * g]);
-          sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sc[kb], 0, 0, 0);
+#pragma unroll
+          for (int u = 0; u < QB; ++u) sc[u][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[u][s], sc[u][kb], 0, 0, 0);
         }
       }
       // Scores in base 2: x = s * D^-1/2 * log2(e), p = 2^(x - ref), the scaling
@@ -507,44 +534,13 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
       // wave-uniform test).  The reference ref is raised only when a score
       // exceeds it by more than 8 (p <= 256 stays exact enough in fp16 and the
       // sums are fp32), so acc and l are rescaled on few tiles, not every tile;
-      // a lane's own maximum decides whether any query of the wave may raise,
+      // a lane's own maximum decides whether any query of the block may raise,
       // and only then are the four lanes of each query reduced.
-      const float l2s = p.scale * 1.4426950408889634f;
-      float tmax = kNegInf;
-      if (t * BT + BT <= my_end_min) {
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[kb][v]);
-      } else {
-        const int lim = my_end - t * BT - 4 * g;  // key 16 kb + v of this lane is visible iff < lim
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            sc[kb][v] = 16 * kb + v < lim ? sc[kb][v] : kNegInf;
-            tmax = fmaxf(tmax, sc[kb][v]);
-          }
-      }
-      if (__ballot(tmax * l2s > m + 8.f)) {
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * l2s;
-        const bool raise = tmax > m + 8.f;
-        const float nref = raise ? tmax : m;
-        const float alpha = accl[0] == 0.f ? 0.f : __builtin_amdgcn_exp2f(m - nref);
-        accl[0] *= alpha;
-#pragma unroll
-        for (int d = 0; d < D / 16; ++d) acc[d] *= alpha;
-        m = nref;
-      }
-      const float base = m == kNegInf ? 0.f : m;  // -inf only while every key so far is masked
       // P^T as two B operands of v_mfma_f32_16x16x32_f16: pair c holds, in
       // lane (j, g), the probabilities of keys 32c + 4g + v and 32c + 16 + 4g + v
       // (v < 4), and the A operand (V^T) takes the same two 4-key runs of each
       // dim row.  A third A operand of ones gives every lane the row sum
       // l = sum of the fp16 probabilities, in fp32, with no cross-lane step.
-      // V^T fragments of a key pair: the first pair's LDS reads complete while
-      // the exponentials run, the second's during the first pair's MFMAs.
       // ds_read_b64_tr_b16 on 16-lane groups: value k of lane r comes from the
       // address of lane 4k + r/4 of its group, element r % 4.  Lane (j, g)
       // therefore points at row 4g + j/4 (+ 32c, + 16 for the second run),
@@ -562,22 +558,60 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
           vf[d] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
       };
+      // The first key pair's V^T fragments are read while the exponentials run,
+      // the second's during the first pair's MFMAs.
       half8_t vf[D / 16];
       vfrag(vf, 0);
-      half8_t pp[2];
+      const float l2s = p.scale * 1.4426950408889634f;
+      const bool full = t * BT + BT <= my_end_min;
+      half8_t pp[QB][2];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int u = 0; u < QB; ++u) {
+        float tmax = kNegInf;
+        if (full) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-          pp[kb >> 1][4 * (kb & 1) + v] = f16r(__builtin_amdgcn_exp2f(fmaf(sc[kb][v], l2s, -base)));
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sc[u][kb][v]);
+        } else {
+          const int lim = my_end[u] - t * BT - 4 * g;  // key 16 kb + v of this lane is visible iff < lim
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              sc[u][kb][v] = 16 * kb + v < lim ? sc[u][kb][v] : kNegInf;
+              tmax = fmaxf(tmax, sc[u][kb][v]);
+            }
+        }
+        if (__ballot(tmax * l2s > m[u] + 8.f)) {
+          tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+          tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * l2s;
+          const bool raise = tmax > m[u] + 8.f;
+          const float nref = raise ? tmax : m[u];
+          const float alpha = accl[u][0] == 0.f ? 0.f : __builtin_amdgcn_exp2f(m[u] - nref);
+          accl[u][0] *= alpha;
+#pragma unroll
+          for (int d = 0; d < D / 16; ++d) acc[u][d] *= alpha;
+          m[u] = nref;
+        }
+        const float base = m[u] == kNegInf ? 0.f : m[u];  // -inf only while every key so far is masked
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            pp[u][kb >> 1][4 * (kb & 1) + v] = f16r(__builtin_amdgcn_exp2f(fmaf(sc[u][kb][v], l2s, -base)));
+      }
       const half8_t ones = {f16(1.f), f16(1.f), f16(1.f), f16(1.f), f16(1.f), f16(1.f), f16(1.f), f16(1.f)};
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         half8_t vn[D / 16];
         if (c == 0) vfrag(vn, 1);
 #pragma unroll
-        for (int d = 0; d < D / 16; ++d) acc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[d], pp[c], acc[d], 0, 0, 0);
-        accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pp[c], accl, 0, 0, 0);
+        for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+          for (int u = 0; u < QB; ++u) acc[u][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[d], pp[u][c], acc[u][d], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < QB; ++u) accl[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pp[u][c], accl[u], 0, 0, 0);
         if (c == 0) {
 #pragma unroll
           for (int d = 0; d < D / 16; ++d) vf[d] = vn[d];
@@ -593,44 +627,68 @@ __global__ __launch_bounds__(256 * KS, (D == 64 ? 4 : 2) / KS) void prefill_mfma
     if (s_ + 1 < nsteps) step(s_ + 1, st0);
   }
   if constexpr (KS == 2) {
-    // Group 1 hands its (m, l, acc) per lane to group 0 through LDS (free after
-    // the last barrier); group 0 merges on the larger reference: the states
-    // are sums of 2^(x - m).
+    // Group 1 hands its (m, l, acc) per lane and block to group 0 through LDS
+    // (free after the last barrier); group 0 merges on the larger reference:
+    // the states are sums of 2^(x - m).
     constexpr int PER = D / 16 * 4 + 2;
-    float* xs = reinterpret_cast<float*>(lds_raw) + (qw * 64 + lane) * PER;
+    float* xs = reinterpret_cast<float*>(lds_raw) + (qw * 64 + lane) * PER * QB;
     if (grp == 1) {
 #pragma unroll
-      for (int d = 0; d < D / 16; ++d)
+      for (int u = 0; u < QB; ++u) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) xs[4 * d + v] = acc[d][v];
-      xs[PER - 2] = m;
-      xs[PER - 1] = accl[0];
+        for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) xs[u * PER + 4 * d + v] = acc[u][d][v];
+        xs[u * PER + PER - 2] = m[u];
+        xs[u * PER + PER - 1] = accl[u][0];
+      }
     }
     __syncthreads();
     if (grp == 1) return;
-    const float l = accl[0];
-    const float m1 = xs[PER - 2], l1 = xs[PER - 1];
-    const float nm = fmaxf(l > 0.f ? m : kNegInf, l1 > 0.f ? m1 : kNegInf);
-    const float f0 = l > 0.f ? __builtin_amdgcn_exp2f(m - nm) : 0.f;
-    const float f1 = l1 > 0.f ? __builtin_amdgcn_exp2f(m1 - nm) : 0.f;
-    accl[0] = l * f0 + l1 * f1;
 #pragma unroll
-    for (int d = 0; d < D / 16; ++d)
+    for (int u = 0; u < QB; ++u) {
+      const float l = accl[u][0];
+      const float m1 = xs[u * PER + PER - 2], l1 = xs[u * PER + PER - 1];
+      const float nm = fmaxf(l > 0.f ? m[u] : kNegInf, l1 > 0.f ? m1 : kNegInf);
+      const float f0 = l > 0.f ? __builtin_amdgcn_exp2f(m[u] - nm) : 0.f;
+      const float f1 = l1 > 0.f ? __builtin_amdgcn_exp2f(m1 - nm) : 0.f;
+      // Explicit fmas: with contraction left to the compiler, a * f0 + b * f1
+      // may fuse either product, and differently per instantiation (the bits
+      // of a query would then depend on QB).
+      accl[u][0] = fmaf(l1, f1, l * f0);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[d][v] = acc[d][v] * f0 + xs[4 * d + v] * f1;
+      for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[u][d][v] = fmaf(xs[u * PER + 4 * d + v], f1, acc[u][d][v] * f0);
+    }
   }
 
-  if (my_q >= a.q_len) return;
-  const float l = accl[0];
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(my_q) * a.o_sq;
 #pragma unroll
-  for (int d = 0; d < D / 16; ++d) {
-    half4_t o;
+  for (int u = 0; u < QB; ++u) {
+    if (my_q[u] >= a.q_len) continue;
+    const float l = accl[u][0];
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(my_q[u]) * a.o_sq;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) o[v] = f16r(l > 0.f ? acc[d][v] * inv : 0.f);
-    *reinterpret_cast<half4_t*>(op + 16 * d + 4 * g) = o;
+    for (int d = 0; d < D / 16; ++d) {
+      half4_t o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = f16r(l > 0.f ? acc[u][d][v] * inv : 0.f);
+      *reinterpret_cast<half4_t*>(op + 16 * d + 4 * g) = o;
+    }
   }
+}
+
+// K and V rows, two buffers per key group; the KS = 2 merge reuses them.
+template <int D, int KS, int QB>
+hipError_t launch_prefill(dim3 grid, const AttnParams& p, hipStream_t stream) {
+  constexpr size_t lds = size_t(KS) * 2 * 2 * 64 * (D + 8) * 2;
+  static_assert(KS == 1 || size_t(256) * (D / 16 * 4 + 2) * QB * 4 <= lds, "merge fits the tile buffers");
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, KS, QB>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((prefill_mfma_kernel<D, KS, QB>), grid, dim3(256 * KS), lds, stream, p);
+  return hipGetLastError();
 }
 
 template <int D, bool VEC>
@@ -680,27 +738,26 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
     if (a.qkv_partials) return hipErrorInvalidValue;
     dim3 grid = blocks_per;
     if constexpr (VEC) {
-      grid.x = unsigned((a.q_len + 63) / 64);
-      // Few query tiles (<= 512 workgroups, e.g. one long sequence of a few
-      // heads): 8 waves per tile in two key groups, so each SIMD holds two waves
-      // (causal B1 H4 4096^2: 75 -> 54 us, B1 H12 2048^2: 54 -> 48 us); from
-      // 768 workgroups the 4-wave kernel is as fast or faster (B8 H12 512^2:
-      // 26 against 28 us, B32 H25 320^2: 55 against 65 us).
+      // Few query tiles (<= 512 workgroups of 64 queries, e.g. one long
+      // sequence of a few heads): 8 waves per tile in two key groups, so each
+      // SIMD holds two waves (causal B1 H4 4096^2: 75 -> 54 us, B1 H12 2048^2:
+      // 54 -> 48 us); from 768 workgroups the 4-wave kernel is as fast or
+      // faster (B8 H12 512^2: 26 against 28 us, B32 H25 320^2: 55 against 65 us).
       // batch_invariant (the runtime's prefill) always takes the key-split
-      // kernel, so a query's sums never depend on the grid.
-      const int64_t wgs = int64_t(grid.x) * grid.y * grid.z;
-      constexpr size_t lds1 = 2 * 2 * 64 * (D + 8) * 2;  // K and V rows, two buffers
-      if (wgs <= 512 || a.batch_invariant) {
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, 2>),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(2 * lds1));
-        if (attr != hipSuccess) return attr;
-        hipLaunchKernelGGL((prefill_mfma_kernel<D, 2>), grid, dim3(512), 2 * lds1, stream, p);
-      } else {
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, 1>),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds1));
-        if (attr != hipSuccess) return attr;
-        hipLaunchKernelGGL((prefill_mfma_kernel<D, 1>), grid, dim3(256), lds1, stream, p);
+      // kernel, so a query's sums never depend on the grid.  64-dim heads take
+      // two 16-query blocks per wave (128 queries per workgroup) once that
+      // still leaves enough workgroups (at 128 dims the second block's
+      // registers spill).
+      const int64_t heads_rows = int64_t(grid.y) * grid.z;
+      const int64_t wgs = (a.q_len + 63) / 64 * heads_rows, wgs2 = (a.q_len + 127) / 128 * heads_rows;
+      const bool split_keys = wgs <= 512 || a.batch_invariant;
+      const bool two_blocks = D == 64 && (split_keys ? wgs2 >= 512 : wgs2 >= 768);
+      grid.x = unsigned(two_blocks ? (a.q_len + 127) / 128 : (a.q_len + 63) / 64);
+      if constexpr (D == 64) {
+        if (two_blocks)
+          return split_keys ? launch_prefill<D, 2, 2>(grid, p, stream) : launch_prefill<D, 1, 2>(grid, p, stream);
       }
+      return split_keys ? launch_prefill<D, 2, 1>(grid, p, stream) : launch_prefill<D, 1, 1>(grid, p, stream);
     } else {
       grid.x = unsigned((a.q_len + 3) / 4);
       hipLaunchKernelGGL((attention_kernel<D, 4, 1, VEC>), grid, dim3(256), 0, stream, p);
