@@ -375,8 +375,12 @@ __global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
 // tiles of K and V through double-buffered LDS, stopping at the last key any
 // of its queries may see.  The global loads of the next two tiles are in
 // flight during a tile's MFMAs (one tile ahead left every tile waiting a full
-// memory round trip).  Staging gives each wave instruction 64 consecutive keys
-// of one 8-dim segment (16-byte K and V row stores).
+// memory round trip).  Staging gives each group of 8 lanes one whole key row
+// (1 KiB contiguous per wave instruction, conflict-free 16-byte LDS stores).
+// K and V rows sit at a pitch of D + 16 halves: measured on gfx950 with
+// SQ_LDS_BANK_CONFLICT, the K fragment reads and the transposing V reads are
+// conflict-free at D + 16 (64: 80, 128: 144) and conflict on 2/3 to 2x of
+// their cycles at D + 8 (and at 160 for D = 128).
 // Numerics: scores, max, sum and accumulation in fp32 (exponentials in base 2
 // of the log2(e)-scaled scores), probabilities rounded to fp16 for the PV
 // product and its row sum (numerator and denominator weigh each key alike);
@@ -391,14 +395,14 @@ constexpr int prefill_waves_per_simd(int d, int ks, int qb) {
 
 template <int D, int KS, int QB = 1>
 __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void prefill_mfma_kernel(AttnParams p) {
-  constexpr int BQ = 64 * QB, BT = 64, KP = D + 8;
+  constexpr int BQ = 64 * QB, BT = 64, KPK = D + 16, KPV = D + 16;
   constexpr int SEGS = D / 8;                 // 16-byte pieces per key row
   constexpr int PIECES = BT * SEGS / 256;     // per thread per tile (2 or 4)
   // Dynamic LDS: [2 buffers][KS tiles] of K rows, then of V rows (row-major;
   // the PV operand is read transposed by ds_read_b64_tr_b16).
   extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
-  auto ks = reinterpret_cast<f16(*)[KS][BT][KP]>(lds_raw);
-  auto vs = reinterpret_cast<f16(*)[KS][BT][KP]>(lds_raw + 2 * KS * BT * KP * sizeof(f16));
+  auto ks = reinterpret_cast<f16(*)[KS][BT][KPK]>(lds_raw);
+  auto vs = reinterpret_cast<f16(*)[KS][BT][KPV]>(lds_raw + 2 * KS * BT * KPK * sizeof(f16));
   const AttnArgs& a = p.a;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // KS = 2: waves 4..7 are a second key group taking the odd tiles of each
@@ -462,9 +466,9 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   }
 
   // Cooperative tile staging: each group of 256 threads stages its tile of a
-  // step; piece r of group thread t is key (t + 256 r) % BT (the lane), 8 dims
-  // at ((t + 256 r) / BT) * 8 (uniform in a wave); keys past key_end re-read
-  // key_end - 1.  Two register sets hold the next two steps.
+  // step; piece r of group thread t is key (t + 256 r) / SEGS, 8 dims at
+  // ((t + 256 r) % SEGS) * 8; keys past key_end re-read key_end - 1.  Two
+  // register sets hold the next two steps.
   struct Staged {
     half8_t k[PIECES], v[PIECES];
   };
@@ -473,7 +477,7 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
     const int t = step * KS + grp;
 #pragma unroll
     for (int r = 0; r < PIECES; ++r) {
-      const int piece = gt + 256 * r, key = piece % BT, seg = piece / BT;
+      const int piece = gt + 256 * r, key = piece / SEGS, seg = piece % SEGS;
       const int64_t kk = min(t * BT + key, key_end - 1);
       r_.k[r] = *reinterpret_cast<const half8_t*>(kbase + kk * D + 8 * seg);
       r_.v[r] = *reinterpret_cast<const half8_t*>(vbase + kk * D + 8 * seg);
@@ -482,7 +486,7 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   auto store_tile = [&](const Staged& r_, int buf) {
 #pragma unroll
     for (int r = 0; r < PIECES; ++r) {
-      const int piece = gt + 256 * r, key = piece % BT, seg = piece / BT;
+      const int piece = gt + 256 * r, key = piece / SEGS, seg = piece % SEGS;
       *reinterpret_cast<half8_t*>(&ks[buf][grp][key][8 * seg]) = r_.k[r];
       *reinterpret_cast<half8_t*>(&vs[buf][grp][key][8 * seg]) = r_.v[r];
     }
@@ -554,7 +558,7 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
           const f16* vrow = &vs[buf][grp][32 * c + 4 * g + (j >> 2)][16 * d + 4 * (j & 3)];
           const half4_t lo = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_vec*)(vrow)));
           const half4_t hi =
-              __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_vec*)(vrow + 16 * KP)));
+              __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_vec*)(vrow + 16 * KPV)));
           vf[d] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
       };
@@ -679,10 +683,11 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   }
 }
 
-// K and V rows, two buffers per key group; the KS = 2 merge reuses them.
+// K and V rows (pitch D + 16), two buffers per key group; the KS = 2 merge
+// reuses them.
 template <int D, int KS, int QB>
 hipError_t launch_prefill(dim3 grid, const AttnParams& p, hipStream_t stream) {
-  constexpr size_t lds = size_t(KS) * 2 * 2 * 64 * (D + 8) * 2;
+  constexpr size_t lds = size_t(KS) * 2 * 2 * 64 * (D + 16) * 2;
   static_assert(KS == 1 || size_t(256) * (D / 16 * 4 + 2) * QB * 4 <= lds, "merge fits the tile buffers");
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, KS, QB>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
