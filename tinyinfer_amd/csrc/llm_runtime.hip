@@ -22,17 +22,18 @@
 //    batch size into a hipGraph whose kernels read all lengths, offsets and slots
 //    from device memory, so later steps are one graph launch between a pinned
 //    H2D copy of the step metadata and a D2H copy of the next tokens;
-//  * the captured step ends with a feed kernel (its greedy ids become the next
-//    step's input ids, positions advance by one), so ti_llm_greedy_batch queues
-//    each run of decode steps over an unchanged set of requests back to back,
-//    records every step's ids on the device, and waits once per run;
-//  * such a run of more than kLaneRows requests splits evenly over lanes of at
-//    most kLaneRows, each with its own stream, activations, scratch and
-//    captured graph over the shared weights and KV cache, queued side by side:
-//    one lane's chain of 64 dependent launches leaves most CUs idle, and
-//    free-running chains fill them.  A request's logits are the same bits in
-//    any lane, since the decode kernels sum every row in one K order at every
-//    batch size.
+//  * the captured step ends with greedy_feed_kernel (each greedy id is
+//    recorded, becomes the next step's input with its embedding and ln_1
+//    written, positions advance by one), so ti_llm_greedy_batch queues each
+//    run of decode steps over an unchanged set of requests back to back and
+//    waits once per run;
+//  * such a run of more than kLaneRows requests, over int8 weights that fit
+//    the Infinity Cache, splits evenly over lanes of at most kLaneRows, each
+//    with its own stream, activations, scratch and captured graph over the
+//    shared weights and KV cache, queued side by side: one lane's chain of 63
+//    dependent launches leaves most CUs idle, and free-running chains fill
+//    them.  A request's logits are the same bits in any lane, since the
+//    decode kernels sum every row in one K order at every batch size.
 #include <algorithm>
 #include <chrono>
 #include <climits>
@@ -64,6 +65,11 @@ constexpr int kHeadDim = 64;
 constexpr int kResidualSplitWorkgroups = 192;
 // Decode steps of more than this many requests run as two concurrent lanes.
 constexpr int kLanes = 2, kLaneRows = 16;
+// Lanes pay when the second lane finds the weight records the first just read
+// in cache: the decode's int8 weights must fit the 256 MiB Infinity Cache
+// (GPT-2 small, 124 MB: b = 32 102 K tok/s with two lanes against 90 K with
+// one; GPT-2 XL, 1.6 GB: 11.1 K with two against 11.8 K with one).
+constexpr size_t kLaneWeightBytes = size_t(256) << 20;
 static_assert(kLanes * kLaneRows >= 32, "the lanes must hold a full decode batch");
 
 struct GpuError : std::runtime_error {
@@ -639,7 +645,10 @@ struct ti_llm_model {
     // Lanes 1.. (decode runs of more than kLaneRows requests over the packed
     // INT8 weights): own stream, 32-row activations, metadata, head outputs
     // and scratch.
-    if (opt.max_batch > kLaneRows && quantized && head.packed && H % 64 == 0)
+    size_t decode_weights = size_t(head.k) * size_t(head.n);
+    for (const auto* ls : {&c_attn, &c_proj, &c_fc, &c_proj2})
+      for (const Linear& w : *ls) decode_weights += size_t(w.k) * size_t(w.n);
+    if (opt.max_batch > kLaneRows && quantized && head.packed && H % 64 == 0 && decode_weights <= kLaneWeightBytes)
       lane_count = std::min(kLanes, (opt.max_batch + kLaneRows - 1) / kLaneRows);
     for (int i = 1; i < lane_count; ++i) {
       Lane& l = lanes[i];
