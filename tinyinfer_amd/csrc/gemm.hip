@@ -1602,7 +1602,14 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
 // (Tiles of 128 x 64 and 128 x 128 halve the LDS bytes and dequant work per
 // MFMA, but hold one or two 4-wave workgroups per CU and measured 1.3-2x slower
 // from M = 512 to 8192; the 64 x 64 tile keeps three per CU.)
+// 64 x 64 tiles; a shape that would split K over fewer than 192 of them but
+// has 192 tiles of 32 x 64 takes those unsplit instead (no fp32 partials:
+// M = 512, 3072 -> 768 moved 2.85x its algorithmic bytes as three K splits;
+// 23.5 -> 21.2 us).  The canonical (batch-invariant) route keeps 64-row tiles.
 hipError_t launch_panel(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
+  const int64_t tiles64 = int64_t((g.m + 63) / 64) * ((g.n + 63) / 64);
+  const int64_t tiles32 = int64_t((g.m + 31) / 32) * ((g.n + 63) / 64);
+  if (!g.canonical && tiles64 < 192 && tiles32 >= 192) return launch_panel_cfg<1, 4, 2, 1, 4>(g, s, stream, deferred);
   return launch_panel_cfg<1, 4, 4, 1, 4>(g, s, stream, deferred);
 }
 
