@@ -267,6 +267,30 @@ def first_divergence(a, b):
     return None if len(a) == len(b) else min(len(a), len(b))
 
 
+@pytest.mark.parametrize("batch", [17, 31])
+def test_greedy_runs_and_lanes_match_alone(model, batch):
+    """ti_llm_greedy_batch decodes in runs (each run advances every unfinished
+    request by the fewest tokens any still needs) and splits a run of more than
+    16 requests into two lanes: with ragged prompt lengths and token counts the
+    active set shrinks run by run and the lanes split unevenly (9 + 8, 16 + 15,
+    then smaller), yet every request's tokens, output lengths and timings
+    match the request decoded alone."""
+    rng = np.random.default_rng(batch)
+    prompts = [rng.integers(0, 50257, int(n)).tolist() for n in rng.integers(1, 40, batch)]
+    counts = [int(c) for c in rng.integers(1, 48, batch)]
+    counts[0], counts[-1] = 47, 1
+    say("greedy runs and lanes, batch", batch)
+    model.reset_all()
+    res = model.greedy(prompts, counts)
+    assert res["output_lengths"] == counts
+    assert all(0 < f <= t for f, t in zip(res["ttft_ms"], res["total_ms"]))
+    for i in (0, 1, batch // 2, batch - 1):
+        model.reset_all()
+        alone = model.greedy([prompts[i]], counts[i], slots=[33])
+        assert alone["tokens"][0] == res["tokens"][i], f"request {i}"
+    model.reset_all()
+
+
 @pytest.mark.parametrize("batch", [1, 32])
 def test_greedy_tokens_match_oracle(model, cpu_model, batch):
     """32 seeded uniform prompt ids per request, 64 greedy tokens."""
