@@ -387,7 +387,7 @@ __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scal
 // fragments before the MFMAs; the launch then covers K in one round of one
 // split (W * CPW >= kc).  PA: A is P32 fragment-packed (each A fragment one
 // contiguous KiB).
-template <int MT, int W, int CPW, int CBG, bool LNA = false, bool PA = false>
+template <int MT, int W, int CPW, int CBG, bool LNA = false, bool PA = false, bool CW = false>
 __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   __shared__ float red[W][CBG][MT * 256];
   __shared__ float stat[LNA ? W : 1][MT * 16];  // per-wave LayerNorm partial sums
@@ -463,13 +463,17 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     u32x4_t wf[CPW][CBG];
     half8_t af[CPW][2][MT];
     half8_t gbv;
-    // Plain (cached) loads: two decode lanes stream the same records
-    // microseconds apart, and the second finds them in cache (b = 32 decode as
-    // two 16-row lanes: 102 K against 92 K tok/s with nontemporal loads).
+    // CW: cached loads, for two decode lanes that stream the same records
+    // microseconds apart, the second finding them in cache (b = 32 decode as
+    // two 16-row lanes: 102 K against 92 K tok/s with nontemporal loads);
+    // otherwise the records stream past the caches (GPT-2 XL decode, whose
+    // 1.6 GB do not stay cached: 12.06 K against 11.81 K tok/s with cached
+    // loads).
     auto load_w = [&](int i) {
       const int c = min(c0 + i * W, c_end - 1);
 #pragma unroll
-      for (int r = 0; r < CBG; ++r) wf[i][r] = wb[r][int64_t(c) * 64];
+      for (int r = 0; r < CBG; ++r)
+        wf[i][r] = CW ? wb[r][int64_t(c) * 64] : __builtin_nontemporal_load(wb[r] + int64_t(c) * 64);
     };
     auto load_a = [&](int i) {
       const int c = min(c0 + i * W, c_end - 1);
@@ -784,7 +788,7 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
   auto load = [&](Block& b, int i) {
     const int cb = min(cb_first + W * i, p.nb - 1), col = min(cb * 16 + j, p.n - 1);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) b.w[c] = p.w[(int64_t(cb) * KC + c) * 64 + lane];  // cached, as the packed GEMV
+    for (int c = 0; c < KC; ++c) b.w[c] = __builtin_nontemporal_load(p.w + (int64_t(cb) * KC + c) * 64 + lane);
     b.scale = p.scales[col];
     b.bias = bsrc[has_bias ? col : 0];
   };
@@ -1412,11 +1416,11 @@ GemvShape gemv_shape(int mt, int chunks, bool one_round, int nb) {
   return s;
 }
 
-template <int MT, bool LNA, bool PA>
+template <int MT, bool LNA, bool PA, bool CW = false>
 hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipStream_t st) {
 #define TIA_GEMV(W_, C_, B_)                                                                            \
   if (sh.w == W_ && sh.cpw == C_ && sh.cbg == B_) {                                                     \
-    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA, PA>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
+    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA, PA, CW>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
     return hipGetLastError();                                                                           \
   }
   TIA_GEMV(4, 3, 1)
@@ -1543,9 +1547,20 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
     p.amax_i = g.amax_i;
     *g.amax_groups = grid;
   }
-  if (g.a_p32)
+  if (g.a_p32) {
+    if constexpr (MT == 1) {
+      if (g.weights_shared)
+        return ln ? launch_gemv_shape<MT, true, true, true>(p, sh, grid, stream)
+                  : launch_gemv_shape<MT, false, true, true>(p, sh, grid, stream);
+    }
     return ln ? launch_gemv_shape<MT, true, true>(p, sh, grid, stream)
               : launch_gemv_shape<MT, false, true>(p, sh, grid, stream);
+  }
+  if constexpr (MT == 1) {
+    if (g.weights_shared)
+      return ln ? launch_gemv_shape<MT, true, false, true>(p, sh, grid, stream)
+                : launch_gemv_shape<MT, false, false, true>(p, sh, grid, stream);
+  }
   return ln ? launch_gemv_shape<MT, true, false>(p, sh, grid, stream)
             : launch_gemv_shape<MT, false, false>(p, sh, grid, stream);
 }

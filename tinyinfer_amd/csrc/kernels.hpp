@@ -90,6 +90,10 @@ struct GemmArgs {
   // family and K split are the same for every M up to 16, so a row's sums do
   // not depend on the batch (the single-row part-block GEMV is not used).
   bool decode_batches = false;
+  // Another decode lane reads the same packed weights right after this launch
+  // (the runtime's two-lane decode over cache-resident weights): the GEMV of
+  // up to 16 rows reads them with cached loads instead of streaming them.
+  bool weights_shared = false;
   // A deferred launch over packed weights splits K towards this many
   // workgroups (at least 4 K chunks per split, partials within the scratch).
   // The split count depends on the shape only, never on M.

@@ -710,6 +710,7 @@ struct ti_llm_model {
     g.epi = epi;
     g.canonical = prefill_pass;
     g.decode_batches = !prefill_pass;
+    g.weights_shared = !prefill_pass && lane_count > 1;  // two lanes stream the same records
     g.defer_workgroups = defer_workgroups;
     ck(tia::gemm(g, &scratch, stream, deferred));
   }
