@@ -28,6 +28,7 @@
 // Dequantisation mirrors reference kernels/src/cuda/tc/gemm.cu:21,24 and the
 // bias epilogue mirrors gemm.cu:73-80 / :118-124; accumulation is fp32.
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <map>
 #include <mutex>
@@ -38,6 +39,14 @@
 
 namespace tia {
 namespace {
+
+// A 16-bit load from global memory through a pointer the compiler cannot
+// place (a select of two kernel-argument pointers): typed as global, it is a
+// global_load, not a flat one, so later waits count it exactly (a pending flat
+// load makes the next wait for any load wait for every load).
+__device__ __forceinline__ uint16_t ldg_u16(const uint16_t* ptr) {
+  return *(const uint16_t __attribute__((address_space(1)))*)ptr;
+}
 
 __device__ __forceinline__ float epilogue_bias(const Epilogue& e, int n) {
   return e.bias ? h2f(e.bias[n]) : 0.f;
@@ -425,7 +434,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     colmask[r] = (cb0 + r < p.nb && col < p.n) ? 1.f : 0.f;
     // Every output this thread finishes in block r is in column (cb0 + r) * 16 +
     // (threadIdx.x & 15): its bias is fetched now, not after the reduction.
-    bias_raw[r] = bsrc[has_bias ? min((cb0 + r) * 16 + int(threadIdx.x & 15), p.n - 1) : 0];
+    bias_raw[r] = ldg_u16(bsrc + (has_bias ? min((cb0 + r) * 16 + int(threadIdx.x & 15), p.n - 1) : 0));
   }
   const uint16_t* arow[MT];
 #pragma unroll
@@ -449,7 +458,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
     const int o = threadIdx.x + it * W * 64, r = o / per_block, rem = o - r * per_block;
     const int n = (cb0 + r) * 16 + (rem & 15);
     const bool ok = has_res && o < CBG * per_block && cb0 + r < p.nb && n < p.n;
-    res_raw[it] = rsrc[ok ? r_off(p.epi, rem >> 4, n) : 0];
+    res_raw[it] = ldg_u16(rsrc + (ok ? r_off(p.epi, rem >> 4, n) : 0));
   }
 
   float4_t acc[MT][CBG];
@@ -735,142 +744,148 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide decode GEMV (the LM head): M <= 32 rows of P32 activations against many
-// 16-column blocks.  The whole A (KC <= 16 chunks) is copied to LDS once per
-// workgroup and each of its W >= 8 waves streams whole column blocks (every K
-// chunk of a block in one round of loads; the waves of a CU overlap each
-// other's rounds).  A wave owns its blocks over the full K, so the
-// accumulators go straight to the epilogue (no reduction across waves), which
-// also keeps each row's running argmax for greedy decoding.  The split-K GEMV
-// instead re-reads all of A for every one or two column blocks (1571
-// workgroups x 48 KiB for the 38.6 MB GPT-2 head at M = 32).
+// Wide decode GEMV (the LM head): 17..32 rows against many 16-column blocks.
+// One workgroup per CU over per = ceil(blocks / CUs) <= 16 consecutive column
+// blocks (no CU takes a second turn), one block per wave over the full K, so
+// the accumulators go straight to the epilogue (no reduction across waves)
+// and A is read once per workgroup (the split-K GEMV re-reads all of A for
+// every one or two column blocks: 1571 workgroups x 48 KiB for the 38.6 MB
+// GPT-2 head at M = 32).  A wave issues its share of the A copy, then its
+// block's scale, bias and K chunks in K order (scheduling barriers hold the
+// order: loads return in issue order and a wait names a count, not a load),
+// so A lands first and goes to LDS while the weights stream, and chunk c is
+// multiplied as soon as it has arrived.  EK is the epilogue kind.
 struct WideParams {
   const uint16_t* a;    // P32 fragment-packed [32][K], or row-major [M][lda] (AP32 false)
   int64_t lda;
   const u32x4_t* w;     // panel-packed records
   const float* scales;  // fp32 [N]
-  int m, n, nb, per;    // rows, columns, column blocks, blocks per workgroup
+  int m, n, nb, per;    // rows, columns, column blocks, blocks (waves) per workgroup
   Epilogue epi;
   float* amax_v;        // when set: per (workgroup, row) best logit and its column
   int32_t* amax_i;
 };
 
-template <int MT, int KC, int W, bool AP32>
-__global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
+constexpr int kWideWaves = 16, kWideMinWaves = 8;
+
+template <int MT, int KC, int EK, bool AP32>
+__global__ __launch_bounds__(kWideWaves * 64) void gemv_wide_kernel(WideParams p) {
+  constexpr int W = kWideWaves;
   // A as MFMA fragments ((c * MT + t) * 2 + s) * 64 + lane: rows 16t + (lane & 15),
   // columns 64c + 32s + 8 (lane >> 4) .. + 7 (for MT = 2, the P32 layout).
-  __shared__ half8_t a_lds[KC * MT * 2 * 64];
+  constexpr int kFrags = KC * MT * 2 * 64, kACopy = (kFrags + kWideMinWaves * 64 - 1) / (kWideMinWaves * 64);
+  static_assert(AP32 ? MT == 2 : true, "P32 A holds 32 rows");
+  const int nt = blockDim.x;  // p.per waves, kWideMinWaves <= p.per <= W
+  __shared__ half8_t a_lds[kFrags];
+  __shared__ float sv[W][32];
+  __shared__ int si[W][32];
+  using gu16 = const uint16_t __attribute__((address_space(1)))*;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
-  static_assert((KC * MT * 2 * 64) % (W * 64) == 0, "A copy must divide evenly");
-  static_assert(W >= 8, "the blocks of a wave are not overlapped: at least 8 waves per workgroup");
-  static_assert(AP32 ? MT == 2 : true, "P32 A holds 32 rows");
-  constexpr int kACopy = KC * MT * 2 * 64 / (W * 64);
-  const int cb_first = blockIdx.x * p.per + wave, cb_end = min(p.nb, (blockIdx.x + 1) * p.per);
-  const int count = cb_first < cb_end ? (cb_end - cb_first + W - 1) / W : 0;  // this wave's blocks
-  const bool has_bias = p.epi.kind != EPI_RAW_F32 && p.epi.bias;
-  // Running argmax of this lane's column over its rows 16t + 4g + v (columns
-  // arrive in increasing order, so a tie keeps the first).
-  float bv[MT * 4];
-  int bi[MT * 4];
-#pragma unroll
-  for (int r = 0; r < MT * 4; ++r) {
-    bv[r] = -__builtin_huge_valf();
-    bi[r] = INT_MAX;
-  }
-  const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
+  const int cb = blockIdx.x * p.per + wave;
+  // The last workgroup's waves past the last block load that block again
+  // (the second request finds the first's lines); their sums are never stored.
+  const int cbl = min(cb, p.nb - 1), col = cb * 16 + j, colc = min(cbl * 16 + j, p.n - 1);
+  const bool active = cb < p.nb;
+  const bool has_bias = EK != EPI_RAW_F32 && p.epi.bias;
 
-  struct Block {
-    u32x4_t w[KC];
-    float scale;
-    uint16_t bias;
-  };
-  auto load = [&](Block& b, int i) {
-    const int cb = min(cb_first + W * i, p.nb - 1), col = min(cb * 16 + j, p.n - 1);
+  half8_t ar[kACopy];
 #pragma unroll
-    for (int c = 0; c < KC; ++c) b.w[c] = __builtin_nontemporal_load(p.w + (int64_t(cb) * KC + c) * 64 + lane);
-    b.scale = p.scales[col];
-    b.bias = bsrc[has_bias ? col : 0];
-  };
-  auto compute = [&](const Block& b, int i) {
-    // Four sums, chunk c into sum c % 4, added in that order at the end: the
-    // K order of the 4-wave packed GEMV over the same KC (wave w takes chunks
-    // w, w + 4, ...; the waves are added in order), which serves 1..16 rows,
-    // so a row's logits do not depend on the batch size.
-    float4_t acc[4][MT];
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) acc[q][t] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const half8_t b0 = dequant8(b.w[c][0], b.w[c][1], b.scale);
-      const half8_t b1 = dequant8(b.w[c][2], b.w[c][3], b.scale);
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        float4_t& ac = acc[c % 4][t];
-        ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * MT + t) * 2) * 64 + lane], b0, ac, 0, 0, 0);
-        ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * MT + t) * 2 + 1) * 64 + lane], b1, ac, 0, 0, 0);
-      }
-      // One chunk's LDS reads and dequantisation at a time (hoisting all of
-      // them would hold every A fragment of the block in registers).
-      __builtin_amdgcn_sched_barrier(0);
+  for (int i = 0; i < kACopy; ++i) {
+    const int f = min(i * nt + int(threadIdx.x), kFrags - 1);  // fragment f / 64, lane f % 64
+    if constexpr (AP32) {
+      ar[i] = reinterpret_cast<const half8_t*>(p.a)[f];
+    } else {
+      // Rows past M repeat row M - 1 (their sums are never stored).
+      const int fl = f & 63, frag = f >> 6, s2 = frag & 1, t = (frag >> 1) % MT, c = (frag >> 1) / MT;
+      const int row = min(16 * t + (fl & 15), p.m - 1), acol = 64 * c + 32 * s2 + 8 * (fl >> 4);
+      ar[i] = *reinterpret_cast<const half8_t*>(p.a + int64_t(row) * p.lda + acol);
     }
-    const int col = (cb_first + W * i) * 16 + j;
-    if (col >= p.n) return;
-    const float bias = has_bias ? h2f(b.bias) : 0.f;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const float scale = p.scales[colc];
+  const uint16_t bias_raw = *(gu16)(has_bias ? p.epi.bias + colc : p.a);
+  u32x4_t wr[KC];
+  const u32x4_t* wb = p.w + int64_t(cbl) * KC * 64 + lane;
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    __builtin_amdgcn_sched_barrier(0);
+    wr[c] = __builtin_nontemporal_load(wb + c * 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kACopy; ++i)  // clamped like the loads: a repeated index stores the same value
+    a_lds[min(i * nt + int(threadIdx.x), kFrags - 1)] = ar[i];
+  __syncthreads();
+
+  // Four sums, chunk c into sum c % 4, added in that order at the end: the K
+  // order of the 4-wave packed GEMV over the same KC (wave w takes chunks w,
+  // w + 4, ...; the waves are added in order), which serves 1..16 rows, so a
+  // row's logits do not depend on the batch size.
+  float4_t acc[4][MT];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[q][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    const half8_t b0 = dequant8(wr[c][0], wr[c][1], scale);
+    const half8_t b1 = dequant8(wr[c][2], wr[c][3], scale);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      float4_t& ac = acc[c % 4][t];
+      ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * MT + t) * 2) * 64 + lane], b0, ac, 0, 0, 0);
+      ac = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lds[((c * MT + t) * 2 + 1) * 64 + lane], b1, ac, 0, 0, 0);
+    }
+    // One chunk's LDS reads and dequantisation at a time.
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const float bias = has_bias ? h2f(bias_raw) : 0.f;
+  float vals[MT * 4];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum += acc[q][t][v];
+      vals[t * 4 + v] = sum;
+    }
+  if (active && col < p.n) {
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * t + 4 * g + v;
-        float sum = 0.f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sum += acc[q][t][v];
-        if (p.epi.kind == EPI_F32) {
-          // fp32 logits + bias, with this lane's running argmax.
-          const float val = sum + bias;
-          if (row < p.m) static_cast<float*>(p.epi.y)[int64_t(row) * p.epi.ldy + col] = val;
-          amax_merge(bv[t * 4 + v], bi[t * 4 + v], val, col);
-        } else if (row < p.m) {
-          apply_epilogue(p.epi, row, col, sum, bias);
+        if (row >= p.m) continue;
+        const float sum = vals[t * 4 + v];
+        if constexpr (EK == EPI_F32) {
+          static_cast<float*>(p.epi.y)[int64_t(row) * p.epi.ldy + col] = sum + bias;
+        } else if constexpr (EK == EPI_GELU) {
+          static_cast<uint16_t*>(p.epi.y)[int64_t(row) * p.epi.ldy + col] = f2h(gelu_tanh(rt16(sum + bias)));
+        } else if constexpr (EK == EPI_RESIDUAL) {
+          const float r = h2f(p.epi.residual[int64_t(row) * p.epi.ldr + col]);
+          static_cast<uint16_t*>(p.epi.y)[int64_t(row) * p.epi.ldy + col] = f2h(r + rt16(sum + bias));
+        } else {
+          static_cast<uint16_t*>(p.epi.y)[int64_t(row) * p.epi.ldy + col] = f2h(sum + bias);
         }
       }
-  };
-  Block x;
-  {
-    // A into LDS, then the wave's blocks one at a time (enough waves per CU
-    // to overlap them; issuing the first blocks' weight loads ahead of the A
-    // copy measured slower).
-#pragma unroll
-    for (int i = 0; i < kACopy; ++i) {
-      const int f = i * W * 64 + threadIdx.x;  // fragment f / 64, lane f % 64
-      if constexpr (AP32) {
-        a_lds[f] = reinterpret_cast<const half8_t*>(p.a)[f];
-      } else {
-        const int fl = f & 63, frag = f >> 6, s2 = frag & 1, t = (frag >> 1) % MT, c = (frag >> 1) / MT;
-        const int row = 16 * t + (fl & 15), col = 64 * c + 32 * s2 + 8 * (fl >> 4);
-        a_lds[f] = row < p.m ? *reinterpret_cast<const half8_t*>(p.a + int64_t(row) * p.lda + col) : half8_t{};
-      }
-    }
-    __syncthreads();
-    for (int i = 0; i < count; ++i) {
-      load(x, i);
-      compute(x, i);
-    }
+  }
+  if constexpr (EK == EPI_F32) {
     if (!p.amax_v) return;
     // Argmax partials: across the 16 column lanes of each row, then across the
-    // waves through LDS; one (value, column) per row per workgroup.
-    __shared__ float sv[W][32];
-    __shared__ int si[W][32];
+    // waves (blocks in column order) through LDS; one (value, column) per row
+    // per workgroup, the lowest column on ties.
+    const bool live = active && col < p.n;
 #pragma unroll
     for (int r = 0; r < MT * 4; ++r) {
+      float bv = live ? vals[r] + bias : -__builtin_huge_valf();
+      int bi = live ? col : INT_MAX;
 #pragma unroll
-      for (int o = 1; o < 16; o <<= 1)
-        amax_merge(bv[r], bi[r], __shfl_xor(bv[r], o, 64), __shfl_xor(bi[r], o, 64));
+      for (int o = 1; o < 16; o <<= 1) amax_merge(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
       if (j == 0) {
-        sv[wave][16 * (r >> 2) + 4 * g + (r & 3)] = bv[r];
-        si[wave][16 * (r >> 2) + 4 * g + (r & 3)] = bi[r];
+        sv[wave][16 * (r >> 2) + 4 * g + (r & 3)] = bv;
+        si[wave][16 * (r >> 2) + 4 * g + (r & 3)] = bi;
       }
     }
     __syncthreads();
@@ -878,7 +893,8 @@ __global__ __launch_bounds__(W * 64) void gemv_wide_kernel(WideParams p) {
       float v = sv[0][threadIdx.x];
       int i = si[0][threadIdx.x];
 #pragma unroll
-      for (int w = 1; w < W; ++w) amax_merge(v, i, sv[w][threadIdx.x], si[w][threadIdx.x]);
+      for (int w = 1; w < W; ++w)
+        if (w < p.per) amax_merge(v, i, sv[w][threadIdx.x], si[w][threadIdx.x]);
       p.amax_v[threadIdx.x * gridDim.x + blockIdx.x] = v;
       p.amax_i[threadIdx.x * gridDim.x + blockIdx.x] = i;
     }
@@ -1477,6 +1493,18 @@ hipError_t launch_part(const GemmArgs& g, const Scratch* s, hipStream_t stream, 
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 template <int MT>
 hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   PackedParams p{};
@@ -1505,22 +1533,30 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
     WideParams wp{};
     wp.a = g.a; wp.lda = g.lda; wp.w = p.w; wp.scales = p.scales; wp.m = p.m; wp.n = p.n; wp.nb = p.nb;
     wp.epi = p.epi;
-    wp.per = 16;
+    const int cus = device_cus();
+    wp.per = std::max(kWideMinWaves, std::min(kWideWaves, (p.nb + cus - 1) / cus));
     const int grid = (p.nb + wp.per - 1) / wp.per;
     if (p.epi.kind == EPI_F32 && g.amax_v && g.amax_i && g.amax_groups && size_t(grid) * 32 <= g.amax_capacity) {
       wp.amax_v = g.amax_v;
       wp.amax_i = g.amax_i;
       *g.amax_groups = grid;
     }
-    const dim3 gd{unsigned(grid)}, bd{512u};
+    const dim3 gd{unsigned(grid)}, bd{unsigned(wp.per * 64)};
     if constexpr (MT == 2) {
+      auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, gd, bd, 0, stream, wp); };
       if (g.a_p32) {
-        if (p.kc == 12) hipLaunchKernelGGL((gemv_wide_kernel<2, 12, 8, true>), gd, bd, 0, stream, wp);
-        else hipLaunchKernelGGL((gemv_wide_kernel<2, 16, 8, true>), gd, bd, 0, stream, wp);
-      } else if (p.kc == 12) {
-        hipLaunchKernelGGL((gemv_wide_kernel<2, 12, 8, false>), gd, bd, 0, stream, wp);
+        if (p.kc == 12) go(gemv_wide_kernel<2, 12, EPI_F32, true>);
+        else go(gemv_wide_kernel<2, 16, EPI_F32, true>);
       } else {
-        hipLaunchKernelGGL((gemv_wide_kernel<2, 16, 8, false>), gd, bd, 0, stream, wp);
+        const bool k12 = p.kc == 12;
+        switch (p.epi.kind) {
+          case EPI_F32: k12 ? go(gemv_wide_kernel<2, 12, EPI_F32, false>) : go(gemv_wide_kernel<2, 16, EPI_F32, false>); break;
+          case EPI_GELU: k12 ? go(gemv_wide_kernel<2, 12, EPI_GELU, false>) : go(gemv_wide_kernel<2, 16, EPI_GELU, false>); break;
+          case EPI_RESIDUAL:
+            k12 ? go(gemv_wide_kernel<2, 12, EPI_RESIDUAL, false>) : go(gemv_wide_kernel<2, 16, EPI_RESIDUAL, false>);
+            break;
+          default: k12 ? go(gemv_wide_kernel<2, 12, EPI_F16, false>) : go(gemv_wide_kernel<2, 16, EPI_F16, false>); break;
+        }
       }
     }
     return hipGetLastError();
