@@ -745,12 +745,15 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
 
 // ---------------------------------------------------------------------------
 // Wide decode GEMV (the LM head): 17..32 rows against many 16-column blocks.
-// One workgroup per CU over per = ceil(blocks / CUs) <= 16 consecutive column
-// blocks (no CU takes a second turn), one block per wave over the full K, so
-// the accumulators go straight to the epilogue (no reduction across waves)
-// and A is read once per workgroup (the split-K GEMV re-reads all of A for
-// every one or two column blocks: 1571 workgroups x 48 KiB for the 38.6 MB
-// GPT-2 head at M = 32).  A wave issues its share of the A copy, then its
+// Two workgroups per CU over per = ceil(blocks / (2 CUs)), clamped to 6..16,
+// consecutive column blocks (no CU takes a third turn; on the GPT-2 head 449
+// workgroups of 7 waves: 15.2 us at M = 32 against 17.1 with one workgroup of
+// 13 per CU and 20.7 with 9..12 waves, whose workgroups no longer fit twice),
+// one block per wave over the full K, so the accumulators go straight to the
+// epilogue (no reduction across waves) and A is read once per workgroup (the
+// split-K GEMV re-reads all of A for every one or two column blocks: 1571
+// workgroups x 48 KiB for the 38.6 MB GPT-2 head at M = 32).  A wave issues
+// its share of the A copy, then its
 // block's scale, bias and K chunks in K order (scheduling barriers hold the
 // order: loads return in issue order and a wait names a count, not a load),
 // so A lands first and goes to LDS while the weights stream, and chunk c is
@@ -766,7 +769,7 @@ struct WideParams {
   int32_t* amax_i;
 };
 
-constexpr int kWideWaves = 16, kWideMinWaves = 8;
+constexpr int kWideWaves = 16, kWideMinWaves = 6;
 
 template <int MT, int KC, int EK, bool AP32>
 __global__ __launch_bounds__(kWideWaves * 64) void gemv_wide_kernel(WideParams p) {
@@ -1534,7 +1537,7 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
     wp.a = g.a; wp.lda = g.lda; wp.w = p.w; wp.scales = p.scales; wp.m = p.m; wp.n = p.n; wp.nb = p.nb;
     wp.epi = p.epi;
     const int cus = device_cus();
-    wp.per = std::max(kWideMinWaves, std::min(kWideWaves, (p.nb + cus - 1) / cus));
+    wp.per = std::max(kWideMinWaves, std::min(kWideWaves, (p.nb + 2 * cus - 1) / (2 * cus)));
     const int grid = (p.nb + wp.per - 1) / wp.per;
     if (p.epi.kind == EPI_F32 && g.amax_v && g.amax_i && g.amax_groups && size_t(grid) * 32 <= g.amax_capacity) {
       wp.amax_v = g.amax_v;
