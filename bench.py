@@ -388,14 +388,16 @@ def run_limits(rp):
     kernel replayed back to back from a graph; pure 16-byte streaming reads of
     the decode-attention size (48 MiB over 768 workgroups), a long stream
     (512 MiB over 256 workgroups) and one CU's ceiling (32 workgroups of 1024
-    threads, 256 KiB each); and a sweep of single-launch reads of the configs[1]
-    GEMV's size (2.25 MiB) over workgroup counts 192..2304 and 1, 4 or 16 waves
-    per workgroup, whose best point is the single-launch ceiling for that size.
+    threads, 256 KiB each); and sweeps of single-launch reads of the configs[1]
+    GEMV's size (2.25 MiB, workgroup counts 192..2304 and 1, 4 or 16 waves per
+    workgroup), of the LM head's 38.6 MB and of configs[3]'s 50.9 MB (256..3142
+    workgroups of 1..8 waves), whose best points are the single-launch ceilings
+    for those sizes.
     Every probe rotates over 1 GiB of buffers."""
     import torch
     lib = C.CDLL(str(ROOT / "benchlib" / "liblimits.so"))
     lib.tia_diag_empty.argtypes = [C.c_size_t]
-    lib.tia_diag_stream.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_size_t]
+    lib.tia_diag_stream.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_int, C.c_size_t]
     s = lambda: rp.stream.cuda_stream
     res = {"empty_kernel_us_per_launch": rp.time_us([lambda: _check_diag(lib.tia_diag_empty(s()))] * 256)}
     total = 1 << 30
@@ -406,7 +408,8 @@ def run_limits(rp):
         nbytes = per_wg * wgs
         sets = max(1, min(64, total // nbytes))
         launches = [(lambda off: lambda: _check_diag(lib.tia_diag_stream(
-            src.data_ptr() + off, out.data_ptr(), per_wg, wgs, thr, s())))(i * nbytes) for i in range(sets)]
+            src.data_ptr() + off, out.data_ptr(), out.numel(), per_wg, wgs, thr, s())))(i * nbytes)
+                    for i in range(sets)]
         return rp.time_us(launches), nbytes
 
     for name, per_wg, wgs, thr in (("stream_48MiB_768wg", 64 << 10, 768, 256),
@@ -425,6 +428,16 @@ def run_limits(rp):
     best = max(sweep, key=lambda k: sweep[k]["GBps"])
     res["stream_2.25MiB_sweep"] = sweep
     res["stream_2.25MiB_best"] = dict(sweep[best], shape=best, hbm_frac=sweep[best]["GBps"] / HBM_PEAK_GBS)
+    # The same ceiling at the LM head's weight bytes (768 -> 50257) and at
+    # configs[3]'s K/V bytes: the best single launch that only reads them.
+    for name, size in (("38.6MB", 38_597_376), ("50.9MB", 50_900_000)):
+        sweep = {}
+        for wgs in (256, 512, 768, 1024, 1536, 2048, 3142):
+            for thr in (64, 128, 256, 512):
+                us, nbytes = stream_us(max(1024, size // wgs // 1024 * 1024), wgs, thr)
+                sweep[f"{wgs}wg_x{thr // 64}waves"] = {"us_per_launch": us, "GBps": nbytes / us / 1e3}
+        best = max(sweep, key=lambda k: sweep[k]["GBps"])
+        res[f"stream_{name}_best"] = dict(sweep[best], shape=best, hbm_frac=sweep[best]["GBps"] / HBM_PEAK_GBS)
     del src
     torch.cuda.empty_cache()
     return res

@@ -13,12 +13,13 @@
 
 // Entry points (C ABI, loaded by bench.py through ctypes):
 //   int tia_diag_empty(uintptr_t stream): enqueue one empty kernel.
-//   int tia_diag_stream(const void* src, unsigned* out, int64_t per_wg, int wgs,
-//                       int threads, uintptr_t stream): enqueue a streaming read
-//     of wgs * per_wg bytes from 16-byte aligned `src`, workgroup w reading
-//     [w * per_wg, (w + 1) * per_wg) with `threads` threads (a multiple of 64, at
-//     most 1024); `out` receives wgs * threads dwords; per_wg a positive multiple
-//     of 1024.  Both return 0, or 1 on invalid arguments or a launch error.
+//   int tia_diag_stream(const void* src, unsigned* out, int64_t out_dwords,
+//                       int64_t per_wg, int wgs, int threads, uintptr_t stream):
+//     enqueue a streaming read of wgs * per_wg bytes from 16-byte aligned `src`,
+//     workgroup w reading [w * per_wg, (w + 1) * per_wg) with `threads` threads
+//     (a multiple of 64, at most 1024); `out` (out_dwords long) receives
+//     wgs * threads dwords; per_wg a positive multiple of 1024.  Both return 0,
+//     or 1 on invalid arguments (an `out` too short included) or a launch error.
 
 namespace {
 
@@ -52,10 +53,10 @@ extern "C" int tia_diag_empty(uintptr_t stream) {
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
-extern "C" int tia_diag_stream(const void* src, unsigned* out, int64_t per_wg, int wgs, int threads,
-                               uintptr_t stream) {
+extern "C" int tia_diag_stream(const void* src, unsigned* out, int64_t out_dwords, int64_t per_wg, int wgs,
+                               int threads, uintptr_t stream) {
   if (!src || !out || per_wg < 1024 || per_wg % 1024 != 0 || wgs < 1 || threads < 64 || threads > 1024 ||
-      threads % 64 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0)
+      threads % 64 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0 || int64_t(wgs) * threads > out_dwords)
     return 1;
   hipLaunchKernelGGL(stream_kernel<8>, dim3(wgs), dim3(threads), 0, reinterpret_cast<hipStream_t>(stream),
                      static_cast<const u32x4*>(src), out, per_wg);
