@@ -9,6 +9,13 @@ logits within atol 5e-2 after a ragged 32-request prefill and decode steps; a
 request's logits bit-identical alone and inside the 32-request batch (the two
 head kernels sum K in one order); greedy runs of 20 requests (two decode lanes)
 equal to each request decoded alone.
+
+With 18 layers the INT8 decode weights (278 MB) exceed what the second decode
+lane needs to find in the 256 MiB Infinity Cache, so a context decodes 17..32
+requests in one lane: the step's LM head is then the wide GEMV over 32 P32 rows,
+leaving per-workgroup argmax partials for the step's greedy feed.  Greedy tokens
+of 24 requests together equal each request decoded alone (one row, the packed
+GEMV head), and two decode steps' logits match the oracle.
 """
 import numpy as np
 import pytest
@@ -106,3 +113,42 @@ def test_medium_greedy_lanes_match_alone(model):
         alone = model.greedy([prompts[i]], 8, slots=[33])["tokens"][0]
         assert alone == together[i], f"request {i}"
     model.reset_all()
+
+
+@pytest.fixture(scope="module")
+def deep_artifact(tmp_path_factory):
+    from tinyinfer_amd.artifact import write_synthetic
+    say("writing 18-layer GPT-2 medium-shaped synthetic artifact")
+    return write_synthetic(tmp_path_factory.mktemp("gpt2m18"), dict(MEDIUM_2L, layers=18), seed=17)
+
+
+def test_medium_one_lane_greedy_wide_head_matches_alone_and_oracle(deep_artifact):
+    from tinyinfer_amd import LLM_LIB
+    from tinyinfer_amd.artifact import load_tensors
+    from tinyinfer_amd.runtime import NativeModel
+    prompts = prompts_of(6, 24, 2, 24)
+    with NativeModel(LLM_LIB, deep_artifact, max_batch=32, cache_slots=34, capacity=64) as m:
+        say("medium 18 layers: 24-request greedy in one lane vs each request alone")
+        together = m.greedy(prompts, 6)["tokens"]
+        for i in (0, 11, 23):
+            m.reset_all()
+            alone = m.greedy([prompts[i]], 6, slots=[33])["tokens"][0]
+            assert alone == together[i], f"request {i}"
+        say("medium 18 layers: 24-row decode logits vs oracle")
+        m.reset_all()
+        slots = list(range(24))
+        gpu = logits_of(m.forward(slots, prompts))
+        manifest, tensors = load_tensors(deep_artifact)
+        cpu = oracle.Gpt2(tensors, manifest["architecture"], slots=24, capacity=64)
+        try:
+            ref, nxt = cpu.forward(slots, prompts)
+            print(f"medium-18 prefill max |logit diff| {np.abs(gpu - ref).max():.3g}")
+            assert np.abs(gpu - ref).max() <= 5e-2
+            for _ in range(2):
+                step = [[int(t)] for t in nxt]
+                gpu = logits_of(m.forward(slots, step))
+                ref, nxt = cpu.forward(slots, step)
+                print(f"medium-18 decode max |logit diff| {np.abs(gpu - ref).max():.3g}")
+                assert np.abs(gpu - ref).max() <= 5e-2
+        finally:
+            cpu.close()
