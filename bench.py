@@ -476,8 +476,15 @@ def run_prefill_attention(rp):
 
         us = rp.time_us([launch(i) for i in range(sets)] * 4)
         flops = 4.0 * B * H * D * (N * (N + 1) / 2)
-        res[f"B{B}_H{H}_Q{N}_K{N}_D{D}_causal"] = {"us_per_launch": us, "TFLOPs": flops / us / 1e6,
-                                                    "mfma_frac": flops / us / 1e6 / FP16_DENSE_TFLOPS}
+        nbytes = 4 * B * H * N * D * 2  # q, k, v read once, out written once
+        # Below fp16-dense / HBM (2500 TFLOP/s / 8 TB/s = 312 flop per byte) the
+        # shape is bound by its bytes, above by its flops.
+        intensity = flops / nbytes
+        res[f"B{B}_H{H}_Q{N}_K{N}_D{D}_causal"] = {
+            "us_per_launch": us, "TFLOPs": flops / us / 1e6, "mfma_frac": flops / us / 1e6 / FP16_DENSE_TFLOPS,
+            "bytes": nbytes, "GBps": nbytes / us / 1e3, "hbm_frac": nbytes / us / 1e3 / HBM_PEAK_GBS,
+            "flop_per_byte": intensity,
+            "bound": "hbm" if intensity < FP16_DENSE_TFLOPS / (HBM_PEAK_GBS / 1e3) else "mfma"}
         del q, k, v
         torch.cuda.empty_cache()
     return res
