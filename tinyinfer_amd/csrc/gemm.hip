@@ -700,9 +700,12 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
   // Epilogue operands of output column cb*16 + QC h + threadIdx.x % QC, loaded
   // first and unconditionally (A's first element stands in), converted at use.
   const int ecol = min(cb * 16 + QC * h + int(threadIdx.x % QC), p.n - 1);
-  const uint16_t bias_raw = (has_bias ? p.epi.bias : p.a)[has_bias ? ecol : 0];
-  const uint16_t res_raw = (has_res ? p.epi.residual : p.a)[has_res ? r_off(p.epi, 0, ecol) : 0];
-  const float scale = p.scales[min(col, p.n - 1)] * (col < p.n ? 1.f : 0.f);
+  const uint16_t bias_raw = ldg_u16(has_bias ? p.epi.bias + ecol : p.a);
+  const uint16_t res_raw = ldg_u16(has_res ? p.epi.residual + r_off(p.epi, 0, ecol) : p.a);
+  // Masked only at use: an arithmetic use here would wait for this load before
+  // the weight loads below are issued.
+  const float scale = p.scales[min(col, p.n - 1)];
+  const bool col_ok = col < p.n;
   const u32x4_t* wb = p.w + int64_t(cb) * p.kc * 64 + g * 16 + QC * h + c;
   const uint16_t* arow = p.a + 8 * g;
   const int steps = (p.kc + RPL - 1) / RPL;
@@ -721,7 +724,7 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const bool live = s0 + i * W < steps && RPL * (s0 + i * W) + r < p.kc;
-      const float si = live ? scale : 0.f;
+      const float si = live && col_ok ? scale : 0.f;
       const half8_t b0 = dequant8(wf[i][0], wf[i][1], si);
       const half8_t b1 = dequant8(wf[i][2], wf[i][3], si);
 #pragma unroll
@@ -753,11 +756,11 @@ __global__ __launch_bounds__(W * 64) void gemv_part_kernel(PackedParams p) {
 // epilogue (no reduction across waves) and A is read once per workgroup (the
 // split-K GEMV re-reads all of A for every one or two column blocks: 1571
 // workgroups x 48 KiB for the 38.6 MB GPT-2 head at M = 32).  A wave issues
-// its share of the A copy, then its
-// block's scale, bias and K chunks in K order (scheduling barriers hold the
-// order: loads return in issue order and a wait names a count, not a load),
-// so A lands first and goes to LDS while the weights stream, and chunk c is
-// multiplied as soon as it has arrived.  EK is the epilogue kind.
+// its share of the A copy, then its block's scale, bias and K chunks in K
+// order (scheduling barriers hold the order: loads return in issue order and a
+// wait names a count, not a load), so A lands first and goes to LDS while the
+// weights stream, and chunk c is multiplied as soon as it has arrived.  EK is
+// the epilogue kind.
 struct WideParams {
   const uint16_t* a;    // P32 fragment-packed [32][K], or row-major [M][lda] (AP32 false)
   int64_t lda;
@@ -782,7 +785,6 @@ __global__ __launch_bounds__(kWideWaves * 64) void gemv_wide_kernel(WideParams p
   __shared__ half8_t a_lds[kFrags];
   __shared__ float sv[W][32];
   __shared__ int si[W][32];
-  using gu16 = const uint16_t __attribute__((address_space(1)))*;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int cb = blockIdx.x * p.per + wave;
@@ -807,7 +809,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void gemv_wide_kernel(WideParams p
   }
   __builtin_amdgcn_sched_barrier(0);
   const float scale = p.scales[colc];
-  const uint16_t bias_raw = *(gu16)(has_bias ? p.epi.bias + colc : p.a);
+  const uint16_t bias_raw = ldg_u16(has_bias ? p.epi.bias + colc : p.a);
   u32x4_t wr[KC];
   const u32x4_t* wb = p.w + int64_t(cbl) * KC * 64 + lane;
 #pragma unroll
