@@ -61,6 +61,23 @@ __device__ __forceinline__ int64_t r_off(const Epilogue& e, int m, int n) {
   return e.p32 ? p32_off(m, n) : int64_t(m) * e.ldr + n;
 }
 
+// EPI_QKV element (m, n) = acc + bias: fp16 into y, and for the K and V
+// columns of a real token the same bits into the slot cache.
+__device__ __forceinline__ void qkv_store(const Epilogue& e, int m, int n, float val) {
+  const uint16_t hv = f2h(val);
+  static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = hv;
+  if (n >= e.hidden) {
+    const int b = m / e.qrows, t = m - b * e.qrows;
+    if (t < e.qlens[b]) {
+      const int part = n >= 2 * e.hidden ? 2 : 1;
+      const int c = n - part * e.hidden, h = c >> 6, d = c & 63;
+      const int64_t pos = int64_t(e.offsets[b]) + t;
+      const int64_t idx = (((int64_t(e.slots[b]) * e.layers + e.layer) * e.heads + h) * e.capacity + pos) * 64 + d;
+      (part == 1 ? e.kcache : e.vcache)[idx] = hv;
+    }
+  }
+}
+
 // `bias` is epilogue_bias(e, n) (callers may load it early); EPI_RAW_F32 ignores it.
 // `resid` is residual[m][n] for EPI_RESIDUAL (likewise loaded by the caller).
 __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias,
@@ -82,22 +99,9 @@ __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, 
       static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(resid + h);
       return;
     }
-    case EPI_QKV: {
-      const uint16_t hv = f2h(acc + bias);
-      static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = hv;
-      if (n >= e.hidden) {
-        const int b = m / e.qrows, t = m - b * e.qrows;
-        if (t < e.qlens[b]) {
-          const int part = n >= 2 * e.hidden ? 2 : 1;
-          const int c = n - part * e.hidden, h = c >> 6, d = c & 63;
-          const int64_t pos = int64_t(e.offsets[b]) + t;
-          const int64_t idx =
-              (((int64_t(e.slots[b]) * e.layers + e.layer) * e.heads + h) * e.capacity + pos) * 64 + d;
-          (part == 1 ? e.kcache : e.vcache)[idx] = hv;
-        }
-      }
+    case EPI_QKV:
+      qkv_store(e, m, n, acc + bias);
       return;
-    }
     default:  // EPI_F16
       static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(acc + bias);
       return;
@@ -970,6 +974,148 @@ __device__ __forceinline__ void wait_chunk(int outstanding) {
   }
 }
 
+// Row pitch (floats) of the fp32 tiles the MFMA GEMMs stage their sums in for
+// the epilogue: rows stay 16-byte aligned, and the accumulator stores (lane
+// (j, g) of a 16-column block writes rows 4g + v, column j) hit 64 distinct
+// banks.
+constexpr int tile_pitch(int bn) { return bn + 4; }
+
+// The 4 bias values of columns col .. col + 3 (0 past N or without a bias),
+// loaded early: used only by the tile epilogue.  Without a bias the loads
+// read `any`, a valid fp16 address (A's first element), and are discarded.
+__device__ __forceinline__ void load_bias4(const Epilogue& e, int col, int n, const uint16_t* any,
+                                           float (&bias)[4]) {
+  const bool has = e.kind != EPI_RAW_F32 && e.bias;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint16_t raw = ldg_u16(has ? e.bias + min(col + c, n - 1) : any);
+    bias[c] = has && col + c < n ? h2f(raw) : 0.f;
+  }
+}
+
+// Epilogue of TR rows x BN columns of fp32 sums staged in LDS at pitch
+// tile_pitch(BN): thread t of NT takes columns col = n0 + 4 (t % (BN / 4))
+// .. + 3 (its bias4) of tile rows t / (BN / 4) + i NT / (BN / 4), tile row 0
+// being output row r0.  The epilogue kind is switched once, outside the
+// loops, so each kind runs straight-line code (a switch per element cost ~70
+// VALU and ~20 scalar instructions per output); residuals are loaded before
+// any result is computed; a group of 4 columns inside the matrix goes out as
+// one 8-byte (fp16) or 16-byte (fp32) store when the layout allows it.
+// partials != null: the raw sums go to partials[(split m + row) n + col]
+// (split-K or a deferred finisher) instead.
+template <int TR, int BN, int NT>
+__device__ __forceinline__ void tile_epilogue(const Epilogue& e, const float* ctile, int r0, int n0, int m, int n,
+                                              const float (&bias)[4], float* partials, int split) {
+  constexpr int CG = BN / 4, RS = NT / CG, RPT = TR / RS;
+  static_assert(NT % CG == 0 && TR % RS == 0 && RPT >= 1, "whole row groups per thread");
+  const int c4 = int(threadIdx.x) % CG, rl0 = int(threadIdx.x) / CG;
+  const int col = n0 + 4 * c4;
+  if (col >= n) return;
+  const bool full = col + 4 <= n;
+  // Row i of this thread: output row r0 + rl0 + i RS, its 4 sums from LDS.
+  auto row_of = [&](int i) { return r0 + rl0 + i * RS; };
+  auto sums = [&](int i) {
+    return *reinterpret_cast<const float4_t*>(ctile + (rl0 + i * RS) * tile_pitch(BN) + 4 * c4);
+  };
+  auto aligned = [](const void* ptr, int bytes) { return reinterpret_cast<uintptr_t>(ptr) % bytes == 0; };
+  // fp32 rows at base + row * ld (+ col): one 16-byte store per row when it can.
+  auto store_f32 = [&](float* base, int64_t ld, auto&& f) {
+    const bool vec = full && ld % 4 == 0 && aligned(base, 16);
+#pragma unroll 1
+    for (int i = 0; i < RPT; ++i) {
+      const int row = row_of(i);
+      if (row >= m) break;
+      const float4_t v = sums(i);
+      float* dst = base + int64_t(row) * ld + col;
+      if (vec) {
+        *reinterpret_cast<float4_t*>(dst) = float4_t{f(v[0], 0), f(v[1], 1), f(v[2], 2), f(v[3], 3)};
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (col + c < n) dst[c] = f(v[c], c);
+      }
+    }
+  };
+  if (partials) {
+    store_f32(partials + int64_t(split) * m * n, n, [](float x, int) { return x; });
+    return;
+  }
+  switch (e.kind) {
+    case EPI_RAW_F32:
+      store_f32(static_cast<float*>(e.y), e.ldy, [](float x, int) { return x; });
+      return;
+    case EPI_F32:
+      store_f32(static_cast<float*>(e.y), e.ldy, [&](float x, int c) { return x + bias[c]; });
+      return;
+    case EPI_QKV:
+#pragma unroll 1
+      for (int i = 0; i < RPT; ++i) {
+        const int row = row_of(i);
+        if (row >= m) break;
+        const float4_t v = sums(i);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (col + c < n) qkv_store(e, row, col + c, v[c] + bias[c]);
+      }
+      return;
+    default:
+      break;
+  }
+  // fp16 outputs (EPI_F16, EPI_GELU, EPI_RESIDUAL), row-major or P32: the 4
+  // columns col .. col + 3 (col % 4 == 0) of a row are contiguous in both
+  // layouts, at y_off(row, col) + c.
+  uint16_t* y = static_cast<uint16_t*>(e.y);
+  const bool vec = full && (e.p32 || e.ldy % 4 == 0) && aligned(y, 8);
+  auto store_f16 = [&](int row, float o0, float o1, float o2, float o3) {
+    uint16_t* dst = y + y_off(e, row, col);
+    if (vec) {
+      *reinterpret_cast<half4_t*>(dst) = half4_t{f16r(o0), f16r(o1), f16r(o2), f16r(o3)};
+    } else {
+      const float o[4] = {o0, o1, o2, o3};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (col + c < n) dst[c] = f2h(o[c]);
+    }
+  };
+  if (e.kind == EPI_RESIDUAL) {
+    // Every residual of the thread in flight before the first result.
+    const bool rvec = full && (e.p32 || e.ldr % 4 == 0) && aligned(e.residual, 8);
+    half4_t rs[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const uint16_t* src = e.residual + r_off(e, min(row_of(i), m - 1), col);
+      if (rvec) {
+        rs[i] = *reinterpret_cast<const half4_t*>(src);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rs[i][c] = __builtin_bit_cast(f16, src[min(c, n - 1 - col)]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int row = row_of(i);
+      if (row >= m) break;
+      const float4_t v = sums(i);
+      float o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = float(rs[i][c]) + rt16(v[c] + bias[c]);
+      store_f16(row, o[0], o[1], o[2], o[3]);
+    }
+    return;
+  }
+  auto rows_f16 = [&](auto&& f) {
+#pragma unroll 1
+    for (int i = 0; i < RPT; ++i) {
+      const int row = row_of(i);
+      if (row >= m) break;
+      const float4_t v = sums(i);
+      store_f16(row, f(v[0], 0), f(v[1], 1), f(v[2], 2), f(v[3], 3));
+    }
+  };
+  if (e.kind == EPI_GELU) rows_f16([&](float x, int c) { return gelu_tanh(rt16(x + bias[c])); });
+  else rows_f16([&](float x, int c) { return x + bias[c]; });
+}
+
 // Workgroup -> (split, tile row, tile column).  Workgroups are dispatched to
 // the 8 XCDs round-robin by id, so ids are first regrouped into 8 contiguous
 // runs (one per XCD); within a split, tiles are walked in groups of GM tile
@@ -1043,13 +1189,11 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
   if (wave < BN / 64)
     __builtin_amdgcn_global_load_lds((global_ptr)(p.scales + min(cb0 * 16 + 64 * wave + lane, p.n - 1)),
                                      (lds_ptr)(lds + S * STAGE + 256 * wave), 4, 0, 0);
-  // The epilogue below gives thread t the outputs of tile column t % BN only:
-  // its bias is loaded now (used only after the loop).
-  static_assert(256 % BN == 0, "a thread's epilogue outputs share one column");
-  const bool has_bias = p.epi.kind != EPI_RAW_F32 && p.epi.bias;
-  const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
-  const int my_col = cb0 * 16 + int(threadIdx.x % BN);
-  const float bias = h2f(bsrc[has_bias ? min(my_col, p.n - 1) : 0]) * (has_bias ? 1.f : 0.f);
+  // The epilogue gives thread t columns 4 (t % (BN / 4)) .. + 3 of the tile:
+  // their bias is loaded now (used only after the loop).
+  const bool epi_now = p.splits == 1 && !p.defer;
+  float bias[4];
+  load_bias4(p.epi, cb0 * 16 + 4 * int(threadIdx.x % (BN / 4)), p.n, p.a, bias);
   float4_t acc[MT][R];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
@@ -1085,10 +1229,9 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
   wait_vmcnt<0>();
 
   // Epilogue through LDS (the stages are free once every wave is past the last
-  // chunk): the accumulators land in a [BM][BN+1] fp32 tile, then thread t
-  // finishes column t % BN of rows t / BN, t / BN + 256 / BN, ... with one
-  // epilogue call site and coalesced stores.
-  static_assert(BM * (BN + 1) * 4 <= S * STAGE, "fp32 tile fits the stages");
+  // chunk): the accumulators land in a BM x BN fp32 tile, which tile_epilogue
+  // finishes 4 columns per thread.
+  static_assert(BM * tile_pitch(BN) * 4 <= S * STAGE, "fp32 tile fits the stages");
   __syncthreads();
   float* ctile = reinterpret_cast<float*>(lds);
 #pragma unroll
@@ -1097,19 +1240,9 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        ctile[((wm * MT + t) * 16 + 4 * g + v) * (BN + 1) + (wn * R + r) * 16 + j] = acc[t][r][v];
+        ctile[((wm * MT + t) * 16 + 4 * g + v) * tile_pitch(BN) + (wn * R + r) * 16 + j] = acc[t][r][v];
   __syncthreads();
-  const bool epi_now = p.splits == 1 && !p.defer;
-  const int cl = int(threadIdx.x % BN);
-  if (my_col < p.n) {
-    for (int rl = int(threadIdx.x / BN); rl < BM; rl += 256 / BN) {
-      const int row = m0 + rl;
-      if (row >= p.m) break;
-      const float val = ctile[rl * (BN + 1) + cl];
-      if (epi_now) apply_epilogue(p.epi, row, my_col, val, bias);
-      else p.partials[(int64_t(split) * p.m + row) * p.n + my_col] = val;
-    }
-  }
+  tile_epilogue<BM, BN, 256>(p.epi, ctile, m0, cb0 * 16, p.m, p.n, bias, epi_now ? nullptr : p.partials, split);
 }
 
 // ---------------------------------------------------------------------------
@@ -1760,14 +1893,11 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void f16_gemm_kernel(F16GemmPara
       __builtin_amdgcn_global_load_lds((global_ptr)(src[l] + int64_t(chunk) * stride[l]),
                                        (lds_ptr)(lds + stage * STAGE + (wave * LPW + l) * 1024), 16, 0, 0);
   };
-  // The epilogue gives thread t the outputs of tile column t % BN: its bias is
-  // loaded now and used after the loop (a null bias reads A's first element).
-  static_assert(NT % BN == 0, "epilogue column mapping");
+  // The epilogue gives thread t columns 4 (t % (BN / 4)) .. + 3 of the tile:
+  // their bias is loaded now and used after the loop.
   const bool epi_now = p.splits == 1 && !p.defer;
-  const bool has_bias = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias;
-  const uint16_t* bsrc = has_bias ? p.epi.bias : p.a;
-  const int my_col = cb0 * 16 + int(threadIdx.x % BN);
-  const uint16_t braw = bsrc[has_bias ? min(my_col, p.n - 1) : 0];
+  float bias[4];
+  load_bias4(p.epi, cb0 * 16 + 4 * int(threadIdx.x % (BN / 4)), p.n, p.a, bias);
 
   float4_t acc[MT][R];
 #pragma unroll
@@ -1794,14 +1924,12 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void f16_gemm_kernel(F16GemmPara
   }
   wait_vmcnt<0>();
 
-  // Epilogue through an LDS fp32 tile of BM / EP rows x (BN + 1), EP passes
-  // (one epilogue call site, coalesced stores; the accumulators never meet the
-  // epilogue's registers; EP = 2 halves the LDS the kernel needs).
+  // Epilogue through an LDS fp32 tile of BM / EP rows x BN, EP passes (the
+  // accumulators never meet the epilogue's registers; EP > 1 cuts the LDS the
+  // kernel needs), each finished 4 columns per thread by tile_epilogue.
   constexpr int PR = BM / EP;  // rows per pass
   static_assert(BM % EP == 0 && PR % 16 == 0, "whole 16-row blocks per pass");
   float* ctile = reinterpret_cast<float*>(lds);
-  const int cl = int(threadIdx.x % BN);
-  const float bias = has_bias ? h2f(braw) : 0.f;
 #pragma unroll
   for (int pass = 0; pass < EP; ++pass) {
     __syncthreads();
@@ -1812,18 +1940,12 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void f16_gemm_kernel(F16GemmPara
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) ctile[(rb + 4 * g + v) * (BN + 1) + (wn * R + r) * 16 + j] = acc[t][r][v];
+        for (int v = 0; v < 4; ++v)
+          ctile[(rb + 4 * g + v) * tile_pitch(BN) + (wn * R + r) * 16 + j] = acc[t][r][v];
     }
     __syncthreads();
-    if (my_col < p.n) {
-      for (int rl = int(threadIdx.x / BN); rl < PR; rl += NT / BN) {
-        const int row = m0 + pass * PR + rl;
-        if (row >= p.m) break;
-        const float val = ctile[rl * (BN + 1) + cl];
-        if (epi_now) apply_epilogue(p.epi, row, my_col, val, bias);
-        else p.partials[(int64_t(split) * p.m + row) * p.n + my_col] = val;
-      }
-    }
+    tile_epilogue<PR, BN, NT>(p.epi, ctile, m0 + pass * PR, cb0 * 16, p.m, p.n, bias,
+                              epi_now ? nullptr : p.partials, split);
   }
 }
 
@@ -1831,7 +1953,7 @@ template <int WM, int WN, int MT, int R, int S, int EP = 1, int OCC = 2>
 hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   constexpr int BM = WM * MT * 16, BN = WN * R * 16;
   constexpr int NL = BM / 16 + BN / 16;
-  constexpr size_t kLds = std::max(size_t(S) * NL * 1024, size_t(BM / EP) * (BN + 1) * 4);
+  constexpr size_t kLds = std::max(size_t(S) * NL * 1024, size_t(BM / EP) * tile_pitch(BN) * 4);
   static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds));
   if (attr != hipSuccess) return attr;
