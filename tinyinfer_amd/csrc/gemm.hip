@@ -32,6 +32,7 @@
 #include <climits>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #include "common.hpp"
@@ -80,32 +81,41 @@ __device__ __forceinline__ void qkv_store(const Epilogue& e, int m, int n, float
 
 // `bias` is epilogue_bias(e, n) (callers may load it early); EPI_RAW_F32 ignores it.
 // `resid` is residual[m][n] for EPI_RESIDUAL (likewise loaded by the caller).
+// Element (m, n) of epilogue kind K (EPI_F16 for any kind not listed).
+template <int K>
+__device__ __forceinline__ void epilogue_k(const Epilogue& e, int m, int n, float acc, float bias, float resid) {
+  if constexpr (K == EPI_RAW_F32) {
+    static_cast<float*>(e.y)[int64_t(m) * e.ldy + n] = acc;
+  } else if constexpr (K == EPI_F32) {
+    static_cast<float*>(e.y)[int64_t(m) * e.ldy + n] = acc + bias;
+  } else if constexpr (K == EPI_GELU) {
+    static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(gelu_tanh(rt16(acc + bias)));
+  } else if constexpr (K == EPI_RESIDUAL) {
+    static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(resid + rt16(acc + bias));
+  } else if constexpr (K == EPI_QKV) {
+    qkv_store(e, m, n, acc + bias);
+  } else {
+    static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(acc + bias);
+  }
+}
+
+// Calls f(std::integral_constant<int, kind>) for the epilogue kind of e, so a
+// loop written inside f is compiled once per kind with no switch per element.
+template <typename F>
+__device__ __forceinline__ void with_epilogue_kind(const Epilogue& e, F&& f) {
+  switch (e.kind) {
+    case EPI_RAW_F32: f(std::integral_constant<int, EPI_RAW_F32>{}); return;
+    case EPI_F32: f(std::integral_constant<int, EPI_F32>{}); return;
+    case EPI_GELU: f(std::integral_constant<int, EPI_GELU>{}); return;
+    case EPI_RESIDUAL: f(std::integral_constant<int, EPI_RESIDUAL>{}); return;
+    case EPI_QKV: f(std::integral_constant<int, EPI_QKV>{}); return;
+    default: f(std::integral_constant<int, EPI_F16>{}); return;
+  }
+}
+
 __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias,
                                                float resid) {
-  switch (e.kind) {
-    case EPI_RAW_F32:
-      static_cast<float*>(e.y)[int64_t(m) * e.ldy + n] = acc;
-      return;
-    case EPI_F32:
-      static_cast<float*>(e.y)[int64_t(m) * e.ldy + n] = acc + bias;
-      return;
-    case EPI_GELU: {
-      const float h = rt16(acc + bias);
-      static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(gelu_tanh(h));
-      return;
-    }
-    case EPI_RESIDUAL: {
-      const float h = rt16(acc + bias);
-      static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(resid + h);
-      return;
-    }
-    case EPI_QKV:
-      qkv_store(e, m, n, acc + bias);
-      return;
-    default:  // EPI_F16
-      static_cast<uint16_t*>(e.y)[y_off(e, m, n)] = f2h(acc + bias);
-      return;
-  }
+  with_epilogue_kind(e, [&](auto k) { epilogue_k<decltype(k)::value>(e, m, n, acc, bias, resid); });
 }
 
 __device__ __forceinline__ void apply_epilogue(const Epilogue& e, int m, int n, float acc, float bias) {
@@ -306,21 +316,27 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* parti
   __shared__ float red[4][64];
   const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int64_t total = int64_t(m) * n;
-  for (int64_t base = int64_t(blockIdx.x) * 64; base < total; base += int64_t(gridDim.x) * 64) {
-    const int64_t i = base + lane;
-    float s = 0.f;
-    if (i < total) {
+  // One loop per epilogue kind (the kind is uniform over the launch).
+  with_epilogue_kind(epi, [&](auto kind) {
+    constexpr int K = decltype(kind)::value;
+    for (int64_t base = int64_t(blockIdx.x) * 64; base < total; base += int64_t(gridDim.x) * 64) {
+      const int64_t i = base + lane;
+      float s = 0.f;
+      if (i < total) {
 #pragma unroll 4
-      for (int sp = grp; sp < splits; sp += 4) s += partials[i + sp * total];
+        for (int sp = grp; sp < splits; sp += 4) s += partials[i + sp * total];
+      }
+      red[grp][lane] = s;
+      __syncthreads();
+      if (grp == 0 && i < total) {
+        const int row = int(i / n), col = int(i - int64_t(row) * n);
+        const float bias = K == EPI_RAW_F32 ? 0.f : epilogue_bias(epi, col);
+        const float resid = K == EPI_RESIDUAL ? h2f(epi.residual[r_off(epi, row, col)]) : 0.f;
+        epilogue_k<K>(epi, row, col, ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane], bias, resid);
+      }
+      __syncthreads();
     }
-    red[grp][lane] = s;
-    __syncthreads();
-    if (grp == 0 && i < total) {
-      const int row = int(i / n), col = int(i - int64_t(row) * n);
-      apply_epilogue(epi, row, col, ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]);
-    }
-    __syncthreads();
-  }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -1265,8 +1281,13 @@ constexpr int TBM = 64, TBN = 64, TBK = 32, TPAD = 40;  // LDS row pitch in halv
 
 template <bool INT8, bool WVEC, bool AVEC>
 __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
-  __shared__ __attribute__((aligned(16))) f16 As[2][TBM][TPAD];
-  __shared__ __attribute__((aligned(16))) f16 Bs[2][TBN][TPAD];  // transposed: [n][k]
+  // A and W^T double buffers; after the K loop the same bytes hold the fp32
+  // output tile for the epilogue.
+  constexpr size_t kStage = size_t(2) * (TBM + TBN) * TPAD * sizeof(f16);
+  constexpr size_t kTile = size_t(TBM) * tile_pitch(TBN) * sizeof(float);
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kStage > kTile ? kStage : kTile];
+  auto As = reinterpret_cast<f16(*)[TBM][TPAD]>(smem);
+  auto Bs = reinterpret_cast<f16(*)[TBN][TPAD]>(smem + size_t(2) * TBM * TPAD * sizeof(f16));  // transposed: [n][k]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
@@ -1334,6 +1355,9 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
     }
   };
 
+  // The epilogue gives thread t columns n0 + 4 (t % 16) .. + 3: their bias now.
+  float bias[4];
+  load_bias4(p.epi, n0 + 4 * (tid % (TBN / 4)), p.n, p.a, bias);
   float4_t acc[2][2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
@@ -1374,18 +1398,18 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
     if (i + 1 < nst) step(i + 1, s2);
     if (i + 2 < nst) step(i + 2, s0);
   }
-  const bool raw = gridDim.z > 1;
+  // Every wave is past its last LDS read before the tile overwrites the stages.
+  __syncthreads();
+  float* ctile = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = m0 + wm * 32 + 16 * t + 4 * g + v, n = n0 + wn * 32 + 16 * c + j;
-        if (m >= p.m || n >= p.n) continue;
-        if (raw) p.partials[(int64_t(split) * p.m + m) * p.n + n] = acc[t][c][v];
-        else apply_epilogue(p.epi, m, n, acc[t][c][v]);
-      }
+      for (int v = 0; v < 4; ++v)
+        ctile[(wm * 32 + 16 * t + 4 * g + v) * tile_pitch(TBN) + wn * 32 + 16 * c + j] = acc[t][c][v];
+  __syncthreads();
+  tile_epilogue<TBM, TBN, 256>(p.epi, ctile, m0, n0, p.m, p.n, bias, gridDim.z > 1 ? p.partials : nullptr, split);
 }
 
 // ---------------------------------------------------------------------------
