@@ -1814,7 +1814,10 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
 
 // (Tiles of 128 x 64 and 128 x 128 halve the LDS bytes and dequant work per
 // MFMA, but hold one or two 4-wave workgroups per CU and measured 1.3-2x slower
-// from M = 512 to 8192; the 64 x 64 tile keeps three per CU.)
+// from M = 512 to 8192; the 64 x 64 tile keeps three per CU.  A 3-stage ring
+// (two chunks in flight, 36 KiB, four workgroups per CU) times as fast as or
+// faster than 4 stages: M = 512 768->3072 13.2 against 13.7 us, M = 2048
+// 768->2304 24.6 against 25.7 us; 6 stages 15.0 / 32.5 us.)
 // 64 x 64 tiles; a shape that would split K over fewer than 192 of them but
 // has 192 tiles of 32 x 64 takes those unsplit instead (no fp32 partials:
 // M = 512, 3072 -> 768 moved 2.85x its algorithmic bytes as three K splits;
@@ -1823,7 +1826,7 @@ hipError_t launch_panel(const GemmArgs& g, const Scratch* s, hipStream_t stream,
   const int64_t tiles64 = int64_t((g.m + 63) / 64) * ((g.n + 63) / 64);
   const int64_t tiles32 = int64_t((g.m + 31) / 32) * ((g.n + 63) / 64);
   if (!g.canonical && tiles64 < 192 && tiles32 >= 192) return launch_panel_cfg<1, 4, 2, 1, 4>(g, s, stream, deferred);
-  return launch_panel_cfg<1, 4, 4, 1, 4>(g, s, stream, deferred);
+  return launch_panel_cfg<1, 4, 4, 1, 3>(g, s, stream, deferred);
 }
 
 // ---------------------------------------------------------------------------
@@ -2025,7 +2028,10 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
 //   1600->1600 35 us (41);
 // * below that, 64 x 64 tiles on 8 waves (each 32 x 16): M = 2048 768->2304
 //   27.5 us (4 waves: 29.3), 3072->768 37 us (40);
-// * the int8 panels stay for M < 2048 at K < 1536, where the two time the same.
+// * the int8 panels stay for M < 2048 at K < 1536, where the two time the same;
+// * at K >= 1536 the 64 x 64 tiles keep a 4-stage ring (two chunks of 32 in
+//   flight): M = 1024 3072->768 25.3 us against 31.5 with 3 stages, which time
+//   the same or better at K = 768 (6 stages: slower everywhere).
 bool f16_gemm_large(int m, int n, int k) {
   const int64_t tiles = int64_t((m + 127) / 128) * ((n + 127) / 128);
   return tiles >= 384 || (k >= 1536 && tiles >= 192);
@@ -2034,6 +2040,7 @@ bool f16_gemm_preferred(int m, int n, int k) { return f16_gemm_large(m, n, k) ||
 
 hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   if (f16_gemm_large(g.m, g.n, g.k)) return launch_f16_cfg<2, 4, 4, 2, 3, 4, 3>(g, s, stream, deferred);
+  if (g.k >= 1536) return launch_f16_cfg<2, 4, 2, 1, 4, 1, 3>(g, s, stream, deferred);
   return launch_f16_cfg<2, 4, 2, 1, 3, 1, 3>(g, s, stream, deferred);
 }
 
@@ -2118,10 +2125,12 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   if (g.canonical && g.w_int8 && g.w_packed && g.k % 64 == 0 && avec && !g.a_p32 && !g.ln_gamma &&
       reinterpret_cast<uintptr_t>(g.w_packed) % 16 == 0) {
     // Batch-invariant rows: the fp16-record or the int8 panel kernel (same MFMA
-    // sequence, same values) at every M, unsplit.  Unsplit, the fp16 records
-    // time at or below the panels at every M (M = 32 768->768: 7.4 vs 9.1 us;
-    // M = 1024 3072->768: 26.1 vs 26.0 us), so they serve whenever present.
-    if (g.w_f16p && reinterpret_cast<uintptr_t>(g.w_f16p) % 16 == 0)
+    // sequence, same values) at every M, unsplit, each where it times faster:
+    // the panels below f16_gemm_preferred's shapes (M = 1024 768->2304 17.5
+    // against 18.3 us, 3072->768 24.7 against 25.3 us), the fp16 records at
+    // the large-tile shapes and M >= 2048 at K < 1536, and at M <= 64
+    // (M = 32 768->768: 7.4 against 9.1 us).
+    if (g.w_f16p && reinterpret_cast<uintptr_t>(g.w_f16p) % 16 == 0 && (g.m <= 64 || f16_gemm_preferred(g.m, g.n, g.k)))
       return launch_f16(g, s, stream, deferred);
     return launch_panel(g, s, stream, deferred);
   }
