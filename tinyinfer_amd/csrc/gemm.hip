@@ -1225,22 +1225,37 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
     __builtin_amdgcn_s_barrier();
     if (c + S - 1 < kc) issue(c + S - 1, (c + S - 1) % S);
     const uint8_t* st = lds + (c % S) * STAGE;
+    // Every LDS read of the chunk is issued first (scales and records, then
+    // the A fragments; LDS reads return in order, so each use waits for its
+    // own read only): the dequantisation runs while the A fragments arrive.
+    float sc[R];
+    u32x4_t raw[R];
+    half8_t af[MT][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      sc[r] = scale_lds[(wn * R + r) * 16 + j];
+      raw[r] = *reinterpret_cast<const u32x4_t*>(st + (NA + wn * R + r) * 1024 + lane * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        af[t][s] = *reinterpret_cast<const half8_t*>(st + (((wm * MT + t) * 2 + s) * 1024) + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
     half8_t bq[R][2];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const float sc = scale_lds[(wn * R + r) * 16 + j];
-      const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(st + (NA + wn * R + r) * 1024 + lane * 16);
-      bq[r][0] = dequant8(raw[0], raw[1], sc);
-      bq[r][1] = dequant8(raw[2], raw[3], sc);
+      bq[r][0] = dequant8(raw[r][0], raw[r][1], sc[r]);
+      bq[r][1] = dequant8(raw[r][2], raw[r][3], sc[r]);
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const half8_t af = *reinterpret_cast<const half8_t*>(st + (((wm * MT + t) * 2 + s) * 1024) + lane * 16);
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bq[r][s], acc[t][r], 0, 0, 0);
-      }
+        for (int r = 0; r < R; ++r)
+          acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][s], bq[r][s], acc[t][r], 0, 0, 0);
   }
   wait_vmcnt<0>();
 
