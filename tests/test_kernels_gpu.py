@@ -381,6 +381,52 @@ def test_f16_packed_prefill_gemm_against_oracle(ops, m, k, n):
     close(h(hbits(res)), expect)
 
 
+@pytest.mark.parametrize("layout", ["row_major", "panel", "f16"])
+@pytest.mark.parametrize("n,off", [(1000, 0), (1000, 1), (998, 0)])
+def test_gemm_tile_epilogue_ragged_and_unaligned(ops, layout, n, off):
+    """The M > 32 GEMMs finish from an LDS tile, 4 columns per thread, with one
+    8-byte store per group when the output allows it.  N = 1000 at offset 0
+    takes the vector stores (a part-filled last tile); the same output one
+    element into its buffer (2-byte aligned) and N = 998 (rows not a multiple
+    of 4 elements, a 2-column group at the edge) take the per-element path.
+    Bias, bias+GELU and in-place residual epilogues of the row-major,
+    int8-panel and fp16-record kernels against the oracle, and nothing
+    written outside the output."""
+    t = torch()
+    m, k = 65, 128
+    rng = np.random.default_rng(n + 7 * off + len(layout))
+    a = f16(rng.standard_normal((m, k)))
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32)
+    bias = f16(rng.standard_normal(n) * 0.02)
+    say("gemm tile epilogue", layout, n, "offset", off)
+    ad, sd, bd = dev(a, t.float16), dev(s), dev(bias, t.float16)
+    if layout == "panel":
+        w = _pack_gpu(ops.lib, dev(q), k, n)
+        run = lambda b_, y_, r_, epi: _packed(ops.lib, ad, w, sd, b_, y_, r_, m, n, k, epi)
+    elif layout == "f16":
+        w = _pack16_gpu(ops.lib, dev(q), sd, k, n)
+        run = lambda b_, y_, r_, epi: _w16(ops.lib, ad, w, b_, y_, r_, m, n, k, epi) == 0 or pytest.fail(
+            ops.lib.ti_v2_last_error())
+    else:
+        qd = dev(q)
+        run = lambda b_, y_, r_, epi: _fused(ops.lib, ad, qd, sd, b_, y_, r_, m, n, k, epi)
+    buf = t.zeros(m * n + 8, dtype=t.float16, device="cuda")
+    y = buf[off:off + m * n].view(m, n)
+    ref = oracle.linear(a, q=q, scales=s, bias_bits=bias)
+    run(bd, y, None, 0)
+    close(h(hbits(y)), h(ref))
+    run(None, y, None, 1)
+    close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, gelu=True)))
+    r0 = f16(rng.standard_normal((m, n)))
+    y.copy_(dev(r0, t.float16))
+    run(bd, y, y, 2)
+    close(h(hbits(y)), (h(r0) + h(ref)).astype(np.float16).astype(np.float64))
+    # Nothing outside the output was written.
+    rest = hbits(buf).astype(np.int64)
+    assert not rest[:off].any() and not rest[off + m * n:].any()
+
+
 def test_f16_packed_gemm_rejects_unsupported_shapes(ops):
     t = torch()
     a = t.zeros((64, 96), dtype=t.float16, device="cuda")
