@@ -355,11 +355,14 @@ def test_pack_w16_layout_bit_exact(ops, k, n):
 
 @pytest.mark.parametrize("m,k,n", [(33, 768, 3072), (64, 3072, 768), (130, 128, 100), (512, 64, 2000),
                                    (512, 768, 3072), (1024, 768, 2304), (2048, 3072, 768), (4100, 1600, 6400),
-                                   (70, 224, 40), (2100, 1632, 1700), (3000, 800, 4000)])
+                                   (70, 224, 40), (2100, 1632, 1700), (3000, 800, 4000), (3000, 4096, 4000),
+                                   (8200, 256, 4000)])
 def test_f16_packed_prefill_gemm_against_oracle(ops, m, k, n):
     """Prefill GEMM over the pre-dequantised fp16 weights: ragged row and column
-    tiles, K a multiple of 32 but not of 64, bias / bias+GELU / in-place residual epilogues against the
-    oracle's int8 linear (the same weight values)."""
+    tiles, K a multiple of 32 but not of 64, the 256 x 256 tiles (K >= 4096,
+    192 of them) and the 256 x 128 tiles (1056 of them), bias / bias+GELU /
+    in-place residual epilogues against the oracle's int8 linear (the same
+    weight values)."""
     t = torch()
     rng = np.random.default_rng(13 * m + k + n)
     a = f16(rng.standard_normal((m, k)))

@@ -2053,8 +2053,26 @@ bool f16_gemm_large(int m, int n, int k) {
 }
 bool f16_gemm_preferred(int m, int n, int k) { return f16_gemm_large(m, n, k) || (m >= 2048 && k < 1536); }
 
+// Larger tiles halve the LDS bytes per MFMA (a wave's 128 x 64 or 128 x 32
+// block reads 12 / 10 KiB per 32 / 16 MFMAs, against 6 KiB per 8 for 64 x 32)
+// but hold one (256 x 256: 96 KiB, 202 registers) or two (256 x 128) 8-wave
+// workgroups per CU, so they win only where the grid fills whole rounds of
+// them (timed on MI355X, XL shapes, graph replays):
+// * 256 x 256 at K >= 4096 when the tiles make one nearly full round:
+//   M = 8192 6400->1600 (224 tiles) 199 us against 256; at 112 tiles 188
+//   against 143, at 294 (two rounds) 388 against 328;
+// * 256 x 128 from four rounds of two per CU at K < 4096: M = 8192
+//   1600->4800 180 against 194 us, 1600->6400 244 against 257, M = 10752
+//   1600->4800 238 against 250, 1600->6400 310 against 326; at 1.2-2 rounds
+//   slower (M = 4096 1600->4800 121 against 110 us).
 hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
-  if (f16_gemm_large(g.m, g.n, g.k)) return launch_f16_cfg<2, 4, 4, 2, 3, 4, 3>(g, s, stream, deferred);
+  if (f16_gemm_large(g.m, g.n, g.k)) {
+    const int64_t cus = device_cus(), rows256 = (g.m + 255) / 256;
+    const int64_t t256 = rows256 * ((g.n + 255) / 256), t256x128 = rows256 * ((g.n + 127) / 128);
+    if (g.k >= 4096 && 4 * t256 >= 3 * cus && t256 <= cus) return launch_f16_cfg<2, 4, 8, 4, 3, 8, 2>(g, s, stream, deferred);
+    if (g.k < 4096 && t256x128 >= 4 * cus) return launch_f16_cfg<2, 4, 8, 2, 3, 8, 2>(g, s, stream, deferred);
+    return launch_f16_cfg<2, 4, 4, 2, 3, 4, 3>(g, s, stream, deferred);
+  }
   if (g.k >= 1536) return launch_f16_cfg<2, 4, 2, 1, 4, 1, 3>(g, s, stream, deferred);
   return launch_f16_cfg<2, 4, 2, 1, 3, 1, 3>(g, s, stream, deferred);
 }
