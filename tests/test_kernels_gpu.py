@@ -209,7 +209,7 @@ def test_pack_w8_layout_bit_exact(ops, k, n):
 
 @pytest.mark.parametrize("m", [1, 8, 17, 32])
 @pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (768, 2304), (128, 100), (64, 50257), (768, 50257),
-                                 (1024, 16400)])
+                                 (1024, 16400), (1600, 6400)])
 def test_packed_gemv_against_oracle(ops, m, k, n):
     """Decode GEMV over panel-packed weights: bias, bias+GELU and in-place residual
     epilogues against the oracle's fp32-accumulate linear."""

@@ -1636,18 +1636,23 @@ hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipS
   return hipErrorInvalidValue;
 }
 
-// M = 1 over packed weights with at most 128 column blocks (N <= 2048): the
-// part-block kernel, 8 columns per workgroup.  W x LPW covers the record pairs
-// in one round up to K = 3072 (timed on GPT-2 small / XL shapes: 768 -> 768
-// 3.07 -> 2.73 us, 3072 -> 768 4.37 -> 3.30 us, 1600 -> 1600 3.95 -> 3.07 us;
-// at 2304 columns and more the MFMA GEMV is as fast or faster).  Not for a
+// M = 1 over packed weights with at most 128 column blocks (N <= 2048), or
+// any N from K = 1536: the part-block kernel, 8 columns per workgroup.  W x LPW
+// covers the record pairs in one round up to K = 3072 (timed on GPT-2 small /
+// XL shapes: 768 -> 768 3.07 -> 2.73 us, 3072 -> 768 4.37 -> 3.30 us, 1600 ->
+// 1600 3.95 -> 3.07 us; wider, it wins from K = 1536 on: 1600 -> 3072 4.17 ->
+// 3.76 us, 3072 -> 3072 5.11 -> 4.51 us, 1600 -> 6400 5.66 -> 5.35 us, 1600 ->
+// 50257 26.4 -> 24.0 us, and ties or loses below: 768 -> 3072 3.24 either way,
+// 1024 -> 3072 3.45 against 3.58 us).  Not for a
 // batching caller's decode (GemmArgs::decode_batches): there one kernel family
 // serves every M up to 16, so a row's sums do not depend on the batch; the
 // part-block kernel with several rows per workgroup measured slower than the
 // MFMA GEMV from two rows up (b = 8 decode 25.8 K against 26.6 K tok/s, b = 16
 // 44 K against 51 K).
 bool part_gemv_preferred(const GemmArgs& g) {
-  return g.m == 1 && !g.a_p32 && !g.ln_gamma && !g.decode_batches && (g.n + 15) / 16 <= 128;
+  // (A caller that wants argmax partials keeps the MFMA GEMV, which writes them.)
+  return g.m == 1 && !g.a_p32 && !g.ln_gamma && !g.decode_batches && !g.amax_groups &&
+         ((g.n + 15) / 16 <= 128 || g.k >= 1536);
 }
 
 hipError_t launch_part(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
