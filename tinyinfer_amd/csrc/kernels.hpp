@@ -90,6 +90,13 @@ struct GemmArgs {
   // family and K split are the same for every M up to 16, so a row's sums do
   // not depend on the batch (the single-row part-block GEMV is not used).
   bool decode_batches = false;
+  // Optional padded-batch row map for the M > 32 MFMA GEMMs: row b * row_pitch
+  // + t of A and of the output is a real row iff t < row_lens[b] (the
+  // runtime's ragged prefill, one request per row_pitch rows).  Row tiles that
+  // hold no real row are skipped: their outputs are left as they were (padding
+  // rows feed only padding rows).
+  const int32_t* row_lens = nullptr;
+  int row_pitch = 0;
   // Another decode lane reads the same packed weights right after this launch
   // (the runtime's two-lane decode over cache-resident weights): the GEMV of
   // up to 16 rows reads them with cached loads instead of streaming them.

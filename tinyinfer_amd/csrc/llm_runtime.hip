@@ -709,6 +709,8 @@ struct ti_llm_model {
     g.ln_eps = 1e-5f;
     g.epi = epi;
     g.canonical = prefill_pass;
+    g.row_lens = row_lens;
+    g.row_pitch = row_pitch;
     g.decode_batches = !prefill_pass;
     g.weights_shared = !prefill_pass && lane_count > 1;  // two lanes stream the same records
     g.defer_workgroups = defer_workgroups;
@@ -723,6 +725,11 @@ struct ti_llm_model {
   // construction: one kernel and one K split per shape for every M up to 16
   // (tia::GemmArgs::decode_batches).
   bool prefill_pass = false;
+  // The padded row map of the prefill pass in progress (rows b * qlen + t, real
+  // iff t < qlens[b]): its GEMMs skip row tiles of padding only.  Null outside
+  // layers().
+  const int32_t* row_lens = nullptr;
+  int row_pitch = 0;
 
   // x += a @ w + bias (fp16 rounding points of reference runtime.cu:149/153), then
   // norm = LayerNorm(x; g, beta).  Decode-sized GEMMs leave split-K partials that
@@ -793,6 +800,8 @@ struct ti_llm_model {
   void layers(int b, int qlen, bool embedded = false) {
     const int rows = b * qlen;
     prefill_pass = qlen > 1;
+    row_lens = prefill_pass && b > 1 ? d_qlens : nullptr;
+    row_pitch = qlen;
     const bool fuse = ln_fused(b, qlen);
     const bool p32 = p32_pass(b, qlen);
     norm_p32 = p32;
@@ -908,6 +917,7 @@ struct ti_llm_model {
         ck(p32 ? tia::layernorm_f16_p32(x, lnf_g, lnf_b, norm, rows, H, 1e-5f, stream)
                : tia::layernorm_f16(x, lnf_g, lnf_b, norm, rows, H, 1e-5f, stream));
     }
+    row_lens = nullptr;
   }
 
   // Logits of each request's last row (norm already holds ln_f), fp32 without
