@@ -25,6 +25,17 @@ namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
+// Offset of query row qi of request b in q or out (batch stride sb, row stride
+// sq): b * sb + qi * sq, or (q_row_start[b] + qi) * sq over compact rows.
+__device__ __forceinline__ int64_t query_row(const AttnArgs& a, int b, int qi, int64_t sb, int64_t sq) {
+  return a.q_row_start ? (int64_t(a.q_row_start[b]) + qi) * sq : int64_t(b) * sb + int64_t(qi) * sq;
+}
+// Queries of request b whose output rows are written: its q_len slots, or over
+// compact rows (where the next request's rows follow) only its q_valid own.
+__device__ __forceinline__ int written_queries(const AttnArgs& a, int q_valid) {
+  return a.q_row_start ? q_valid : a.q_len;
+}
+
 struct AttnParams {
   AttnArgs a;
   float scale;
@@ -158,7 +169,7 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   // Unfused: q is re-read with each pair of tiles (an L2 hit after the first)
   // rather than once up front, which would make the compiler wait for it
   // before issuing any K/V load.
-  const uint16_t* qptr = a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(qi) * a.q_sq + 8 * ds;
+  const uint16_t* qptr = a.q + query_row(a, b, qi, a.q_sb, a.q_sq) + int64_t(h) * a.q_sh + 8 * ds;
 
   float m = kNegInf, l = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -303,10 +314,10 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
     for (int e = 0; e < 8; ++e) part[2 + 8 * ds + e] = acc[e];
     return;
   }
-  if (qi >= a.q_len || kg != 0) return;
+  if (qi >= written_queries(a, q_valid) || kg != 0) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   uint16_t* op = a.out + (a.out_p32 ? p32_off(b * a.q_len + qi, h * D + 8 * ds)
-                                    : int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(qi) * a.o_sq + 8 * ds);
+                                    : query_row(a, b, qi, a.o_sb, a.o_sq) + int64_t(h) * a.o_sh + 8 * ds);
   half8_t o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = f16r(l > 0.f ? acc[e] * inv : 0.f);
@@ -457,7 +468,7 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
 #pragma unroll
   for (int u = 0; u < QB; ++u) {
     const uint16_t* qp =
-        a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + int64_t(min(my_q[u], max(q_valid, 1) - 1)) * a.q_sq;
+        a.q + query_row(a, b, min(my_q[u], max(q_valid, 1) - 1), a.q_sb, a.q_sq) + int64_t(h) * a.q_sh;
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) {
       qf[u][s] = *reinterpret_cast<const half8_t*>(qp + 32 * s + 8 * g);
@@ -669,10 +680,10 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
 
 #pragma unroll
   for (int u = 0; u < QB; ++u) {
-    if (my_q[u] >= a.q_len) continue;
+    if (my_q[u] >= written_queries(a, q_valid)) continue;
     const float l = accl[u][0];
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + int64_t(my_q[u]) * a.o_sq;
+    uint16_t* op = a.out + query_row(a, b, my_q[u], a.o_sb, a.o_sq) + int64_t(h) * a.o_sh;
 #pragma unroll
     for (int d = 0; d < D / 16; ++d) {
       half4_t o;

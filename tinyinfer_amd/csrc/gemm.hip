@@ -62,13 +62,31 @@ __device__ __forceinline__ int64_t r_off(const Epilogue& e, int m, int n) {
   return e.p32 ? p32_off(m, n) : int64_t(m) * e.ldr + n;
 }
 
-// EPI_QKV element (m, n) = acc + bias: fp16 into y, and for the K and V
-// columns of a real token the same bits into the slot cache.
-__device__ __forceinline__ void qkv_store(const Epilogue& e, int m, int n, float val) {
+// Request b and token t of row m of an EPI_QKV output: m = b * qrows + t, or
+// m = row_start[b] + t over compact rows (a binary search of row_start).
+__device__ __forceinline__ void qkv_row(const Epilogue& e, int m, int& b, int& t) {
+  if (e.row_start) {
+    int lo = 0, hi = e.batch;  // row_start[lo] <= m < row_start[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (e.row_start[mid] <= m) lo = mid;
+      else hi = mid;
+    }
+    b = lo;
+    t = m - e.row_start[lo];
+  } else {
+    b = m / e.qrows;
+    t = m - b * e.qrows;
+  }
+}
+
+// EPI_QKV element (m, n) = acc + bias of token t of request b: fp16 into y,
+// and for the K and V columns of a real token the same bits into the slot
+// cache.
+__device__ __forceinline__ void qkv_store_bt(const Epilogue& e, int b, int t, int m, int n, float val) {
   const uint16_t hv = f2h(val);
   static_cast<uint16_t*>(e.y)[int64_t(m) * e.ldy + n] = hv;
   if (n >= e.hidden) {
-    const int b = m / e.qrows, t = m - b * e.qrows;
     if (t < e.qlens[b]) {
       const int part = n >= 2 * e.hidden ? 2 : 1;
       const int c = n - part * e.hidden, h = c >> 6, d = c & 63;
@@ -77,6 +95,12 @@ __device__ __forceinline__ void qkv_store(const Epilogue& e, int m, int n, float
       (part == 1 ? e.kcache : e.vcache)[idx] = hv;
     }
   }
+}
+
+__device__ __forceinline__ void qkv_store(const Epilogue& e, int m, int n, float val) {
+  int b, t;
+  qkv_row(e, m, b, t);
+  qkv_store_bt(e, b, t, m, n, val);
 }
 
 // `bias` is epilogue_bias(e, n) (callers may load it early); EPI_RAW_F32 ignores it.
@@ -959,8 +983,6 @@ struct PanelParams {
   int64_t lda;
   const u32x4_t* w;     // panel-packed records
   const float* scales;  // fp32 [N]
-  const int32_t* row_lens;  // GemmArgs::row_lens / row_pitch
-  int row_pitch;
   int m, n, k;
   int nb, kc;           // column blocks, K chunks
   int tiles_n, tiles;   // tiles per row of tiles, tiles per split
@@ -1071,9 +1093,11 @@ __device__ __forceinline__ void tile_epilogue(const Epilogue& e, const float* ct
         const int row = row_of(i);
         if (row >= m) break;
         const float4_t v = sums(i);
+        int rb, rt;
+        qkv_row(e, row, rb, rt);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-          if (col + c < n) qkv_store(e, row, col + c, v[c] + bias[c]);
+          if (col + c < n) qkv_store_bt(e, rb, rt, row, col + c, v[c] + bias[c]);
       }
       return;
     default:
@@ -1134,26 +1158,6 @@ __device__ __forceinline__ void tile_epilogue(const Epilogue& e, const float* ct
   else rows_f16([&](float x, int c) { return x + bias[c]; });
 }
 
-// Whether rows [m0, m0 + BM) hold a real row of a padded batch (row b * pitch
-// + t is real iff t < lens[b]; no map: every row is).  Each wave tests all BM
-// rows, so the answer is uniform over the workgroup and a tile without real
-// rows can return before its first load or barrier.
-template <int BM>
-__device__ __forceinline__ bool tile_has_rows(const int32_t* lens, int pitch, int m0, int m) {
-  if (!lens || pitch <= 0) return true;
-  const int lane = threadIdx.x & 63;
-  bool real = false;
-#pragma unroll
-  for (int i = 0; i < (BM + 63) / 64; ++i) {
-    const int r = lane + 64 * i, row = m0 + r;
-    if (r < BM && row < m) {
-      const int b = row / pitch;
-      real = real || row - b * pitch < lens[b];
-    }
-  }
-  return __any(real);
-}
-
 // Workgroup -> (split, tile row, tile column).  Workgroups are dispatched to
 // the 8 XCDs round-robin by id, so ids are first regrouped into 8 contiguous
 // runs (one per XCD); within a split, tiles are walked in groups of GM tile
@@ -1187,7 +1191,6 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
   int split, tm, tn;
   tile_of_block(p.group_m, p.tiles_n, p.tiles, split, tm, tn);
   const int m0 = tm * BM, cb0 = tn * NB;
-  if (!tile_has_rows<BM>(p.row_lens, p.row_pitch, m0, p.m)) return;
   const int c_begin = split * p.chunks_per_split;
   const int kc = min(p.kc - c_begin, p.chunks_per_split);  // chunks of this split (>= 1)
 
@@ -1822,7 +1825,6 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
   if (attr != hipSuccess) return attr;
   PanelParams p{};
   p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
-  p.row_lens = g.row_lens; p.row_pitch = g.row_pitch;
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.nb = (g.n + 15) / 16;
   p.kc = g.k / 64;
@@ -1888,8 +1890,6 @@ struct F16GemmParams {
   const uint16_t* a;
   int64_t lda;
   const u32x4_t* w;  // fp16 B records
-  const int32_t* row_lens;  // GemmArgs::row_lens / row_pitch
-  int row_pitch;
   int m, n, k;
   int kk;            // K groups of 32
   int tiles_n, tiles;
@@ -1939,7 +1939,6 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void f16_gemm_kernel(F16GemmPara
   int split, tm, tn;
   tile_of_block(p.group_m, p.tiles_n, p.tiles, split, tm, tn);
   const int m0 = tm * BM, cb0 = tn * NB;
-  if (!tile_has_rows<BM>(p.row_lens, p.row_pitch, m0, p.m)) return;
   const int nbt = (p.n + 15) / 16;
   const int c_begin = split * p.chunks_per_split;
   const int kc = min(p.kk - c_begin, p.chunks_per_split);  // chunks of this split (>= 1)
@@ -2033,7 +2032,6 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
   if (attr != hipSuccess) return attr;
   F16GemmParams p{};
   p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_f16p);
-  p.row_lens = g.row_lens; p.row_pitch = g.row_pitch;
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.kk = (g.k + 31) / 32;
   p.tiles_n = (g.n + BN - 1) / BN;
@@ -2102,12 +2100,8 @@ hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, i
   if (f16_gemm_large(g.m, g.n, g.k)) {
     const int64_t cus = device_cus(), rows256 = (g.m + 255) / 256;
     const int64_t t256 = rows256 * ((g.n + 255) / 256), t256x128 = rows256 * ((g.n + 127) / 128);
-    // (A padded batch keeps 128-row tiles: more of them hold padding only and
-    // are skipped.)
-    const bool whole = !g.row_lens;
-    if (whole && g.k >= 4096 && 4 * t256 >= 3 * cus && t256 <= cus)
-      return launch_f16_cfg<2, 4, 8, 4, 3, 8, 2>(g, s, stream, deferred);
-    if (whole && g.k < 4096 && t256x128 >= 4 * cus) return launch_f16_cfg<2, 4, 8, 2, 3, 8, 2>(g, s, stream, deferred);
+    if (g.k >= 4096 && 4 * t256 >= 3 * cus && t256 <= cus) return launch_f16_cfg<2, 4, 8, 4, 3, 8, 2>(g, s, stream, deferred);
+    if (g.k < 4096 && t256x128 >= 4 * cus) return launch_f16_cfg<2, 4, 8, 2, 3, 8, 2>(g, s, stream, deferred);
     return launch_f16_cfg<2, 4, 4, 2, 3, 4, 3>(g, s, stream, deferred);
   }
   if (g.k >= 1536) return launch_f16_cfg<2, 4, 2, 1, 4, 1, 3>(g, s, stream, deferred);

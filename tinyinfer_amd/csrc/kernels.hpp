@@ -35,6 +35,11 @@ struct Epilogue {
   const int32_t* offsets = nullptr;
   const int32_t* qlens = nullptr;
   int qrows = 1, hidden = 0, heads = 0, layer = 0, layers = 0, capacity = 0;
+  // Compact rows (a ragged prefill without padding): row row_start[b] + t holds
+  // token t of request b, row_start[0..batch] ascending, row_start[batch] = M;
+  // qrows is then ignored.
+  const int32_t* row_start = nullptr;
+  int batch = 0;
   // EPI_F16 / EPI_GELU / EPI_RESIDUAL: y (and residual) are P32 fragment-packed
   // (common.hpp p32_off) instead of row-major; ldy / ldr are ignored.
   bool p32 = false;
@@ -90,13 +95,6 @@ struct GemmArgs {
   // family and K split are the same for every M up to 16, so a row's sums do
   // not depend on the batch (the single-row part-block GEMV is not used).
   bool decode_batches = false;
-  // Optional padded-batch row map for the M > 32 MFMA GEMMs: row b * row_pitch
-  // + t of A and of the output is a real row iff t < row_lens[b] (the
-  // runtime's ragged prefill, one request per row_pitch rows).  Row tiles that
-  // hold no real row are skipped: their outputs are left as they were (padding
-  // rows feed only padding rows).
-  const int32_t* row_lens = nullptr;
-  int row_pitch = 0;
   // Another decode lane reads the same packed weights right after this launch
   // (the runtime's two-lane decode over cache-resident weights): the GEMV of
   // up to 16 rows reads them with cached loads instead of streaming them.
@@ -196,6 +194,10 @@ struct AttnArgs {
   // Several queries per request: one kernel variant whatever the grid, so a
   // query's result does not depend on the other requests of the call.
   bool batch_invariant = false;
+  // Compact query rows (a ragged prefill without padding): query qi of request
+  // b is q row q_row_start[b] + qi and out row likewise (q_sb / o_sb ignored),
+  // and only its q_lengths[b] queries are written.
+  const int32_t* q_row_start = nullptr;
 };
 // With a scratch, single-query attention over a long cache (kv_len 512 ..
 // 4096 for head_dim 64, 256 .. 2048 for 128) splits the keys of each (b, h)

@@ -95,15 +95,17 @@ struct DeviceScope {
 };
 
 // ---------------------------------------------------------------- kernels
-// out[b] = x[b * qlen + qlens[b] - 1] (reference runtime.cu:56-58).
-__global__ void gather_last_kernel(const uint16_t* x, uint16_t* out, const int32_t* qlens, int batch,
-                                   int qlen, int hidden) {
+// out[b] = x[b * qlen + qlens[b] - 1] (reference runtime.cu:56-58), or
+// x[row_start[b] + qlens[b] - 1] over compact rows.
+__global__ void gather_last_kernel(const uint16_t* x, uint16_t* out, const int32_t* qlens,
+                                   const int32_t* row_start, int batch, int qlen, int hidden) {
   const int per_row = hidden / 8;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= batch * per_row) return;
   const int b = i / per_row, c = (i % per_row) * 8;
+  const int64_t first = row_start ? int64_t(row_start[b]) : int64_t(b) * qlen;  // compact or padded rows
   *reinterpret_cast<tia::half8_t*>(out + int64_t(b) * hidden + c) =
-      *reinterpret_cast<const tia::half8_t*>(x + (int64_t(b) * qlen + qlens[b] - 1) * hidden + c);
+      *reinterpret_cast<const tia::half8_t*>(x + (first + qlens[b] - 1) * hidden + c);
 }
 
 // One embedding row, x = fp16(wte[id] + wpe[pos]) (zeros when !valid;
@@ -162,16 +164,27 @@ __device__ __forceinline__ void embed_ln_row(int lane, bool valid, int id, int p
   }
 }
 
-// Embedding rows of a pass, row = b * qlen + t, position offsets[b] + t, zero
-// for t >= qlens[b]: one wave per row.
+// Embedding rows of a pass, row = b * qlen + t (or, over compact rows,
+// row_start[b] + t), position offsets[b] + t, zero for t >= qlens[b]: one wave
+// per row.
 __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t* ids, const int32_t* qlens,
-                                                       const int32_t* offsets, const uint16_t* wte,
-                                                       const uint16_t* wpe, const uint16_t* g, const uint16_t* bt,
-                                                       uint16_t* x, uint16_t* norm, int rows, int qlen, int hidden,
-                                                       bool p32) {
+                                                       const int32_t* offsets, const int32_t* row_start, int batch,
+                                                       const uint16_t* wte, const uint16_t* wpe, const uint16_t* g,
+                                                       const uint16_t* bt, uint16_t* x, uint16_t* norm, int rows,
+                                                       int qlen, int hidden, bool p32) {
   const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int b = row / qlen, t = row - b * qlen;
+  int b = row / qlen, t = row - b * qlen;
+  if (row_start) {
+    int lo = 0, hi = batch;  // row_start[lo] <= row < row_start[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (row_start[mid] <= row) lo = mid;
+      else hi = mid;
+    }
+    b = lo;
+    t = row - row_start[lo];
+  }
   const bool valid = t < qlens[b];
   const int id = valid ? ids[row] : 0, pos = valid ? offsets[b] + t : 0;
   embed_ln_row(lane, valid, id, pos, wte, wpe, g, bt, x, norm, row, hidden, p32);
@@ -383,7 +396,8 @@ struct ti_llm_model {
   uint16_t *x = nullptr, *norm = nullptr, *qkv = nullptr, *attn = nullptr, *mlp = nullptr, *last = nullptr;
   uint16_t *kc = nullptr, *vc = nullptr;
   float* logits = nullptr;
-  int32_t *d_meta = nullptr, *d_ids = nullptr, *d_slots = nullptr, *d_qlens = nullptr, *d_offsets = nullptr;
+  int32_t *d_meta = nullptr, *d_ids = nullptr, *d_slots = nullptr, *d_qlens = nullptr, *d_offsets = nullptr,
+          *d_row_start = nullptr;
   int32_t *d_next = nullptr, *d_score_tokens = nullptr;
   // Greedy partials of the wide head GEMV: [group][32] (value, column).
   static constexpr size_t kAmaxEntries = size_t(4096) * 32;
@@ -391,7 +405,8 @@ struct ti_llm_model {
   int32_t* d_amax_i = nullptr;
   uint8_t* d_score_mask = nullptr;
   double *d_loss = nullptr, *d_loss_sum = nullptr;
-  int32_t *h_meta = nullptr, *h_ids = nullptr, *h_slots = nullptr, *h_qlens = nullptr, *h_offsets = nullptr;
+  int32_t *h_meta = nullptr, *h_ids = nullptr, *h_slots = nullptr, *h_qlens = nullptr, *h_offsets = nullptr,
+          *h_row_start = nullptr;
   int32_t* h_next = nullptr;
   size_t meta_ints = 0;
   tia::Scratch scratch;
@@ -449,17 +464,19 @@ struct ti_llm_model {
     h_meta = l.h_meta; h_next = l.h_next;
     scratch = l.scratch;
     norm_p32 = l.norm_p32;
-    // The metadata layout ids[rows] | slots[B] | qlens[B] | offsets[B] of each
-    // lane, B = max_batch.
+    // The metadata layout ids[rows] | slots[B] | qlens[B] | offsets[B] |
+    // row_start[B + 1] of each lane, B = max_batch.
     const size_t rows = i == 0 ? std::max<size_t>(size_t(opt.max_batch) * opt.capacity, 32) : 32;
     d_ids = d_meta;
     d_slots = d_ids + rows;
     d_qlens = d_slots + opt.max_batch;
     d_offsets = d_qlens + opt.max_batch;
+    d_row_start = d_offsets + opt.max_batch;
     h_ids = h_meta;
     h_slots = h_ids + rows;
     h_qlens = h_slots + opt.max_batch;
     h_offsets = h_qlens + opt.max_batch;
+    h_row_start = h_offsets + opt.max_batch;
   }
 
   template <class T>
@@ -617,13 +634,15 @@ struct ti_llm_model {
     kc = alloc<uint16_t>(cache);
     vc = alloc<uint16_t>(cache);
     logits = alloc<float>(size_t(std::max(opt.max_batch, kScoreRows)) * size_t(head.ldw));
-    // Step metadata: ids[rows] | slots[B] | qlens[B] | offsets[B], mirrored in pinned host memory.
-    meta_ints = rows + 3 * size_t(opt.max_batch);
+    // Step metadata: ids[rows] | slots[B] | qlens[B] | offsets[B] | row_start[B + 1],
+    // mirrored in pinned host memory.
+    meta_ints = rows + 4 * size_t(opt.max_batch) + 1;
     d_meta = alloc<int32_t>(meta_ints);
     d_ids = d_meta;
     d_slots = d_ids + rows;
     d_qlens = d_slots + opt.max_batch;
     d_offsets = d_qlens + opt.max_batch;
+    d_row_start = d_offsets + opt.max_batch;
     d_next = alloc<int32_t>(opt.max_batch);
     d_amax_v = alloc<float>(kAmaxEntries);
     d_amax_i = alloc<int32_t>(kAmaxEntries);
@@ -637,6 +656,7 @@ struct ti_llm_model {
     h_slots = h_ids + rows;
     h_qlens = h_slots + opt.max_batch;
     h_offsets = h_qlens + opt.max_batch;
+    h_row_start = h_offsets + opt.max_batch;
     h_next = h_meta + meta_ints;
     scratch.partials = alloc<float>(tia::kScratchPartialFloats);
     scratch.partial_floats = tia::kScratchPartialFloats;
@@ -660,7 +680,7 @@ struct ti_llm_model {
       l.mlp = alloc<uint16_t>(32 * 4 * size_t(H));
       l.last = alloc<uint16_t>(32 * size_t(H));
       l.logits = alloc<float>(size_t(kLaneRows) * size_t(head.ldw));
-      const size_t ints = 32 + 3 * size_t(opt.max_batch);
+      const size_t ints = 32 + 4 * size_t(opt.max_batch) + 1;
       l.d_meta = alloc<int32_t>(ints);
       l.d_next = alloc<int32_t>(opt.max_batch);
       l.d_amax_v = alloc<float>(kAmaxEntries);
@@ -709,8 +729,6 @@ struct ti_llm_model {
     g.ln_eps = 1e-5f;
     g.epi = epi;
     g.canonical = prefill_pass;
-    g.row_lens = row_lens;
-    g.row_pitch = row_pitch;
     g.decode_batches = !prefill_pass;
     g.weights_shared = !prefill_pass && lane_count > 1;  // two lanes stream the same records
     g.defer_workgroups = defer_workgroups;
@@ -725,11 +743,10 @@ struct ti_llm_model {
   // construction: one kernel and one K split per shape for every M up to 16
   // (tia::GemmArgs::decode_batches).
   bool prefill_pass = false;
-  // The padded row map of the prefill pass in progress (rows b * qlen + t, real
-  // iff t < qlens[b]): its GEMMs skip row tiles of padding only.  Null outside
-  // layers().
-  const int32_t* row_lens = nullptr;
-  int row_pitch = 0;
+  // Rows of the next pass when its requests' tokens are compact (request b at
+  // rows row_start[b] .. row_start[b] + qlens[b] - 1 of x, norm, qkv, attn,
+  // mlp; d_row_start uploaded), 0 when a pass is b x qlen rows.
+  int compact_rows = 0;
 
   // x += a @ w + bias (fp16 rounding points of reference runtime.cu:149/153), then
   // norm = LayerNorm(x; g, beta).  Decode-sized GEMMs leave split-K partials that
@@ -789,19 +806,20 @@ struct ti_llm_model {
 
   // Embedding rows and layer 0's ln_1 of a pass whose metadata is on the device.
   void embed(int b, int qlen) {
-    const int rows = b * qlen;
-    embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets, wte, wpe, ln1_g[0],
-                                                             ln1_b[0], x, norm, rows, qlen, H, p32_pass(b, qlen));
+    const int rows = compact_rows ? compact_rows : b * qlen;
+    embed_ln_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(d_ids, d_qlens, d_offsets,
+                                                             compact_rows ? d_row_start : nullptr, b, wte, wpe,
+                                                             ln1_g[0], ln1_b[0], x, norm, rows, qlen, H,
+                                                             p32_pass(b, qlen));
     ck(hipGetLastError());
   }
 
   // `embedded`: x and norm already hold the embedding rows (the previous
   // decode step's greedy_feed_kernel, or embed()).
   void layers(int b, int qlen, bool embedded = false) {
-    const int rows = b * qlen;
+    const int rows = compact_rows ? compact_rows : b * qlen;
+    const int32_t* row_start = compact_rows ? d_row_start : nullptr;
     prefill_pass = qlen > 1;
-    row_lens = prefill_pass && b > 1 ? d_qlens : nullptr;
-    row_pitch = qlen;
     const bool fuse = ln_fused(b, qlen);
     const bool p32 = p32_pass(b, qlen);
     norm_p32 = p32;
@@ -837,6 +855,8 @@ struct ti_llm_model {
       e.offsets = d_offsets;
       e.qlens = d_qlens;
       e.qrows = qlen;
+      e.row_start = row_start;
+      e.batch = b;
       e.hidden = H;
       e.heads = NH;
       e.layer = l;
@@ -867,6 +887,7 @@ struct ti_llm_model {
       at.kv_sh = head_stride;
       at.kv_slot = d_slots;
       at.out = attn;
+      at.q_row_start = row_start;
       at.o_sb = int64_t(qlen) * H;
       at.o_sh = kHeadDim;
       at.o_sq = H;
@@ -917,7 +938,6 @@ struct ti_llm_model {
         ck(p32 ? tia::layernorm_f16_p32(x, lnf_g, lnf_b, norm, rows, H, 1e-5f, stream)
                : tia::layernorm_f16(x, lnf_g, lnf_b, norm, rows, H, 1e-5f, stream));
     }
-    row_lens = nullptr;
   }
 
   // Logits of each request's last row (norm already holds ln_f), fp32 without
@@ -926,7 +946,8 @@ struct ti_llm_model {
   void head_and_argmax(int b, int qlen, bool greedy, bool feed = false) {
     const uint16_t* rows_in = norm;
     if (qlen > 1) {
-      gather_last_kernel<<<blocks_for(int64_t(b) * H / 8), 256, 0, stream>>>(norm, last, d_qlens, b, qlen, H);
+      gather_last_kernel<<<blocks_for(int64_t(b) * H / 8), 256, 0, stream>>>(
+          norm, last, d_qlens, compact_rows ? d_row_start : nullptr, b, qlen, H);
       ck(hipGetLastError());
       rows_in = last;
     }
@@ -990,10 +1011,11 @@ struct ti_llm_model {
     if (greedy) ++trace.argmax;
   }
 
-  void upload_meta(int b, int qlen) {
+  // `ids`: the token rows of the pass (b x qlen padded, or the compact count).
+  void upload_meta(size_t ids) {
     const size_t rows = size_t(opt.max_batch) * opt.capacity;
-    ck(hipMemcpyAsync(d_ids, h_ids, size_t(b) * qlen * sizeof(int32_t), hipMemcpyHostToDevice, stream));
-    ck(hipMemcpyAsync(d_slots, h_slots, 3 * size_t(opt.max_batch) * sizeof(int32_t), hipMemcpyHostToDevice,
+    ck(hipMemcpyAsync(d_ids, h_ids, ids * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+    ck(hipMemcpyAsync(d_slots, h_slots, (4 * size_t(opt.max_batch) + 1) * sizeof(int32_t), hipMemcpyHostToDevice,
                       stream));
     (void)rows;
   }
@@ -1042,14 +1064,28 @@ struct ti_llm_model {
         if (tokens[int64_t(i) * stride + j] < 0 || tokens[int64_t(i) * stride + j] >= V)
           throw Invalid("token ID outside the model vocabulary");
     }
+    // A ragged prefill runs over compact rows (request i's tokens at rows
+    // row_start[i] ..), not padded to the longest prompt: the GEMMs, row
+    // kernels and attention then do no work for padding.
+    const bool compact = b > 1 && qlen > 1 && std::any_of(lens, lens + b, [&](int32_t n) { return n != qlen; });
+    int rows = 0;
     for (int i = 0; i < b; ++i) {
-      for (int j = 0; j < qlen; ++j) h_ids[int64_t(i) * qlen + j] = j < lens[i] ? tokens[int64_t(i) * stride + j] : 0;
+      h_row_start[i] = rows;
+      if (compact) {
+        for (int j = 0; j < lens[i]; ++j) h_ids[rows + j] = tokens[int64_t(i) * stride + j];
+        rows += lens[i];
+      } else {
+        for (int j = 0; j < qlen; ++j) h_ids[int64_t(i) * qlen + j] = j < lens[i] ? tokens[int64_t(i) * stride + j] : 0;
+        rows += qlen;
+      }
       h_slots[i] = s[i];
       h_qlens[i] = lens[i];
       h_offsets[i] = lengths[s[i]];
     }
+    h_row_start[b] = rows;
     const bool need_head = out || greedy;
-    upload_meta(b, qlen);
+    upload_meta(size_t(rows));
+    compact_rows = compact ? rows : 0;
     if (qlen == 1 && greedy) {
       embed(b, 1);
       decode_step_graph(b);
@@ -1057,6 +1093,7 @@ struct ti_llm_model {
       layers(b, qlen);
       if (need_head) head_and_argmax(b, qlen, greedy != nullptr);
     }
+    compact_rows = 0;
     count_forward(need_head, greedy != nullptr);
     if (out)
       ck(hipMemcpy2DAsync(out, size_t(V) * sizeof(float), logits, size_t(head.ldw) * sizeof(float),
@@ -1092,7 +1129,7 @@ struct ti_llm_model {
         h_qlens[j] = 1;
         h_offsets[j] = lengths[s[i]];
       }
-      upload_meta(count[l], 1);
+      upload_meta(size_t(count[l]));
       embed(count[l], 1);
     }
     for (int t = 0; t < steps; ++t)
@@ -1145,7 +1182,7 @@ struct ti_llm_model {
     h_slots[0] = slot;
     h_qlens[0] = q;
     h_offsets[0] = 0;
-    upload_meta(1, q);
+    upload_meta(size_t(q));
     layers(1, q);  // leaves ln_f of every row in norm
     ++trace.forward_calls;
     ++trace.embedding;
