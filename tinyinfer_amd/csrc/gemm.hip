@@ -1087,7 +1087,13 @@ __device__ __forceinline__ void tile_epilogue(const Epilogue& e, const float* ct
     case EPI_F32:
       store_f32(static_cast<float*>(e.y), e.ldy, [&](float x, int c) { return x + bias[c]; });
       return;
-    case EPI_QKV:
+    case EPI_QKV: {
+      // Per row: the request, its token and cache position once; a full
+      // 4-column group (one head: hidden % 64 == 0) goes to y and, for a K or
+      // V column of a real token, to the slot cache as one 8-byte store each.
+      uint16_t* y = static_cast<uint16_t*>(e.y);
+      const bool vec = full && e.ldy % 4 == 0 && aligned(y, 8) && aligned(e.kcache, 8) && aligned(e.vcache, 8) &&
+                       e.hidden % 64 == 0;
 #pragma unroll 1
       for (int i = 0; i < RPT; ++i) {
         const int row = row_of(i);
@@ -1095,11 +1101,25 @@ __device__ __forceinline__ void tile_epilogue(const Epilogue& e, const float* ct
         const float4_t v = sums(i);
         int rb, rt;
         qkv_row(e, row, rb, rt);
+        if (!vec) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          if (col + c < n) qkv_store_bt(e, rb, rt, row, col + c, v[c] + bias[c]);
+          for (int c = 0; c < 4; ++c)
+            if (col + c < n) qkv_store_bt(e, rb, rt, row, col + c, v[c] + bias[c]);
+          continue;
+        }
+        const half4_t h4 = {f16r(v[0] + bias[0]), f16r(v[1] + bias[1]), f16r(v[2] + bias[2]), f16r(v[3] + bias[3])};
+        *reinterpret_cast<half4_t*>(y + int64_t(row) * e.ldy + col) = h4;
+        if (col >= e.hidden && rt < e.qlens[rb]) {
+          const int part = col >= 2 * e.hidden ? 2 : 1;
+          const int c = col - part * e.hidden, hd = c >> 6, d = c & 63;
+          const int64_t pos = int64_t(e.offsets[rb]) + rt;
+          const int64_t idx =
+              (((int64_t(e.slots[rb]) * e.layers + e.layer) * e.heads + hd) * e.capacity + pos) * 64 + d;
+          *reinterpret_cast<half4_t*>((part == 1 ? e.kcache : e.vcache) + idx) = h4;
+        }
       }
       return;
+    }
     default:
       break;
   }
@@ -2095,13 +2115,15 @@ bool f16_gemm_preferred(int m, int n, int k) { return f16_gemm_large(m, n, k) ||
 // * 256 x 128 from four rounds of two per CU at K < 4096: M = 8192
 //   1600->4800 180 against 194 us, 1600->6400 244 against 257, M = 10752
 //   1600->4800 238 against 250, 1600->6400 310 against 326; at 1.2-2 rounds
-//   slower (M = 4096 1600->4800 121 against 110 us).
+//   slower (M = 4096 1600->4800 121 against 110 us).  Its occupancy (two
+//   8-wave workgroups per CU) needs <= 128 registers, held by the launch
+//   bound (a few epilogue values spill).
 hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   if (f16_gemm_large(g.m, g.n, g.k)) {
     const int64_t cus = device_cus(), rows256 = (g.m + 255) / 256;
     const int64_t t256 = rows256 * ((g.n + 255) / 256), t256x128 = rows256 * ((g.n + 127) / 128);
     if (g.k >= 4096 && 4 * t256 >= 3 * cus && t256 <= cus) return launch_f16_cfg<2, 4, 8, 4, 3, 8, 2>(g, s, stream, deferred);
-    if (g.k < 4096 && t256x128 >= 4 * cus) return launch_f16_cfg<2, 4, 8, 2, 3, 8, 2>(g, s, stream, deferred);
+    if (g.k < 4096 && t256x128 >= 4 * cus) return launch_f16_cfg<2, 4, 8, 2, 3, 8, 4>(g, s, stream, deferred);
     return launch_f16_cfg<2, 4, 4, 2, 3, 4, 3>(g, s, stream, deferred);
   }
   if (g.k >= 1536) return launch_f16_cfg<2, 4, 2, 1, 4, 1, 3>(g, s, stream, deferred);
