@@ -1085,6 +1085,12 @@ struct ti_llm_model {
     h_row_start[b] = rows;
     const bool need_head = out || greedy;
     upload_meta(size_t(rows));
+    // Compact rows for this pass only, also when it throws (decode passes and
+    // captured decode graphs must see b x 1 rows).
+    struct CompactScope {
+      int& rows;
+      ~CompactScope() { rows = 0; }
+    } compact_scope{compact_rows};
     compact_rows = compact ? rows : 0;
     if (qlen == 1 && greedy) {
       embed(b, 1);
@@ -1093,7 +1099,6 @@ struct ti_llm_model {
       layers(b, qlen);
       if (need_head) head_and_argmax(b, qlen, greedy != nullptr);
     }
-    compact_rows = 0;
     count_forward(need_head, greedy != nullptr);
     if (out)
       ck(hipMemcpy2DAsync(out, size_t(V) * sizeof(float), logits, size_t(head.ldw) * sizeof(float),
