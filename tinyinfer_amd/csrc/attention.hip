@@ -759,14 +759,18 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
       // SIMD holds two waves (causal B1 H4 4096^2: 75 -> 54 us, B1 H12 2048^2:
       // 54 -> 48 us); from 768 workgroups the 4-wave kernel is as fast or
       // faster (B8 H12 512^2: 26 against 28 us, B32 H25 320^2: 55 against 65 us).
-      // batch_invariant (the runtime's prefill) always takes the key-split
-      // kernel, so a query's sums never depend on the grid.  64-dim heads take
+      // batch_invariant (the runtime's prefill) always takes one key group,
+      // so a query's sums never depend on the grid: batched prefills are the
+      // runtime's common case (GPT-2 XL, 32 prompts of ~335
+      // tokens: TTFT 56 -> 53.5 ms against the key-split kernel; b = 1 and
+      // 32 with 32- and 128-token prompts as fast or faster), and a single
+      // long prompt loses only the key split's gain above.  64-dim heads take
       // two 16-query blocks per wave (128 queries per workgroup) once that
       // still leaves enough workgroups (at 128 dims the second block's
       // registers spill).
       const int64_t heads_rows = int64_t(grid.y) * grid.z;
       const int64_t wgs = (a.q_len + 63) / 64 * heads_rows, wgs2 = (a.q_len + 127) / 128 * heads_rows;
-      const bool split_keys = wgs <= 512 || a.batch_invariant;
+      const bool split_keys = wgs <= 512 && !a.batch_invariant;
       const bool two_blocks = D == 64 && (split_keys ? wgs2 >= 512 : wgs2 >= 768);
       grid.x = unsigned(two_blocks ? (a.q_len + 127) / 128 : (a.q_len + 63) / 64);
       if constexpr (D == 64) {
