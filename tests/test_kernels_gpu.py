@@ -624,6 +624,30 @@ def test_split_decode_attention_large_batch(ops):
     assert not got[3].any() and not got[9].any()
 
 
+@pytest.mark.parametrize("d,nk", [(64, 384), (64, 4200), (128, 2100)])
+def test_decode_attention_outside_split_range(ops, d, nk):
+    """Single-query attention whose cache is too short (fewer than 4 chunks of
+    128 / 64 keys) or too long (more than 32 chunks) for the key split: one
+    workgroup per (b, h) whose waves split the keys and merge in LDS, with
+    ragged lengths, a row of 0 keys and a causal offset that hides the tail."""
+    t = torch()
+    rng = np.random.default_rng(7 * d + nk)
+    B, H = 4, 2
+    kl = [nk, 0, nk - 45, 1]
+    ql = [1, 1, 1, 1]
+    off = [nk // 2, 0, nk - 46, 0]
+    q = f16(rng.standard_normal((B, H, 1, d)) * 0.5)
+    k = f16(rng.standard_normal((B, H, nk, d)) * 0.5)
+    v = f16(rng.standard_normal((B, H, nk, d)))
+    say("decode attention outside the split range", d, nk)
+    for causal in (False, True):
+        out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
+                            kv_lengths=kl, query_offsets=off, causal=causal)
+        got = h(hbits(out))
+        close(got, h(oracle.attention_f16(q, k, v, ql, kl, off, causal)))
+        assert not got[1].any()
+
+
 @pytest.mark.parametrize("nq,nk", [(64, 64), (300, 300), (1, 2000), (3, 700)])
 def test_attention_prefill_and_long(ops, nq, nk):
     t = torch()
