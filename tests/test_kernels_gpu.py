@@ -578,6 +578,15 @@ def test_decode_attention_config3(ops):
     assert np.abs(got - short).max() > 2 * SIGNAL_ATOL
 
 
+def poison_past_lengths(k, v, kv_lengths):
+    """fp16 NaN in every K and V entry at or past a request's length: keys a
+    request does not see must not reach its output, whatever the cache holds
+    there (the oracle never reads them)."""
+    for b, n in enumerate(kv_lengths):
+        k[b, :, int(n):] = 0x7E00
+        v[b, :, int(n):] = 0x7E00
+
+
 @pytest.mark.parametrize("d,nk", [(64, 1024), (64, 1500), (128, 512), (128, 1100)])
 @pytest.mark.parametrize("causal", [0, 1])
 def test_split_decode_attention_ragged(ops, d, nk, causal):
@@ -593,6 +602,7 @@ def test_split_decode_attention_ragged(ops, d, nk, causal):
     q = f16(rng.standard_normal((B, H, 1, d)) * 0.5)
     k = f16(rng.standard_normal((B, H, nk, d)) * 0.5)
     v = f16(rng.standard_normal((B, H, nk, d)))
+    poison_past_lengths(k, v, kl)
     say("split decode attention", d, nk, causal)
     out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
                         kv_lengths=kl, query_offsets=off, causal=bool(causal))
@@ -639,6 +649,7 @@ def test_decode_attention_outside_split_range(ops, d, nk):
     q = f16(rng.standard_normal((B, H, 1, d)) * 0.5)
     k = f16(rng.standard_normal((B, H, nk, d)) * 0.5)
     v = f16(rng.standard_normal((B, H, nk, d)))
+    poison_past_lengths(k, v, kl)
     say("decode attention outside the split range", d, nk)
     for causal in (False, True):
         out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
