@@ -1,8 +1,10 @@
-"""GPU check of ti_amd_gemm_ex_i8_noalloc (split-K partials in the library's
-fixed device array) against ti_v2_gemm_ex_i8 (partials in the per-stream
-scratch the library allocates), both through the C ABI: identical bits on two
-calls in a row, the second smaller than the first, and within the linear
-tolerance (rtol 1e-2 / atol 2e-2) of the CPU oracle."""
+"""GPU check of ti_amd_gemm_ex_i8_noalloc against ti_v2_gemm_ex_i8 through the
+C ABI: identical bits on two calls in a row, the second smaller than the first,
+and within the linear tolerance (rtol 1e-2 / atol 2e-2) of the CPU oracle; and
+the no-allocation call captured into a graph on a fresh stream (a hipMalloc
+there would fail the capture), its replays bit-identical to the eager call.
+Both entry points keep split-K partials in the calling hardware queue's slot
+of the library's static pool and finish them in the same launch."""
 import ctypes as C
 
 import numpy as np
@@ -89,3 +91,28 @@ def test_noalloc_gemm_validates_before_enqueue():
     assert fn(a.data_ptr(), q.data_ptr(), s.data_ptr(), None, y.data_ptr(), None, 1, 64, 64, 0, 7, stream, 0) == 1
     torch.cuda.synchronize()
     assert torch.all(y == 7.0).item()
+
+
+def test_noalloc_gemm_captured_on_fresh_stream():
+    import torch
+    lib = _lib()
+    m, n, k = 8, 768, 3072  # a split-K plan: partials go to the queue pool slot
+    print(f"[case] noalloc under capture on a fresh stream: M={m} N={n} K={k}", flush=True)
+    a, q, s, bias = _case(m, n, k, seed=5)
+    dev = (torch.from_numpy(a).view(torch.float16).cuda(), torch.from_numpy(q).cuda(),
+           torch.from_numpy(s).cuda(), torch.from_numpy(bias).view(torch.float16).cuda())
+    want = _run(lib, "ti_amd_gemm_ex_i8_noalloc", dev, m, n, k, 0, 0)
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        st = lib.ti_amd_gemm_ex_i8_noalloc(dev[0].data_ptr(), dev[1].data_ptr(), dev[2].data_ptr(),
+                                           dev[3].data_ptr(), y.data_ptr(), None, m, n, k, 0, 0,
+                                           torch.cuda.current_stream().cuda_stream, 0)
+    assert st == 0, lib.ti_v2_last_error()
+    for r in range(3):
+        y.fill_(0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert y.cpu().numpy().tobytes() == want.tobytes(), f"replay {r} differs from the eager call"

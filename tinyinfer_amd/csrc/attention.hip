@@ -19,11 +19,19 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "queue_scratch.hpp"
 
 namespace tia {
 namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
+
+// Split decode of the C ABI: per hardware queue, 2 MiB of chunk states
+// [B][H][chunks][2 + D] and one arrival counter per (b, h) row
+// (queue_scratch.hpp); a call beyond either runs the one-pass kernel.
+constexpr size_t kAttnPoolFloats = size_t(1) << 19;
+constexpr int kAttnPoolRows = 4096;
+TIA_QUEUE_POOL(attn_pool, kAttnPoolFloats, kAttnPoolRows)
 
 // Offset of query row qi of request b in q or out (batch stride sb, row stride
 // sq): b * sb + qi * sq, or (q_row_start[b] + qi) * sq over compact rows.
@@ -40,7 +48,9 @@ struct AttnParams {
   AttnArgs a;
   float scale;
   bool vec;       // every pointer and stride allows 16-byte accesses
-  float* parts;   // split decode: [B][H][chunks][2 + D] = (m, l, unnormalized acc)
+  bool split;     // split decode: key chunks of each (b, h) over workgroups, the
+                  // states [B][H][chunks][2 + D] = (m, l, unnormalized acc) in the
+                  // queue's pool slot, merged by the row's last chunk to finish
   int chunks;     // split decode: key chunks per (b, h)
 };
 
@@ -115,7 +125,13 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
   // Keys [kbeg, end) of this workgroup.
   constexpr int CHUNK = 2 * KW * TK;
   const int kbeg = chunk_id * CHUNK;
-  if constexpr (SPLIT) end = min(end, kbeg + CHUNK);
+  // Split decode: the row's chunks that hold a visible key (at least chunk 0,
+  // which writes a row with no visible key); the others do nothing.
+  const int active = max(1, min(p.chunks, (end + CHUNK - 1) / CHUNK));
+  if constexpr (SPLIT) {
+    if (chunk_id >= active) return;
+    end = min(end, kbeg + CHUNK);
+  }
 
   // Keys at or past `end` re-read key end-1 (valid, written data) instead of
   // branching, so every load of a tile is unconditional and the compiler can
@@ -336,15 +352,69 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
     for (int e = 0; e < 8; ++e) acc[e] = tacc[e];
   }
   if constexpr (SPLIT) {
-    if (kg != 0) return;
-    float* part = p.parts + ((int64_t(b) * a.heads + h) * p.chunks + chunk_id) * (2 + D);
-    if (lane == 0) {
-      part[0] = m;
-      part[1] = l;
-    }
+    if (active > 1) {
+      // Store this chunk's state; the row's last chunk to arrive merges every
+      // chunk's state (common maximum over chunks that saw a key, rescale, sum
+      // in chunk order) and writes fp16_rn(acc / l), or 0 when no key was
+      // visible.
+      const int lane64 = int(threadIdx.x & 63);
+      const unsigned long long key = lane64 < kQueueSlots ? attn_pool_keys[lane64] : 0ull;
+      const int sl = queue_slot_resolve(attn_pool_keys, key);
+      const int64_t row = int64_t(b) * a.heads + h;
+      float* base = attn_pool_data[sl] + row * p.chunks * (2 + D);
+      unsigned* counter = attn_pool_ctr[sl] + row * kCounterStride;
+      if (kg == 0) {
+        float* part = base + chunk_id * (2 + D);
+        if (lane == 0) {
+          st_agent(part, m);
+          st_agent(part + 1, l);
+        }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) part[2 + 8 * ds + e] = acc[e];
-    return;
+        for (int e = 0; e < 8; ++e) st_agent(part + 2 + 8 * ds + e, acc[e]);
+      }
+      if (!arrive_last(counter, active)) return;
+      constexpr int DPL = D / 64;  // dims per lane in the merge
+      float gm = kNegInf;
+      for (int c0 = 0; c0 < active; c0 += 8) {
+        float cm[8], cl[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float* pc = base + min(c0 + c, active - 1) * (2 + D);
+          cm[c] = ld_agent(pc);
+          cl[c] = ld_agent(pc + 1);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (c0 + c < active && cl[c] > 0.f) gm = fmaxf(gm, cm[c]);
+      }
+      float tl = 0.f, tacc[DPL] = {};
+      for (int c0 = 0; c0 < active; c0 += 8) {
+        float cm[8], cl[8], ca[8][DPL];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float* pc = base + min(c0 + c, active - 1) * (2 + D);
+          cm[c] = ld_agent(pc);
+          cl[c] = ld_agent(pc + 1);
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) ca[c][e] = ld_agent(pc + 2 + DPL * lane + e);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          if (c0 + c >= active) break;
+          const float f = cl[c] > 0.f ? __expf(cm[c] - gm) : 0.f;
+          tl += cl[c] * f;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) tacc[e] += ca[c][e] * f;
+        }
+      }
+      depart(counter);
+      uint16_t* op = a.out + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + DPL * lane;
+      const float inv = tl > 0.f ? 1.f / tl : 0.f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) op[e] = f2h(tl > 0.f ? tacc[e] * inv : 0.f);
+      return;
+    }
+    // The row's only chunk finishes as the one-pass kernel does (below).
   }
   if (qi >= written_queries(a, q_valid) || kg != 0) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -358,43 +428,6 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) op[e] = __builtin_bit_cast(uint16_t, o[e]);
   }
-}
-
-// Second pass of the split decode: one wave per (b, h) merges the chunk states
-// (common maximum over chunks that saw a key, rescale, sum) and writes
-// fp16_rn(acc / l), or 0 when no key was visible.  Up to MAXC chunks are read
-// in one round of loads (clamped indices, unused ones weighted 0).
-template <int D, int MAXC>
-__global__ __launch_bounds__(64) void attention_combine_kernel(AttnParams p) {
-  constexpr int DPL = D / 64;  // dims per lane
-  const AttnArgs& a = p.a;
-  const int lane = threadIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const float* base = p.parts + (int64_t(b) * a.heads + h) * p.chunks * (2 + D);
-  float cm[MAXC], cl[MAXC], ca[MAXC][DPL];
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    const float* part = base + min(c, p.chunks - 1) * (2 + D);
-    cm[c] = part[0];
-    cl[c] = c < p.chunks ? part[1] : 0.f;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) ca[c][e] = part[2 + DPL * lane + e];
-  }
-  float gm = kNegInf;
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c)
-    if (cl[c] > 0.f) gm = fmaxf(gm, cm[c]);
-  float l = 0.f, acc[DPL] = {};
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    const float f = cl[c] > 0.f ? __expf(cm[c] - gm) : 0.f;
-    l += cl[c] * f;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[e] += ca[c][e] * f;
-  }
-  uint16_t* op = a.out + (a.out_p32 ? p32_off(b, h * D + DPL * lane) : int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + DPL * lane);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-#pragma unroll
-  for (int e = 0; e < DPL; ++e) op[e] = f2h(l > 0.f ? acc[e] * inv : 0.f);
 }
 
 // Prefill (several queries per request) on MFMA, flash-attention style in the
@@ -756,14 +789,13 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
     while (kw < 8 && kw * 2 * 4 <= tiles) kw *= 2;
     dim3 grid = blocks_per;
     grid.x = 1;
-    if (p.parts) {
+    if (p.split) {
       // Long caches: 2-wave workgroups over chunks of 2 * 2 tiles (all of a
       // wave's loads in flight at once; 4- and 8-wave chunks of 256 / 512 keys
-      // measured slower on configs[3]), spread over every CU, then a merge.
+      // measured slower on configs[3]), spread over every CU; each row's last
+      // chunk merges the row.
       const dim3 split_grid(unsigned(a.heads), unsigned(a.batch), unsigned(p.chunks));
       hipLaunchKernelGGL((attention_kernel<D, 1, 2, VEC, false, true>), split_grid, dim3(128), 0, stream, p);
-      if (p.chunks <= 8) hipLaunchKernelGGL((attention_combine_kernel<D, 8>), grid, dim3(64), 0, stream, p);
-      else hipLaunchKernelGGL((attention_combine_kernel<D, 32>), grid, dim3(64), 0, stream, p);
       return hipGetLastError();
     }
     if (a.qkv_partials) {
@@ -829,14 +861,20 @@ hipError_t attention(const AttnArgs& a, hipStream_t stream, const Scratch* scrat
     return hipErrorInvalidValue;
   AttnParams p{};
   p.a = a;
-  // Decode over a long cache (at least 4 chunks of 128/64 keys per (b, h)) and
-  // enough scratch for the chunk states: split the keys across workgroups.
-  if (scratch && scratch->partials && a.q_len == 1 && !a.qkv_partials && (a.head_dim == 64 || a.head_dim == 128)) {
+  // Decode over a long cache (at least 4 chunks of 128/64 keys per (b, h)) in
+  // the ABI's layout, whose chunk states fit the queue pool slot: split the
+  // keys across workgroups.  (The split kernel loads chunk 0 before the
+  // lengths, clamped to kv_len - 1, which holds for this layout only: with
+  // lengths from offsets a row could see keys past kv_len.)  The choice
+  // follows the shape alone.
+  if (scratch && scratch->queue_pool && a.q_len == 1 && !a.qkv_partials && !a.kv_slot && !a.kv_from_offsets &&
+      !a.q_row_start && !a.out_p32 && (a.head_dim == 64 || a.head_dim == 128)) {
     const int chunk = a.head_dim == 64 ? 128 : 64;  // 2 waves x 2 tiles
     const int chunks = (a.kv_len + chunk - 1) / chunk;
-    const size_t need = size_t(a.batch) * a.heads * chunks * (2 + a.head_dim);
-    if (chunks >= 4 && chunks <= 32 && need <= scratch->partial_floats) {
-      p.parts = scratch->partials;
+    const int64_t rows = int64_t(a.batch) * a.heads;
+    const int64_t need = rows * chunks * (2 + a.head_dim);
+    if (chunks >= 4 && chunks <= 32 && rows <= kAttnPoolRows && need <= int64_t(kAttnPoolFloats)) {
+      p.split = true;
       p.chunks = chunks;
     }
   }

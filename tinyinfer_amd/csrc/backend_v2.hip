@@ -8,7 +8,6 @@
 #include <cstdio>
 #include <initializer_list>
 #include <limits>
-#include <mutex>
 
 #include "../../include/tinyinfer_amd_ext.h"
 #include "../../include/tinyinfer_backend_v2.h"
@@ -67,15 +66,12 @@ int check_workspace(const void* p, int m, int n, int config) {
   return TI_V2_OK;
 }
 
-// `split_scratch`: where split-K partials go (null: the library's
-// per-(device, stream) scratch, allocated on the stream's first call).
+// Split-K partials go to the calling queue's slot of the library's static pool
+// and are finished in the same launch: nothing is allocated, and the call can
+// be captured into a graph on any stream.
 int run_gemm(const uint16_t* a, const void* w, bool int8, const float* scales, const uint16_t* bias,
-             void* y, float* workspace, int m, int n, int k, int dtype, int config, uintptr_t stream,
-             int device, const tia::Scratch* split_scratch = nullptr) {
+             void* y, float* workspace, int m, int n, int k, int dtype, int config, uintptr_t stream) {
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t err = hipSuccess;
-  const tia::Scratch* lib_scratch = split_scratch ? split_scratch : tia::library_scratch(device, st, &err);
-  if (!lib_scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -95,7 +91,7 @@ int run_gemm(const uint16_t* a, const void* w, bool int8, const float* scales, c
     g.epi.y = y;
   }
   g.epi.ldy = n;
-  err = tia::gemm(g, lib_scratch, st);
+  hipError_t err = tia::gemm(g, tia::queue_pool_scratch(), st);
   if (err == hipSuccess && separate) err = tia::bias_epilogue(workspace, bias, y, int64_t(m) * n, n, dtype, st);
   return hip_status(err);
 }
@@ -127,7 +123,7 @@ extern "C" int ti_v2_gemm_ex_f16(const uint16_t* a, const uint16_t* b, const uin
   if (status) return status;
   if ((status = check_gemm(a, b, bias, y, m, n, k, dtype, config, false))) return status;
   if ((status = check_workspace(workspace, m, n, config))) return status;
-  return run_gemm(a, b, false, nullptr, bias, y, workspace, m, n, k, dtype, config, stream, device);
+  return run_gemm(a, b, false, nullptr, bias, y, workspace, m, n, k, dtype, config, stream);
 }
 
 extern "C" int ti_v2_gemm_ex_i8(const uint16_t* a, const int8_t* b, const float* scales,
@@ -138,70 +134,17 @@ extern "C" int ti_v2_gemm_ex_i8(const uint16_t* a, const int8_t* b, const float*
   if ((status = check_gemm(a, b, bias, y, m, n, k, dtype, config, true))) return status;
   if (!aligned(scales, 4)) return fail(TI_V2_INVALID_ARGUMENT, "scales pointer must be nonnull aligned FP32[N]");
   if ((status = check_workspace(workspace, m, n, config))) return status;
-  return run_gemm(a, b, true, scales, bias, y, workspace, m, n, k, dtype, config, stream, device);
+  return run_gemm(a, b, true, scales, bias, y, workspace, m, n, k, dtype, config, stream);
 }
 
-// ---------------------------------------------------------------------------
-// No-allocation variant of ti_v2_gemm_ex_i8.  Its split-K partials live in a
-// file-scope device array instead of the library's hipMalloc'd per-stream
-// scratch.  In host code `scratch` names a host-side stand-in, not device
-// memory: kernels get the per-device address hipGetSymbolAddress returns.
-// ---------------------------------------------------------------------------
-constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
-constexpr size_t kNoAllocScratchFloats = kNoAllocScratchBytes / sizeof(float);
-static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
-
-namespace {
-constexpr int kNoAllocMaxDevices = 64;
-std::mutex noalloc_mutex;
-float* noalloc_base[kNoAllocMaxDevices] = {};
-
-// Device address of `scratch` on `device` (the current device: begin() checked
-// it), looked up once per device and kept.
-float* noalloc_scratch(int device, hipError_t* err) {
-  if (device >= kNoAllocMaxDevices) {
-    *err = hipErrorInvalidDevice;
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lock(noalloc_mutex);
-  if (!noalloc_base[device]) {
-    void* address = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !address) {
-      *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
-      return nullptr;
-    }
-    noalloc_base[device] = static_cast<float*>(address);
-  }
-  return noalloc_base[device];
-}
-}  // namespace
-
+// ti_amd_gemm_ex_i8_noalloc: ti_v2_gemm_ex_i8 for callers that must not
+// allocate.  Every entry point of this library is allocation-free (split
+// work goes to the queue pool), so it is the same call: same arguments,
+// validation, status codes and bits.
 extern "C" int ti_amd_gemm_ex_i8_noalloc(const uint16_t* a, const int8_t* b, const float* scales,
                                          const uint16_t* bias, void* y, float* workspace, int m, int n,
                                          int k, int dtype, int config, uintptr_t stream, int device) {
-  int status = begin(device);
-  if (status) return status;
-  if ((status = check_gemm(a, b, bias, y, m, n, k, dtype, config, true))) return status;
-  if (!aligned(scales, 4)) return fail(TI_V2_INVALID_ARGUMENT, "scales pointer must be nonnull aligned FP32[N]");
-  if ((status = check_workspace(workspace, m, n, config))) return status;
-  // The split plan is the one ti_v2_gemm_ex_i8 takes with the library scratch,
-  // so both entry points return the same bits; a plan that needs more than the
-  // fixed array is refused rather than changed.
-  const size_t need = tia::row_major_gemm_scratch_floats(m, n, k, tia::kScratchPartialFloats);
-  if (need > kNoAllocScratchFloats) {
-    char text[200];
-    std::snprintf(text, sizeof(text),
-                  "no-allocation GEMM: this shape's split-K plan needs %zu bytes of scratch, above the fixed "
-                  "%zu-byte maximum; call ti_v2_gemm_ex_i8",
-                  need * sizeof(float), kNoAllocScratchBytes);
-    return fail(TI_V2_INVALID_ARGUMENT, text);
-  }
-  hipError_t err = hipSuccess;
-  float* base = noalloc_scratch(device, &err);
-  if (!base) return hip_status(err);
-  const tia::Scratch fixed{base, kNoAllocScratchFloats};
-  return run_gemm(a, b, true, scales, bias, y, workspace, m, n, k, dtype, config, stream, device, &fixed);
+  return ti_v2_gemm_ex_i8(a, b, scales, bias, y, workspace, m, n, k, dtype, config, stream, device);
 }
 
 extern "C" int ti_v2_gemm_f16(const uint16_t* a, const uint16_t* b, const uint16_t* bias, void* y,
@@ -270,13 +213,10 @@ extern "C" int ti_v2_attention_f16(const uint16_t* q, const uint16_t* k, const u
   a.kv_len = nk;
   a.head_dim = d;
   a.causal = causal != 0;
-  // The library's per-stream scratch lets a long single-query call split its
-  // keys across workgroups; without it (first call on a stream under graph
-  // capture) the one-pass kernel runs.
-  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t scratch_err = hipSuccess;
-  const tia::Scratch* lib_scratch = tia::library_scratch(device, st, &scratch_err);
-  return hip_status(tia::attention(a, st, lib_scratch));
+  // A long single-query call splits its keys across workgroups, the chunk
+  // states in the calling queue's slot of the library's static pool (merged in
+  // the same launch; the choice follows the shape alone).
+  return hip_status(tia::attention(a, reinterpret_cast<hipStream_t>(stream), tia::queue_pool_scratch()));
 }
 
 extern "C" int ti_v2_layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,
@@ -317,9 +257,6 @@ extern "C" int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const fl
   if (epilogue < 0 || epilogue > 2 || (epilogue == 2 && !aligned(residual, 2)))
     return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t err = hipSuccess;
-  const tia::Scratch* lib_scratch = tia::library_scratch(device, st, &err);
-  if (!lib_scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -335,7 +272,7 @@ extern "C" int ti_amd_gemm_i8_fused(const uint16_t* a, const int8_t* q, const fl
   g.epi.ldy = n;
   g.epi.residual = residual;
   g.epi.ldr = n;
-  return hip_status(tia::gemm(g, lib_scratch, st));
+  return hip_status(tia::gemm(g, tia::queue_pool_scratch(), st));
 }
 
 extern "C" int64_t ti_amd_packed_w8_bytes(int k, int n) {
@@ -377,9 +314,6 @@ extern "C" int ti_amd_gemm_w16p_fused(const uint16_t* a, const void* packed16, c
   if (epilogue < 0 || epilogue > 2 || (epilogue == 2 && !aligned(residual, 2)))
     return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t err = hipSuccess;
-  const tia::Scratch* lib_scratch = tia::library_scratch(device, st, &err);
-  if (!lib_scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -394,7 +328,7 @@ extern "C" int ti_amd_gemm_w16p_fused(const uint16_t* a, const void* packed16, c
   g.epi.ldy = n;
   g.epi.residual = residual;
   g.epi.ldr = n;
-  return hip_status(tia::gemm(g, lib_scratch, st));
+  return hip_status(tia::gemm(g, tia::queue_pool_scratch(), st));
 }
 
 extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, const float* scales,
@@ -410,9 +344,6 @@ extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, cons
   if (epilogue < 0 || epilogue > 2 || (epilogue == 2 && !aligned(residual, 2)))
     return fail(TI_V2_INVALID_ARGUMENT, "epilogue must be 0 (bias), 1 (bias+GELU) or 2 (bias+residual)");
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t err = hipSuccess;
-  const tia::Scratch* lib_scratch = tia::library_scratch(device, st, &err);
-  if (!lib_scratch) return hip_status(err);
   tia::GemmArgs g;
   g.a = a;
   g.lda = k;
@@ -429,7 +360,7 @@ extern "C" int ti_amd_gemm_w8p_fused(const uint16_t* a, const void* packed, cons
   g.epi.ldy = n;
   g.epi.residual = residual;
   g.epi.ldr = n;
-  return hip_status(tia::gemm(g, lib_scratch, st));
+  return hip_status(tia::gemm(g, tia::queue_pool_scratch(), st));
 }
 
 extern "C" int ti_amd_gemm_w8p_ln_fused(const uint16_t* a, const uint16_t* gamma, const uint16_t* beta, float eps,

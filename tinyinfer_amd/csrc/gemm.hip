@@ -17,11 +17,13 @@
 //    with A padded to 16/32 rows.  A lane loads one dword (4 consecutive output
 //    columns) from 8 consecutive K rows, so the MFMA for "column slot" c covers
 //    columns {n0 + 4j + c}; the 4 waves of a workgroup split K, reduce through
-//    LDS, and workgroups split K further: each writes fp32 partials and a
-//    second kernel sums them in split order and runs the fused epilogue (bias /
-//    GELU / residual / KV scatter).  (A single-kernel last-arrival reduction
-//    needs agent-scope release/acquire fences, which on the multi-XCD part
-//    write back and invalidate the whole L2 in every workgroup.)
+//    LDS, and workgroups split K further: each writes fp32 partials, which
+//    are summed in split order and finished with the fused epilogue (bias /
+//    GELU / residual / KV scatter) either by a second kernel (callers that own
+//    a scratch buffer: the runtime) or, for the C ABIs, by the last workgroup
+//    of the tile in the same launch (partials in the queue's slot of a static
+//    pool, written and read with agent-scope accesses, so no L2-wide
+//    writeback or invalidate is needed; queue_scratch.hpp).
 //  * tiled (M > 32, prefill): 64x64x32 tiles, A and the dequantised weight tile
 //    staged in LDS (weights transposed to [n][k] so both MFMA operands are one
 //    ds_read_b128 per lane), double buffered, same fused epilogues.
@@ -30,16 +32,50 @@
 #include <algorithm>
 #include <atomic>
 #include <climits>
-#include <map>
-#include <mutex>
 #include <type_traits>
 #include <utility>
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "queue_scratch.hpp"
 
 namespace tia {
 namespace {
+
+// Split-K scratch of the C ABIs' GEMMs: per hardware queue, 4 MiB of fp32
+// partials and 1024 tile arrival counters (a split plan is sized to fit).
+constexpr size_t kPoolFloats = size_t(1) << 20;
+constexpr int kPoolTiles = 1024;
+TIA_QUEUE_POOL(gemm_pool, kPoolFloats, kPoolTiles)
+
+struct PoolSlot {
+  float* parts;
+  unsigned* ctr;
+};
+// The calling dispatch's slot (a whole wave calls it).
+__device__ __forceinline__ PoolSlot gemm_pool_slot() {
+  const int lane = int(threadIdx.x & 63);
+  const unsigned long long key = lane < kQueueSlots ? gemm_pool_keys[lane] : 0ull;
+  const int s = queue_slot_resolve(gemm_pool_keys, key);
+  return {gemm_pool_data[s], gemm_pool_ctr[s]};
+}
+
+// Sum of the `splits` partials of one output element at p, p + stride, ...
+// in the order splitk_epilogue_kernel adds them: split sp into group sp % 4 in
+// increasing order, then ((g0 + g1) + g2) + g3.  Agent-scope loads, up to 8 in
+// flight.
+__device__ __forceinline__ float pool_split_sum(const float* p, int64_t stride, int splits) {
+  float r[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int sp0 = 0; sp0 < splits; sp0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = sp0 + u < splits ? ld_agent(p + int64_t(sp0 + u) * stride) : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (sp0 + u < splits) r[u & 3] += v[u];
+  }
+  return ((r[0] + r[1]) + r[2]) + r[3];
+}
 
 // A 16-bit load from global memory through a pointer the compiler cannot
 // place (a select of two kernel-argument pointers): typed as global, it is a
@@ -164,6 +200,7 @@ struct SkinnyParams {
   int steps_per_block; // K steps owned by one workgroup (its waves take every 4th)
   int splits;
   bool defer;          // always leave fp32 partials (even for one split), no epilogue
+  bool pool;           // splits > 1 finish in this launch through the queue pool
   Epilogue epi;
   float* partials;     // [splits][M][N]
 };
@@ -320,6 +357,32 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) 
   __syncthreads();
 
   constexpr int kElems = MT * 16 * 64;
+  if (p.pool && p.splits > 1) {
+    // This split's sums to the queue's pool slot; the tile's last split to
+    // arrive sums them all in split order and runs the epilogue.
+    const PoolSlot slot = gemm_pool_slot();
+    const int64_t plane = int64_t(p.m) * p.n;
+    for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
+      const int row = e >> 6, cc = e & 63, n = n0 + cc;
+      if (row < p.m && n < p.n)
+        st_agent(slot.parts + int64_t(split) * plane + int64_t(row) * p.n + n,
+                 red[0][row][cc] + red[1][row][cc] + red[2][row][cc] + red[3][row][cc]);
+    }
+    if (!wg_arrive_last(slot.ctr + tile * kCounterStride, p.splits)) return;
+    with_epilogue_kind(p.epi, [&](auto kind) {
+      constexpr int K = decltype(kind)::value;
+      for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
+        const int row = e >> 6, n = n0 + (e & 63);
+        if (row >= p.m || n >= p.n) continue;
+        const float total = pool_split_sum(slot.parts + int64_t(row) * p.n + n, plane, p.splits);
+        const float bias = K == EPI_RAW_F32 ? 0.f : epilogue_bias(p.epi, n);
+        const float resid = K == EPI_RESIDUAL ? h2f(p.epi.residual[r_off(p.epi, row, n)]) : 0.f;
+        epilogue_k<K>(p.epi, row, n, total, bias, resid);
+      }
+    });
+    depart(slot.ctr + tile * kCounterStride);
+    return;
+  }
   for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
     const int row = e >> 6, cc = e & 63, n = n0 + cc;
     if (row < p.m && n < p.n) {
@@ -989,6 +1052,7 @@ struct PanelParams {
   int group_m;          // tile rows per group of the tile order
   int chunks_per_split, splits;
   bool defer;
+  bool pool;            // splits > 1 finish in this launch through the queue pool
   Epilogue epi;
   float* partials;      // [splits][M][N] when splits > 1 or defer
 };
@@ -1019,6 +1083,49 @@ __device__ __forceinline__ void wait_chunk(int outstanding) {
 // (j, g) of a 16-column block writes rows 4g + v, column j) hit 64 distinct
 // banks.
 constexpr int tile_pitch(int bn) { return bn + 4; }
+
+// In-launch split-K finish of a TR x BN fp32 tile staged in LDS at pitch
+// tile_pitch(BN), rows r0.., columns n0.. (the thread mapping of
+// tile_epilogue): this split's sums go to the pool slot at
+// parts[(split m + row) n + col]; the last split of the tile to arrive adds
+// every split's sums (pool_split_sum's order) back into the LDS tile and
+// returns true, and the caller then runs tile_epilogue on it; every other
+// workgroup returns false.
+template <int TR, int BN, int NT>
+__device__ bool tile_split_finish(float* ctile, int r0, int n0, int m, int n, int split, int splits, int tile) {
+  constexpr int CG = BN / 4, RS = NT / CG, RPT = TR / RS;
+  const int c4 = int(threadIdx.x) % CG, rl0 = int(threadIdx.x) / CG;
+  const int col = n0 + 4 * c4;
+  const PoolSlot slot = gemm_pool_slot();
+  const int64_t plane = int64_t(m) * n;
+  if (col < n) {
+#pragma unroll 1
+    for (int i = 0; i < RPT; ++i) {
+      const int row = r0 + rl0 + i * RS;
+      if (row >= m) break;
+      const float* v = ctile + (rl0 + i * RS) * tile_pitch(BN) + 4 * c4;
+      float* dst = slot.parts + int64_t(split) * plane + int64_t(row) * n + col;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (col + c < n) st_agent(dst + c, v[c]);
+    }
+  }
+  if (!wg_arrive_last(slot.ctr + tile * kCounterStride, splits)) return false;
+  if (col < n) {
+#pragma unroll 1
+    for (int i = 0; i < RPT; ++i) {
+      const int row = r0 + rl0 + i * RS;
+      if (row >= m) break;
+      float* v = ctile + (rl0 + i * RS) * tile_pitch(BN) + 4 * c4;
+      const float* src = slot.parts + int64_t(row) * n + col;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (col + c < n) v[c] = pool_split_sum(src + c, plane, splits);
+    }
+  }
+  depart(slot.ctr + tile * kCounterStride);
+  return true;
+}
 
 // The 4 bias values of columns col .. col + 3 (0 past N or without a bias),
 // loaded early: used only by the tile epilogue.  Without a bias the loads
@@ -1319,6 +1426,11 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
       for (int v = 0; v < 4; ++v)
         ctile[((wm * MT + t) * 16 + 4 * g + v) * tile_pitch(BN) + (wn * R + r) * 16 + j] = acc[t][r][v];
   __syncthreads();
+  if (p.pool && p.splits > 1) {
+    if (tile_split_finish<BM, BN, 256>(ctile, m0, cb0 * 16, p.m, p.n, split, p.splits, tm * p.tiles_n + tn))
+      tile_epilogue<BM, BN, 256>(p.epi, ctile, m0, cb0 * 16, p.m, p.n, bias, nullptr, split);
+    return;
+  }
   tile_epilogue<BM, BN, 256>(p.epi, ctile, m0, cb0 * 16, p.m, p.n, bias, epi_now ? nullptr : p.partials, split);
 }
 
@@ -1334,9 +1446,11 @@ struct TiledParams {
   int64_t ldw;
   Epilogue epi;
   // Split-K (gridDim.z > 1): split z takes K steps [z * steps_per_split, ...)
-  // and stores raw fp32 sums at partials[(z * m + row) * n + col].
+  // and stores raw fp32 sums at partials[(z * m + row) * n + col], or with
+  // `pool` in the queue pool slot, finished by the tile's last split.
   int steps_per_split;
   float* partials;
+  bool pool;
 };
 constexpr int TBM = 64, TBN = 64, TBK = 32, TPAD = 40;  // LDS row pitch in halves
 
@@ -1470,6 +1584,12 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
       for (int v = 0; v < 4; ++v)
         ctile[(wm * 32 + 16 * t + 4 * g + v) * tile_pitch(TBN) + wn * 32 + 16 * c + j] = acc[t][c][v];
   __syncthreads();
+  if (p.pool && gridDim.z > 1) {
+    if (tile_split_finish<TBM, TBN, 256>(ctile, m0, n0, p.m, p.n, split, int(gridDim.z),
+                                         int(blockIdx.x + gridDim.x * blockIdx.y)))
+      tile_epilogue<TBM, TBN, 256>(p.epi, ctile, m0, n0, p.m, p.n, bias, nullptr, split);
+    return;
+  }
   tile_epilogue<TBM, TBN, 256>(p.epi, ctile, m0, n0, p.m, p.n, bias, gridDim.z > 1 ? p.partials : nullptr, split);
 }
 
@@ -1595,11 +1715,13 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   p.ldw = g.ldw > 0 ? g.ldw : g.n;
   p.ntile = (g.n + 63) / 64;
   p.steps = (g.k + 31) / 32;
-  int splits = skinny_splits(g.m, g.n, g.k, (s && s->partials) ? s->partial_floats : 0);
+  const bool pool = s && s->queue_pool && !deferred && p.ntile <= kPoolTiles;
+  int splits = skinny_splits(g.m, g.n, g.k, pool ? kPoolFloats : (s && s->partials) ? s->partial_floats : 0);
   const int spb = (p.steps + splits - 1) / splits;
   p.steps_per_block = spb;
   p.splits = splits;
   p.defer = deferred != nullptr;
+  p.pool = pool;
   p.partials = s ? s->partials : nullptr;
   if (p.defer && (!p.partials || size_t(splits) * g.m * g.n > s->partial_floats)) return hipErrorInvalidValue;
   const dim3 grid(unsigned(p.ntile) * unsigned(splits));
@@ -1613,7 +1735,7 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
     *deferred = splits;
     return hipGetLastError();
   }
-  if (splits > 1) {
+  if (splits > 1 && !pool) {
     const int64_t total = int64_t(g.m) * g.n;
     const unsigned blocks = unsigned(std::min<int64_t>((total + 63) / 64, 8192));
     hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m,
@@ -1854,14 +1976,17 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
   if (tiles > (int64_t(1) << 28)) return hipErrorInvalidValue;
   p.tiles = int(tiles);
   int splits = 1;
-  if (may_split && s && s->partials && tiles < 192) {
+  const bool pool = s && s->queue_pool && !deferred && tiles <= kPoolTiles;
+  const size_t capacity = pool ? kPoolFloats : (s && s->partials) ? s->partial_floats : 0;
+  if (may_split && capacity > 0 && tiles < 192) {
     splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, p.kc / (S - 1))));
-    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
+    while (splits > 1 && size_t(splits) * g.m * g.n > capacity) --splits;
   }
   p.chunks_per_split = (p.kc + splits - 1) / splits;
   splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
   p.splits = splits;
   p.defer = deferred != nullptr && splits > 1;
+  p.pool = pool;
   p.partials = s ? s->partials : nullptr;
   hipLaunchKernelGGL((panel_gemm_kernel<WM, WN, MT, R, S>), dim3(unsigned(tiles * splits)), dim3(256), kLds,
                      stream, p);
@@ -1869,7 +1994,7 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
     *deferred = splits;
     return hipGetLastError();
   }
-  if (splits > 1) {
+  if (splits > 1 && !pool) {
     const int64_t total = int64_t(g.m) * g.n;
     const unsigned blocks = unsigned(std::min<int64_t>((total + 63) / 64, 8192));
     hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m, g.n,
@@ -1916,6 +2041,7 @@ struct F16GemmParams {
   int group_m;       // tile rows per group of the tile order
   int chunks_per_split, splits;
   bool defer;
+  bool pool;         // splits > 1 finish in this launch through the queue pool (EP == 1 only)
   Epilogue epi;
   float* partials;
 };
@@ -2037,6 +2163,13 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void f16_gemm_kernel(F16GemmPara
           ctile[(rb + 4 * g + v) * tile_pitch(BN) + (wn * R + r) * 16 + j] = acc[t][r][v];
     }
     __syncthreads();
+    if constexpr (EP == 1) {
+      if (p.pool && p.splits > 1) {
+        if (tile_split_finish<PR, BN, NT>(ctile, m0, cb0 * 16, p.m, p.n, split, p.splits, tm * p.tiles_n + tn))
+          tile_epilogue<PR, BN, NT>(p.epi, ctile, m0, cb0 * 16, p.m, p.n, bias, nullptr, split);
+        return;
+      }
+    }
     tile_epilogue<PR, BN, NT>(p.epi, ctile, m0 + pass * PR, cb0 * 16, p.m, p.n, bias,
                               epi_now ? nullptr : p.partials, split);
   }
@@ -2060,14 +2193,18 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
   if (tiles > (int64_t(1) << 28)) return hipErrorInvalidValue;
   p.tiles = int(tiles);
   int splits = 1;
-  if (!g.canonical && s && s->partials && tiles < 192) {
+  const bool pool = s && s->queue_pool && !deferred;
+  const size_t capacity = !pool ? ((s && s->partials) ? s->partial_floats : 0)
+                                : (EP == 1 && tiles <= kPoolTiles) ? kPoolFloats : 0;
+  if (!g.canonical && capacity > 0 && tiles < 192) {
     splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, p.kk / (S - 1))));
-    while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
+    while (splits > 1 && size_t(splits) * g.m * g.n > capacity) --splits;
   }
   p.chunks_per_split = (p.kk + splits - 1) / splits;
   splits = (p.kk + p.chunks_per_split - 1) / p.chunks_per_split;
   p.splits = splits;
   p.defer = deferred != nullptr && splits > 1;
+  p.pool = pool;
   p.partials = s ? s->partials : nullptr;
   hipLaunchKernelGGL((f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC>), dim3(unsigned(tiles * splits)), dim3(WM * WN * 64),
                      kLds, stream, p);
@@ -2075,7 +2212,7 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
     *deferred = splits;
     return hipGetLastError();
   }
-  if (splits > 1) {
+  if (splits > 1 && !pool) {
     const int64_t total = int64_t(g.m) * g.n;
     const unsigned blocks = unsigned(std::min<int64_t>((total + 63) / 64, 8192));
     hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m, g.n,
@@ -2157,9 +2294,13 @@ hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, const Scratch* 
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.ldw = g.ldw > 0 ? g.ldw : g.n;
   const int steps = (g.k + TBK - 1) / TBK;
-  int splits = tiled_splits(g.m, g.n, g.k, g.canonical, (s && s->partials) ? s->partial_floats : 0);
+  const int64_t tiles = int64_t((g.n + TBN - 1) / TBN) * ((g.m + TBM - 1) / TBM);
+  const bool pool = s && s->queue_pool && tiles <= kPoolTiles;
+  int splits = tiled_splits(g.m, g.n, g.k, g.canonical,
+                            pool ? kPoolFloats : (s && s->partials) ? s->partial_floats : 0);
   p.steps_per_split = (steps + splits - 1) / splits;
-  p.partials = splits > 1 ? s->partials : nullptr;
+  p.partials = splits > 1 && !pool ? s->partials : nullptr;
+  p.pool = pool;
   const dim3 grid(unsigned((g.n + TBN - 1) / TBN), unsigned((g.m + TBM - 1) / TBM), unsigned(splits));
 #define TIA_TILED(WV, AV) hipLaunchKernelGGL((tiled_kernel<INT8, WV, AV>), grid, dim3(256), 0, stream, p)
   if (wvec && avec) TIA_TILED(true, true);
@@ -2167,7 +2308,7 @@ hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, const Scratch* 
   else if (avec) TIA_TILED(false, true);
   else TIA_TILED(false, false);
 #undef TIA_TILED
-  if (splits > 1) {
+  if (splits > 1 && !pool) {
     const int64_t total = int64_t(g.m) * g.n;
     const unsigned blocks = unsigned(std::min<int64_t>((total + 63) / 64, 8192));
     hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, stream, p.partials, splits, g.m, g.n,
@@ -2233,12 +2374,6 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
   return g.w_int8 ? launch_tiled<true>(g, wvec, avec, s, stream) : launch_tiled<false>(g, wvec, avec, s, stream);
 }
 
-size_t row_major_gemm_scratch_floats(int m, int n, int k, size_t capacity) {
-  if (m <= 0 || n <= 0 || k <= 0) return 0;
-  const int splits = m <= 32 ? skinny_splits(m, n, k, capacity) : tiled_splits(m, n, k, false, capacity);
-  return splits > 1 ? size_t(splits) * size_t(m) * size_t(n) : 0;
-}
-
 hipError_t argmax_partials(const float* vals, const int32_t* idx, int groups, int rows, int32_t* out,
                            hipStream_t stream) {
   if (rows < 1 || rows > 32 || groups < 1) return hipErrorInvalidValue;
@@ -2248,28 +2383,6 @@ hipError_t argmax_partials(const float* vals, const int32_t* idx, int groups, in
 
 bool gemm_ln_supported(int m, int k, int n) {
   return m >= 1 && m <= 32 && n >= 1 && k >= 64 && k % 64 == 0 && k / 64 <= kLnMaxChunks;
-}
-
-const Scratch* library_scratch(int device, hipStream_t stream, hipError_t* err) {
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, Scratch> table;
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = table.find({device, stream});
-  if (it != table.end()) return &it->second;
-  Scratch s;
-  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &capture) == hipSuccess && capture != hipStreamCaptureStatusNone) {
-    // Allocation is not allowed under capture: the stream must run one call eagerly first.
-    *err = hipErrorStreamCaptureUnsupported;
-    return nullptr;
-  }
-  const hipError_t e = hipMalloc(&s.partials, kScratchPartialFloats * sizeof(float));
-  if (e != hipSuccess) {
-    *err = e;
-    return nullptr;
-  }
-  s.partial_floats = kScratchPartialFloats;
-  return &(table[{device, stream}] = s);
 }
 
 size_t packed_w16_bytes(int k, int n) {

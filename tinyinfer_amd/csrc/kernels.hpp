@@ -45,13 +45,25 @@ struct Epilogue {
   bool p32 = false;
 };
 
-// Split-K partial sums of the skinny (M <= 32) GEMM: [splits][M][N] fp32.
-// Launches that share one Scratch must be ordered (same stream).
+// Where split work goes.  Caller memory: split-K partial sums [splits][M][N]
+// fp32 (and split-key attention states) finished by a second kernel or by the
+// caller (a deferred GEMM); launches that share one such Scratch must be
+// ordered (same stream).  queue_pool: no caller memory -- the split kernels use
+// the calling hardware queue's slot of a static pool in the library and the
+// last workgroup of each tile (or (b, h) row) finishes it in the same launch,
+// so nothing is allocated and every call can be captured into a graph
+// (queue_scratch.hpp); `partials` is then unused.
 struct Scratch {
   float* partials = nullptr;
   size_t partial_floats = 0;
+  bool queue_pool = false;
 };
 constexpr size_t kScratchPartialFloats = size_t(8) << 20;  // 32 MiB
+// The scratch the C ABIs pass.
+inline const Scratch* queue_pool_scratch() {
+  static const Scratch s{nullptr, 0, true};
+  return &s;
+}
 
 struct GemmArgs {
   const uint16_t* a = nullptr;  // fp16 [M, lda]
@@ -142,15 +154,6 @@ hipError_t splitk_residual_layernorm(const float* partials, int splits, int rows
                                      const uint16_t* bias, uint16_t* x, const uint16_t* gamma,
                                      const uint16_t* beta, uint16_t* norm, float eps,
                                      hipStream_t stream, bool p32 = false);
-// Floats of split-K partials that gemm() keeps in a scratch of `capacity`
-// floats for row-major weights without packing, LayerNorm or P32 operands (the
-// v2 ABI's GEMMs); 0 when the call runs unsplit.
-size_t row_major_gemm_scratch_floats(int m, int n, int k, size_t capacity);
-
-// Per-(device, stream) scratch owned by the library, created on the first call
-// on that stream (never under graph capture).  Returns nullptr and sets *err if
-// it cannot be created.
-const Scratch* library_scratch(int device, hipStream_t stream, hipError_t* err);
 // y = ws + bias (fp16 or fp32 output): the separate-epilogue pass of configs 6..11.
 hipError_t bias_epilogue(const float* ws, const uint16_t* bias, void* y, int64_t count, int n,
                          int dtype, hipStream_t stream);
@@ -199,9 +202,11 @@ struct AttnArgs {
   // and only its q_lengths[b] queries are written.
   const int32_t* q_row_start = nullptr;
 };
-// With a scratch, single-query attention over a long cache (kv_len 512 ..
-// 4096 for head_dim 64, 256 .. 2048 for 128) splits the keys of each (b, h)
-// across workgroups and merges the chunk states in a second kernel.
+// With the queue pool (queue_pool_scratch()), single-query attention over a
+// long cache (kv_len 512 .. 4096 for head_dim 64, 256 .. 2048 for 128) in the
+// ABI layout (no kv_slot, no lengths from offsets, no compact rows) splits the
+// keys of each (b, h) across workgroups; the last chunk of a row to finish
+// merges the row's chunk states in the same launch.
 hipError_t attention(const AttnArgs& args, hipStream_t stream, const Scratch* scratch = nullptr);
 
 hipError_t layernorm_f16(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y,

@@ -1,0 +1,108 @@
+// Scratch for kernels that finish their own split work inside one launch
+// (split-K GEMMs, split-key decode attention) without any allocation: static
+// device arrays, one slot per hardware queue.
+//
+// Why per queue: HIP enqueues every kernel dispatch with the AQL barrier bit
+// set, so dispatches on one hardware queue never overlap in time; kernels that
+// run at the same time come from different queues.  A kernel finds its queue's
+// slot through the queue address (__builtin_amdgcn_queue_ptr), which every
+// workgroup of a dispatch sees alike.  Streams share hardware queues (HIP maps
+// them round-robin onto GPU_MAX_HW_QUEUES queues, 4 by default), so a slot is
+// only ever used within one dispatch: split work is finished by the last
+// workgroup of the same launch, never by a later one.
+//
+// Slots are claimed once per queue with a compare-and-swap on the key table and
+// never released (a process uses a handful of queues per device), so a key
+// once seen is final; a stale cached read can only show a free entry, which the
+// compare-and-swap then resolves.  With more than kQueueSlots queues in use on
+// one device, further queues share slot (queue address / 4096) mod kQueueSlots
+// and calls that overlap on two such queues race.
+//
+// Each translation unit that includes this header and expands
+// TIA_QUEUE_POOL(prefix, floats, counters) holds its own pool; counters are
+// zero at load and every kernel leaves them zero.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tia {
+
+constexpr int kQueueSlots = 32;
+// Counters sit 32 apart (one 128-byte line each).
+constexpr int kCounterStride = 32;
+
+#define TIA_QUEUE_POOL(prefix, data_floats, counter_count)                                          \
+  static __device__ __align__(256) unsigned long long prefix##_keys[::tia::kQueueSlots];            \
+  static __device__ __align__(256) float prefix##_data[::tia::kQueueSlots][(data_floats)];          \
+  static __device__ __align__(256) unsigned prefix##_ctr[::tia::kQueueSlots][(counter_count) * ::tia::kCounterStride];
+
+// The slot of the calling dispatch's queue.  Called by a whole wave (every lane
+// gets the same answer); `key` is keys[lane] for lanes < kQueueSlots, read
+// earlier with a plain load (it may be stale: see above).
+__device__ __forceinline__ int queue_slot_resolve(unsigned long long* keys, unsigned long long key) {
+  const unsigned long long me = reinterpret_cast<unsigned long long>(__builtin_amdgcn_queue_ptr());
+  const int lane = int(threadIdx.x & 63);
+  const unsigned long long hit = __ballot(lane < kQueueSlots && key == me);
+  if (hit) return __builtin_ffsll(static_cast<long long>(hit)) - 1;
+  // Entries that read as free, in index order: claim the first that is free,
+  // or find this queue's key in it (a claim another workgroup made since).
+  unsigned long long cand = __ballot(lane < kQueueSlots && key == 0);
+  while (cand) {
+    const int e = __builtin_ffsll(static_cast<long long>(cand)) - 1;
+    cand &= cand - 1;
+    unsigned long long prev = 0;  // the entry's value before the exchange
+    if (lane == 0)
+      __hip_atomic_compare_exchange_strong(keys + e, &prev, me, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0, 64);
+    if (prev == 0 || prev == me) return e;
+  }
+  return int((me >> 12) % kQueueSlots);
+}
+
+// Relaxed agent-scope accesses: visible to every XCD (the hardware writes these
+// stores through the XCD's L2 and reads these loads coherently).
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival of one of `parties` workgroups at `counter` after it stored its
+// share with st_agent; called by a whole wave.  Returns true in the last
+// workgroup to arrive, which then reads every share with ld_agent and must
+// call depart().  The wait makes this wave's stores complete (acknowledged at
+// the coherence point) before the counter moves; the last arriver's loads
+// follow the counter's value.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, int parties) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  unsigned old = 0;
+  if ((threadIdx.x & 63) == 0)
+    old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readfirstlane(old);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return old == unsigned(parties - 1);
+}
+// The same for a whole workgroup whose waves all stored shares: each wave
+// waits for its own stores, the workgroup meets, one thread moves the counter,
+// and every thread learns whether this workgroup arrived last.
+__device__ __forceinline__ bool wg_arrive_last(unsigned* counter, int parties) {
+  __shared__ int last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == unsigned(parties - 1);
+  __syncthreads();
+  return last != 0;
+}
+// Leaves the counter at zero for the next dispatch on this queue (called by
+// the last arriver once; any thread of it).
+__device__ __forceinline__ void depart(unsigned* counter) {
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace tia
