@@ -60,21 +60,23 @@ __device__ __forceinline__ PoolSlot gemm_pool_slot() {
   return {gemm_pool_data[s], gemm_pool_ctr[s]};
 }
 
-// Sum of the `splits` partials of one output element at p, p + stride, ...
-// in the order splitk_epilogue_kernel adds them: split sp into group sp % 4 in
-// increasing order, then ((g0 + g1) + g2) + g3.  Agent-scope loads, up to 8 in
-// flight.
-__device__ __forceinline__ float pool_split_sum(const float* p, int64_t stride, int splits) {
-  float r[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int sp0 = 0; sp0 < splits; sp0 += 8) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = sp0 + u < splits ? ld_agent(p + int64_t(sp0 + u) * stride) : 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (sp0 + u < splits) r[u & 3] += v[u];
-  }
-  return ((r[0] + r[1]) + r[2]) + r[3];
+// Most partials a finishing thread loads from the pool (one round of 16-byte
+// loads, 64 registers); the launchers size pool split plans to it.
+constexpr int kPoolLoads = 16;
+// Pool split plans: at most this many splits of a tile whose finishing threads
+// each hold `per_thread` float4s.
+constexpr int pool_max_splits(int per_thread) { return kPoolLoads / per_thread; }
+// Rounds of loads the tile finisher takes at most (its tile is read by one
+// workgroup, so more splits mostly add bytes for one CU to fetch).
+constexpr int kTileRounds = 2;
+// A pool split plan over `tiles` tiles of `tile_floats` floats: at most
+// `max_splits` splits, the tile-contiguous partials within the slot, and
+// rounded to whole ranges of `units` (K steps or chunks).
+int pool_splits(int splits, int64_t tiles, int64_t tile_floats, int max_splits, int units) {
+  splits = std::max(1, std::min(splits, max_splits));
+  while (splits > 1 && tiles * splits * tile_floats > int64_t(kPoolFloats)) --splits;
+  const int per = (units + splits - 1) / splits;
+  return (units + per - 1) / per;
 }
 
 // A 16-bit load from global memory through a pointer the compiler cannot
@@ -291,7 +293,9 @@ __device__ __forceinline__ half8_t afrag(const uint16_t* a, int64_t lda, int M, 
   return out;
 }
 
-template <bool INT8, int MT, bool WVEC, bool AVEC>
+// POOL: this instantiation finishes splits > 1 in the launch through the queue
+// pool (the C ABIs); the other keeps its registers free of the finisher.
+template <bool INT8, int MT, bool WVEC, bool AVEC, bool POOL = false>
 __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) {
   __shared__ float red[4][MT * 16][65];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -357,30 +361,74 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) 
   __syncthreads();
 
   constexpr int kElems = MT * 16 * 64;
-  if (p.pool && p.splits > 1) {
-    // This split's sums to the queue's pool slot; the tile's last split to
-    // arrive sums them all in split order and runs the epilogue.
+  if (POOL && p.splits > 1) {
+    // This split's sums to the queue's pool slot, tile-contiguous: thread t
+    // holds columns 4 (t % 16) .. + 3 of row t / 16 (+ 16 in pass 1); the
+    // tile's last split to arrive loads every split's float4s of the rows
+    // below M in one round of loads spread over its threads, sums them in
+    // split order and runs the epilogue.
     const PoolSlot slot = gemm_pool_slot();
-    const int64_t plane = int64_t(p.m) * p.n;
-    for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
-      const int row = e >> 6, cc = e & 63, n = n0 + cc;
-      if (row < p.m && n < p.n)
-        st_agent(slot.parts + int64_t(split) * plane + int64_t(row) * p.n + n,
-                 red[0][row][cc] + red[1][row][cc] + red[2][row][cc] + red[3][row][cc]);
+    const auto rs = agent_rsrc(slot.parts, uint32_t(kPoolFloats * sizeof(float)));
+    const int t = int(threadIdx.x), c4 = t & 15, r0 = t >> 4;
+    auto off = [&](int sp, int pass, int idx) {
+      return uint32_t(((int64_t(tile) * p.splits + sp) * MT + pass) * kSkinnyThreads + idx) * 16u;
+    };
+#pragma unroll
+    for (int pass = 0; pass < MT; ++pass) {
+      const int row = r0 + 16 * pass;
+      f32x4_t v;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        v[c] = red[0][row][4 * c4 + c] + red[1][row][4 * c4 + c] + red[2][row][4 * c4 + c] + red[3][row][4 * c4 + c];
+      st_agent4(rs, off(split, pass, t), v);
     }
     if (!wg_arrive_last(slot.ctr + tile * kCounterStride, p.splits)) return;
+    // Group gi of the G groups of 16 R threads (R = rows below M in a pass)
+    // sums splits [gi spg, (gi + 1) spg) in order, group sums meet in LDS and
+    // group 0 adds them in group order, then runs the epilogue.
+    constexpr int SMAX = pool_max_splits(MT);
+    __shared__ f32x4_t gsum[kSkinnyThreads][MT];
+    const int rr = min(p.m, 16), per = 16 * rr, ng = max(1, kSkinnyThreads / per);
+    const int spg = (p.splits + ng - 1) / ng;
+    const int gi = t / per, wi = t - gi * per;
+    f32x4_t v[MT][SMAX];
+#pragma unroll
+    for (int pass = 0; pass < MT; ++pass)
+#pragma unroll
+      for (int u = 0; u < SMAX; ++u) {
+        const int sp = gi * spg + u;
+        v[pass][u] = (gi < ng && u < spg && sp < p.splits && (wi >> 4) + 16 * pass < p.m) ? ld_agent4(rs, off(sp, pass, wi))
+                                                                                          : f32x4_t{};
+      }
+    depart(slot.ctr + tile * kCounterStride);
+#pragma unroll
+    for (int pass = 0; pass < MT; ++pass) {
+      f32x4_t acc = v[pass][0];
+#pragma unroll
+      for (int u = 1; u < SMAX; ++u)
+        if (u < spg && gi * spg + u < p.splits) acc += v[pass][u];
+      if (gi < ng) gsum[t][pass] = acc;
+    }
+    __syncthreads();
+    if (gi != 0) return;
     with_epilogue_kind(p.epi, [&](auto kind) {
       constexpr int K = decltype(kind)::value;
-      for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
-        const int row = e >> 6, n = n0 + (e & 63);
-        if (row >= p.m || n >= p.n) continue;
-        const float total = pool_split_sum(slot.parts + int64_t(row) * p.n + n, plane, p.splits);
-        const float bias = K == EPI_RAW_F32 ? 0.f : epilogue_bias(p.epi, n);
-        const float resid = K == EPI_RESIDUAL ? h2f(p.epi.residual[r_off(p.epi, row, n)]) : 0.f;
-        epilogue_k<K>(p.epi, row, n, total, bias, resid);
+#pragma unroll
+      for (int pass = 0; pass < MT; ++pass) {
+        const int row = (wi >> 4) + 16 * pass;
+        if (row >= p.m) continue;
+        f32x4_t acc = gsum[wi][pass];
+        for (int q = 1; q < ng && q * spg < p.splits; ++q) acc += gsum[q * per + wi][pass];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int n = n0 + 4 * (wi & 15) + c;
+          if (n >= p.n) continue;
+          const float bias = K == EPI_RAW_F32 ? 0.f : epilogue_bias(p.epi, n);
+          const float resid = K == EPI_RESIDUAL ? h2f(p.epi.residual[r_off(p.epi, row, n)]) : 0.f;
+          epilogue_k<K>(p.epi, row, n, acc[c], bias, resid);
+        }
       }
     });
-    depart(slot.ctr + tile * kCounterStride);
     return;
   }
   for (int e = threadIdx.x; e < kElems; e += kSkinnyThreads) {
@@ -1085,44 +1133,46 @@ __device__ __forceinline__ void wait_chunk(int outstanding) {
 constexpr int tile_pitch(int bn) { return bn + 4; }
 
 // In-launch split-K finish of a TR x BN fp32 tile staged in LDS at pitch
-// tile_pitch(BN), rows r0.., columns n0.. (the thread mapping of
-// tile_epilogue): this split's sums go to the pool slot at
-// parts[(split m + row) n + col]; the last split of the tile to arrive adds
-// every split's sums (pool_split_sum's order) back into the LDS tile and
-// returns true, and the caller then runs tile_epilogue on it; every other
-// workgroup returns false.
+// tile_pitch(BN), in tile_epilogue's thread mapping (thread t holds RPT
+// float4s: columns 4 (t % (BN / 4)) .. + 3 of tile rows t / (BN / 4) + i RS).
+// This split's float4s go to the queue's pool slot, tile-contiguous in the
+// threads' own order (float4 i of thread t of split s at ((tile splits + s)
+// RPT + i) NT + t), so every store and load is a coalesced 16-byte access; the
+// last split of the tile to arrive loads every split's float4s in one round
+// (splits <= pool_max_splits(RPT)), adds them in split order back into the
+// LDS tile and returns true, and the caller then runs tile_epilogue on it;
+// every other workgroup returns false.
 template <int TR, int BN, int NT>
-__device__ bool tile_split_finish(float* ctile, int r0, int n0, int m, int n, int split, int splits, int tile) {
-  constexpr int CG = BN / 4, RS = NT / CG, RPT = TR / RS;
-  const int c4 = int(threadIdx.x) % CG, rl0 = int(threadIdx.x) / CG;
-  const int col = n0 + 4 * c4;
+__device__ bool tile_split_finish(float* ctile, int split, int splits, int tile) {
+  constexpr int CG = BN / 4, RS = NT / CG, RPT = TR / RS, SMAX = pool_max_splits(RPT);
+  static_assert(SMAX >= 1, "a finishing thread's float4s fit one round of loads");
+  // (splits <= kTileRounds * SMAX: the finish takes up to kTileRounds rounds.)
+  const int t = int(threadIdx.x), c4 = t % CG, rl0 = t / CG;
   const PoolSlot slot = gemm_pool_slot();
-  const int64_t plane = int64_t(m) * n;
-  if (col < n) {
-#pragma unroll 1
-    for (int i = 0; i < RPT; ++i) {
-      const int row = r0 + rl0 + i * RS;
-      if (row >= m) break;
-      const float* v = ctile + (rl0 + i * RS) * tile_pitch(BN) + 4 * c4;
-      float* dst = slot.parts + int64_t(split) * plane + int64_t(row) * n + col;
+  const auto rs = agent_rsrc(slot.parts, uint32_t(kPoolFloats * sizeof(float)));
+  auto off = [&](int sp, int i) { return uint32_t(((int64_t(tile) * splits + sp) * RPT + i) * NT + t) * 16u; };
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (col + c < n) st_agent(dst + c, v[c]);
-    }
-  }
+  for (int i = 0; i < RPT; ++i)
+    st_agent4(rs, off(split, i), *reinterpret_cast<const f32x4_t*>(ctile + (rl0 + i * RS) * tile_pitch(BN) + 4 * c4));
   if (!wg_arrive_last(slot.ctr + tile * kCounterStride, splits)) return false;
-  if (col < n) {
-#pragma unroll 1
-    for (int i = 0; i < RPT; ++i) {
-      const int row = r0 + rl0 + i * RS;
-      if (row >= m) break;
-      float* v = ctile + (rl0 + i * RS) * tile_pitch(BN) + 4 * c4;
-      const float* src = slot.parts + int64_t(row) * n + col;
+  f32x4_t acc[RPT];
+  for (int r0 = 0; r0 < splits; r0 += SMAX) {
+    f32x4_t v[RPT][SMAX];
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (col + c < n) v[c] = pool_split_sum(src + c, plane, splits);
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int sp = 0; sp < SMAX; ++sp) v[i][sp] = r0 + sp < splits ? ld_agent4(rs, off(r0 + sp, i)) : f32x4_t{};
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      if (r0 == 0) acc[i] = v[i][0];
+      else acc[i] += v[i][0];
+#pragma unroll
+      for (int sp = 1; sp < SMAX; ++sp)
+        if (r0 + sp < splits) acc[i] += v[i][sp];
     }
   }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) *reinterpret_cast<f32x4_t*>(ctile + (rl0 + i * RS) * tile_pitch(BN) + 4 * c4) = acc[i];
   depart(slot.ctr + tile * kCounterStride);
   return true;
 }
@@ -1302,7 +1352,7 @@ __device__ __forceinline__ void tile_of_block(int gm_max, int tiles_n, int tiles
   tn = r / gm;
 }
 
-template <int WM, int WN, int MT, int R, int S>
+template <int WM, int WN, int MT, int R, int S, bool POOL = false>
 __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
   constexpr int BM = WM * MT * 16, BN = WN * R * 16;
   constexpr int NA = (BM / 16) * 2, NB = BN / 16, NL = NA + NB;
@@ -1426,8 +1476,8 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(PanelParams p) {
       for (int v = 0; v < 4; ++v)
         ctile[((wm * MT + t) * 16 + 4 * g + v) * tile_pitch(BN) + (wn * R + r) * 16 + j] = acc[t][r][v];
   __syncthreads();
-  if (p.pool && p.splits > 1) {
-    if (tile_split_finish<BM, BN, 256>(ctile, m0, cb0 * 16, p.m, p.n, split, p.splits, tm * p.tiles_n + tn))
+  if (POOL && p.splits > 1) {
+    if (tile_split_finish<BM, BN, 256>(ctile, split, p.splits, tm * p.tiles_n + tn))
       tile_epilogue<BM, BN, 256>(p.epi, ctile, m0, cb0 * 16, p.m, p.n, bias, nullptr, split);
     return;
   }
@@ -1454,7 +1504,7 @@ struct TiledParams {
 };
 constexpr int TBM = 64, TBN = 64, TBK = 32, TPAD = 40;  // LDS row pitch in halves
 
-template <bool INT8, bool WVEC, bool AVEC>
+template <bool INT8, bool WVEC, bool AVEC, bool POOL = false>
 __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
   // A and W^T double buffers; after the K loop the same bytes hold the fp32
   // output tile for the epilogue.
@@ -1584,9 +1634,8 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledParams p) {
       for (int v = 0; v < 4; ++v)
         ctile[(wm * 32 + 16 * t + 4 * g + v) * tile_pitch(TBN) + wn * 32 + 16 * c + j] = acc[t][c][v];
   __syncthreads();
-  if (p.pool && gridDim.z > 1) {
-    if (tile_split_finish<TBM, TBN, 256>(ctile, m0, n0, p.m, p.n, split, int(gridDim.z),
-                                         int(blockIdx.x + gridDim.x * blockIdx.y)))
+  if (POOL && gridDim.z > 1) {
+    if (tile_split_finish<TBM, TBN, 256>(ctile, split, int(gridDim.z), int(blockIdx.x + gridDim.x * blockIdx.y)))
       tile_epilogue<TBM, TBN, 256>(p.epi, ctile, m0, n0, p.m, p.n, bias, nullptr, split);
     return;
   }
@@ -1706,6 +1755,13 @@ int skinny_splits(int m, int n, int k, size_t capacity) {
   return (steps + spb - 1) / spb;
 }
 
+// The skinny finisher spreads a tile's splits over its idle threads: rows
+// below M of each 16-row pass take 16 threads each, and the 256 threads form
+// skinny_groups(M) such groups, each summing a run of at most
+// pool_max_splits(MT) splits.
+int skinny_groups(int m) { return std::max(1, kSkinnyThreads / (16 * std::min(m, 16))); }
+int skinny_pool_max_splits(int m, int mt) { return skinny_groups(m) * pool_max_splits(mt); }
+
 template <bool INT8, int MT>
 hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch* s,
                          hipStream_t stream, int* deferred) {
@@ -1717,6 +1773,7 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   p.steps = (g.k + 31) / 32;
   const bool pool = s && s->queue_pool && !deferred && p.ntile <= kPoolTiles;
   int splits = skinny_splits(g.m, g.n, g.k, pool ? kPoolFloats : (s && s->partials) ? s->partial_floats : 0);
+  if (pool) splits = pool_splits(splits, p.ntile, int64_t(MT) * kSkinnyThreads * 4, skinny_pool_max_splits(g.m, MT), p.steps);
   const int spb = (p.steps + splits - 1) / splits;
   p.steps_per_block = spb;
   p.splits = splits;
@@ -1725,7 +1782,13 @@ hipError_t launch_skinny(const GemmArgs& g, bool wvec, bool avec, const Scratch*
   p.partials = s ? s->partials : nullptr;
   if (p.defer && (!p.partials || size_t(splits) * g.m * g.n > s->partial_floats)) return hipErrorInvalidValue;
   const dim3 grid(unsigned(p.ntile) * unsigned(splits));
-#define TIA_SKINNY(WV, AV) hipLaunchKernelGGL((skinny_kernel<INT8, MT, WV, AV>), grid, dim3(kSkinnyThreads), 0, stream, p)
+#define TIA_SKINNY(WV, AV)                                                                                 \
+  do {                                                                                                     \
+    if (pool && splits > 1)                                                                                \
+      hipLaunchKernelGGL((skinny_kernel<INT8, MT, WV, AV, true>), grid, dim3(kSkinnyThreads), 0, stream, p); \
+    else                                                                                                   \
+      hipLaunchKernelGGL((skinny_kernel<INT8, MT, WV, AV>), grid, dim3(kSkinnyThreads), 0, stream, p);       \
+  } while (0)
   if (wvec && avec) TIA_SKINNY(true, true);
   else if (wvec) TIA_SKINNY(true, false);
   else if (avec) TIA_SKINNY(false, true);
@@ -1964,7 +2027,11 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
   constexpr size_t kLds = size_t(S) * NL * 1024 + BN * 4;
   static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&panel_gemm_kernel<WM, WN, MT, R, S>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds));
+  static hipError_t attr_pool = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&panel_gemm_kernel<WM, WN, MT, R, S, true>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds));
   if (attr != hipSuccess) return attr;
+  if (attr_pool != hipSuccess) return attr_pool;
   PanelParams p{};
   p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
@@ -1981,6 +2048,7 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
   if (may_split && capacity > 0 && tiles < 192) {
     splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, p.kc / (S - 1))));
     while (splits > 1 && size_t(splits) * g.m * g.n > capacity) --splits;
+    if (pool) splits = pool_splits(splits, tiles, BM * BN, kTileRounds * pool_max_splits(BM / (256 / (BN / 4))), p.kc);
   }
   p.chunks_per_split = (p.kc + splits - 1) / splits;
   splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
@@ -1988,8 +2056,12 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
   p.defer = deferred != nullptr && splits > 1;
   p.pool = pool;
   p.partials = s ? s->partials : nullptr;
-  hipLaunchKernelGGL((panel_gemm_kernel<WM, WN, MT, R, S>), dim3(unsigned(tiles * splits)), dim3(256), kLds,
-                     stream, p);
+  if (pool && splits > 1)
+    hipLaunchKernelGGL((panel_gemm_kernel<WM, WN, MT, R, S, true>), dim3(unsigned(tiles * splits)), dim3(256), kLds,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((panel_gemm_kernel<WM, WN, MT, R, S>), dim3(unsigned(tiles * splits)), dim3(256), kLds,
+                       stream, p);
   if (p.defer) {
     *deferred = splits;
     return hipGetLastError();
@@ -2016,7 +2088,12 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
 hipError_t launch_panel(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* deferred) {
   const int64_t tiles64 = int64_t((g.m + 63) / 64) * ((g.n + 63) / 64);
   const int64_t tiles32 = int64_t((g.m + 31) / 32) * ((g.n + 63) / 64);
-  if (!g.canonical && tiles64 < 192 && tiles32 >= 192) return launch_panel_cfg<1, 4, 2, 1, 4>(g, s, stream, deferred);
+  // Pool plans finish each tile in one workgroup with a bounded split count
+  // (4 for 64 x 64 tiles, 8 for 32 x 64), so a grid short of tiles takes the
+  // 32-row tiles there too.
+  const bool pool = s && s->queue_pool && !deferred;
+  if (!g.canonical && tiles64 < 192 && (tiles32 >= 192 || pool))
+    return launch_panel_cfg<1, 4, 2, 1, 4>(g, s, stream, deferred);
   return launch_panel_cfg<1, 4, 4, 1, 3>(g, s, stream, deferred);
 }
 
@@ -2068,7 +2145,7 @@ __global__ void pack_w16_kernel(const int8_t* q, int64_t ldq, const float* scale
 // K in chunks of 32 moved HBM/L2 -> LDS by global_load_lds_dwordx4 (A
 // fragments of 16 rows x 32 K in MFMA A order, B records as stored), S stages
 // as in the int8 panel kernel.  The epilogue runs from the accumulators.
-template <int WM, int WN, int MT, int R, int S, int EP = 1, int OCC = 2>
+template <int WM, int WN, int MT, int R, int S, int EP = 1, int OCC = 2, bool POOL = false>
 __global__ __launch_bounds__(WM * WN * 64, OCC) void f16_gemm_kernel(F16GemmParams p) {
   constexpr int W = WM * WN, NT = W * 64;
   constexpr int BM = WM * MT * 16, BN = WN * R * 16;
@@ -2163,9 +2240,9 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void f16_gemm_kernel(F16GemmPara
           ctile[(rb + 4 * g + v) * tile_pitch(BN) + (wn * R + r) * 16 + j] = acc[t][r][v];
     }
     __syncthreads();
-    if constexpr (EP == 1) {
-      if (p.pool && p.splits > 1) {
-        if (tile_split_finish<PR, BN, NT>(ctile, m0, cb0 * 16, p.m, p.n, split, p.splits, tm * p.tiles_n + tn))
+    if constexpr (EP == 1 && POOL) {
+      if (p.splits > 1) {
+        if (tile_split_finish<PR, BN, NT>(ctile, split, p.splits, tm * p.tiles_n + tn))
           tile_epilogue<PR, BN, NT>(p.epi, ctile, m0, cb0 * 16, p.m, p.n, bias, nullptr, split);
         return;
       }
@@ -2183,6 +2260,11 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
   static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds));
   if (attr != hipSuccess) return attr;
+  static hipError_t attr_pool =
+      EP == 1 ? hipFuncSetAttribute(reinterpret_cast<const void*>(&f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC, EP == 1>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds))
+              : hipSuccess;
+  if (attr_pool != hipSuccess) return attr_pool;
   F16GemmParams p{};
   p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_f16p);
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
@@ -2199,6 +2281,9 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
   if (!g.canonical && capacity > 0 && tiles < 192) {
     splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, p.kk / (S - 1))));
     while (splits > 1 && size_t(splits) * g.m * g.n > capacity) --splits;
+    if (pool)
+      splits = pool_splits(splits, tiles, BM * BN,
+                           kTileRounds * pool_max_splits(std::max(1, BM / (WM * WN * 64 / (BN / 4)))), p.kk);
   }
   p.chunks_per_split = (p.kk + splits - 1) / splits;
   splits = (p.kk + p.chunks_per_split - 1) / p.chunks_per_split;
@@ -2206,8 +2291,12 @@ hipError_t launch_f16_cfg(const GemmArgs& g, const Scratch* s, hipStream_t strea
   p.defer = deferred != nullptr && splits > 1;
   p.pool = pool;
   p.partials = s ? s->partials : nullptr;
-  hipLaunchKernelGGL((f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC>), dim3(unsigned(tiles * splits)), dim3(WM * WN * 64),
-                     kLds, stream, p);
+  if (pool && splits > 1)
+    hipLaunchKernelGGL((f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC, EP == 1>), dim3(unsigned(tiles * splits)),
+                       dim3(WM * WN * 64), kLds, stream, p);
+  else
+    hipLaunchKernelGGL((f16_gemm_kernel<WM, WN, MT, R, S, EP, OCC>), dim3(unsigned(tiles * splits)), dim3(WM * WN * 64),
+                       kLds, stream, p);
   if (p.defer) {
     *deferred = splits;
     return hipGetLastError();
@@ -2298,11 +2387,18 @@ hipError_t launch_tiled(const GemmArgs& g, bool wvec, bool avec, const Scratch* 
   const bool pool = s && s->queue_pool && tiles <= kPoolTiles;
   int splits = tiled_splits(g.m, g.n, g.k, g.canonical,
                             pool ? kPoolFloats : (s && s->partials) ? s->partial_floats : 0);
+  if (pool) splits = pool_splits(splits, tiles, TBM * TBN, kTileRounds * pool_max_splits(TBM / (256 / (TBN / 4))), steps);
   p.steps_per_split = (steps + splits - 1) / splits;
   p.partials = splits > 1 && !pool ? s->partials : nullptr;
   p.pool = pool;
   const dim3 grid(unsigned((g.n + TBN - 1) / TBN), unsigned((g.m + TBM - 1) / TBM), unsigned(splits));
-#define TIA_TILED(WV, AV) hipLaunchKernelGGL((tiled_kernel<INT8, WV, AV>), grid, dim3(256), 0, stream, p)
+#define TIA_TILED(WV, AV)                                                                 \
+  do {                                                                                     \
+    if (pool && splits > 1)                                                                \
+      hipLaunchKernelGGL((tiled_kernel<INT8, WV, AV, true>), grid, dim3(256), 0, stream, p); \
+    else                                                                                   \
+      hipLaunchKernelGGL((tiled_kernel<INT8, WV, AV>), grid, dim3(256), 0, stream, p);       \
+  } while (0)
   if (wvec && avec) TIA_TILED(true, true);
   else if (wvec) TIA_TILED(true, false);
   else if (avec) TIA_TILED(false, true);

@@ -68,6 +68,21 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
 __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16-byte versions through a buffer resource: the same agent scope as the
+// accesses above (cache policy SC1 = 0x10 on gfx950, which the relaxed
+// agent-scope atomics above also carry).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4q_t __attribute__((ext_vector_type(4)));
+constexpr int kAgentScopePolicy = 0x10;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t agent_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+__device__ __forceinline__ void st_agent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4q_t, v), r, int(byte_off), 0, kAgentScopePolicy);
+}
+__device__ __forceinline__ f32x4_t ld_agent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, kAgentScopePolicy));
+}
 
 // Arrival of one of `parties` workgroups at `counter` after it stored its
 // share with st_agent; called by a whole wave.  Returns true in the last
