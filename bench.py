@@ -342,44 +342,159 @@ def xl_artifact_path():
     return m
 
 
-def run_xl(steps):
+def xl_parity_artifact_path():
+    """A 2-layer GPT-2 XL-shaped artifact (d 1600, 25 heads, MLP 6400, the full
+    vocabulary and LM head) for the configs[4] greedy parity report: the CPU
+    oracle runs its whole workload in under a minute."""
+    from tinyinfer_amd.artifact import GPT2_XL, write_synthetic
+    d = Path(tempfile.gettempdir()) / "tinyinfer_amd_gpt2_xl2_seed42_v1"
+    m = d / "manifest.json"
+    if not m.exists():
+        write_synthetic(d, dict(GPT2_XL, layers=2), seed=42)
+    return m
+
+
+def xl_prompts():
+    """configs[4]'s 64 prompts: lengths U[128,512], ids U[0,50257), seed 42."""
+    rng = np.random.default_rng(42)
+    lens = rng.integers(128, 513, 64)
+    return [rng.integers(0, 50257, int(n)).tolist() for n in lens], lens
+
+
+def xl_concurrent(models, prompts, new):
+    """configs[4]'s 64 requests as one dynamic batch on one GPU: the two halves of
+    32 (the reference ABI's max_batch per context) decode at the same time, each
+    in its own context driven by its own host thread (ctypes releases the GIL, so
+    the two ti_llm_greedy_batch calls overlap on the GPU).  Returns the decode
+    window (earliest first token to latest last token, host clock), the 64
+    requests' tokens and the two batches' TTFTs."""
+    import threading
+    out, errors = [None, None], []
+
+    def work(i):
+        try:
+            t0 = time.perf_counter()
+            out[i] = (t0, models[i].greedy(prompts[32 * i:32 * i + 32], new))
+        except Exception as e:  # re-raised below, in the caller's thread
+            errors.append(e)
+    threads = [threading.Thread(target=work, args=(i,)) for i in (0, 1)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    if errors:
+        raise errors[0]
+    first = min(t0 + min(r["ttft_ms"]) / 1e3 for t0, r in out)
+    last = max(t0 + max(r["total_ms"]) / 1e3 for t0, r in out)
+    return last - first, out[0][1]["tokens"] + out[1][1]["tokens"], [min(r["ttft_ms"]) for _, r in out]
+
+
+def xl_sequential(model, prompts, new):
+    """The same 64 requests as two batches of 32 one after the other in one
+    context (slots 0..63): summed decode time (first to last token of each)."""
+    model.reset_all()
+    decode_s, ttft, tokens = 0.0, [], []
+    for half in (0, 1):
+        res = model.greedy(prompts[32 * half:32 * half + 32], new, slots=list(range(32 * half, 32 * half + 32)))
+        decode_s += (max(res["total_ms"]) - min(res["ttft_ms"])) / 1e3
+        ttft.append(min(res["ttft_ms"]))
+        tokens += res["tokens"]
+    return decode_s, tokens, ttft
+
+
+def xl_greedy_parity(new):
+    """configs[4]'s workload (64 prompts of 128..512 ids, `new` greedy tokens,
+    concurrent halves) on the 2-layer XL-shaped artifact, GPU against the CPU
+    oracle: per diverging request the first divergence index and the oracle's
+    own logit gap between the two picks there (the whole 48-layer workload would
+    take hours on the host)."""
+    import oracle
+    from tinyinfer_amd import LLM_LIB, require
+    from tinyinfer_amd.artifact import load_tensors
+    from tinyinfer_amd.runtime import NativeModel
+    m = xl_parity_artifact_path()
+    prompts, _ = xl_prompts()
+    with NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=32, capacity=640) as m0, \
+            NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=32, capacity=640) as m1:
+        _, gpu, _ = xl_concurrent((m0, m1), prompts, new)
+    man, tensors = load_tensors(m)
+    t0 = time.perf_counter()
+    cpu = oracle.Gpt2(tensors, man["architecture"], slots=65, capacity=640 + 1)
+    halves = (list(range(32)), list(range(32, 64)))
+    ref = [[] for _ in range(64)]
+    for sl in halves:
+        _, nxt = cpu.forward(sl, [prompts[i] for i in sl], logits=False)
+        for i, t in zip(sl, nxt):
+            ref[i].append(int(t))
+        for _ in range(new - 1):
+            _, nxt = cpu.forward(sl, [[ref[i][-1]] for i in sl], logits=False)
+            for i, t in zip(sl, nxt):
+                ref[i].append(int(t))
+    diverged = []
+    for b in range(64):
+        idx = next((i for i, (x, y) in enumerate(zip(gpu[b], ref[b])) if x != y), None)
+        if idx is not None:
+            cpu.reset(64)
+            lg, _ = cpu.forward([64], [prompts[b] + ref[b][:idx]])
+            diverged.append({"request": b, "first_divergence": idx,
+                             "oracle_gap": float(lg[0][ref[b][idx]] - lg[0][gpu[b][idx]])})
+    cpu.close()
+    return {"artifact": "GPT-2 XL shapes, 2 layers (d 1600, 25 heads, MLP 6400, full vocabulary), seed 42",
+            "requests": 64, "new_tokens": new, "identical_requests": 64 - len(diverged), "diverged": diverged,
+            "max_oracle_gap": max((e["oracle_gap"] for e in diverged), default=None),
+            "oracle_s": time.perf_counter() - t0}
+
+
+def run_xl(steps, parity=True):
     """GPT-2 XL INT8 (48 layers, d 1600, 25 heads, MLP 6400), random-init
     N(0,0.02) seed 42; 64 requests with seeded prompt lengths U[128,512] (ids
     U[0,50257)), prefill then 128 greedy tokens each.  The runtime ABI takes at
-    most 32 rows per call (reference max_batch), so the 64 requests run as two
-    batches of 32 in their own KV slots; decode tokens/s = 64 * 127 / (sum over the
-    two batches of t_last - t_first)."""
+    most 32 rows per call (reference max_batch): the dynamic batch of 64 runs as
+    two contexts of 32 decoding at the same time (decode tokens/s = 64 * 127 /
+    the decode window); the sequential plan (both batches one after the other in
+    one context) is reported beside it, and the two plans' tokens are compared.
+    greedy_parity: the same workload on a 2-layer XL-shaped artifact against the
+    CPU oracle."""
     from tinyinfer_amd import LLM_LIB, require
     from tinyinfer_amd.runtime import NativeModel
     t0 = time.perf_counter()
     m = xl_artifact_path()
     d = m.parent
     gen_s = time.perf_counter() - t0
-    rng = np.random.default_rng(42)
-    lens = rng.integers(128, 513, 64)
-    prompts = [rng.integers(0, 50257, int(n)).tolist() for n in lens]
+    prompts, lens = xl_prompts()
     new = 128
-    runs = []
-    with NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=64, capacity=640) as model:
+    runs, seq_runs = [], []
+    with NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=32, capacity=640) as m0, \
+            NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=32, capacity=640) as m1:
         for rep in range(max(1, steps) + 1):  # first repetition is warmup
-            model.reset_all()
-            decode_s, ttft = 0.0, []
+            m0.reset_all()
+            m1.reset_all()
             t_run = time.perf_counter()
-            for half in (0, 1):
-                res = model.greedy(prompts[32 * half:32 * half + 32], new, slots=list(range(32 * half, 32 * half + 32)))
-                t_first, t_last = min(res["ttft_ms"]), max(res["total_ms"])
-                decode_s += (t_last - t_first) / 1e3
-                ttft.append(t_first)
+            window, tokens, ttft = xl_concurrent((m0, m1), prompts, new)
             if rep:
-                runs.append({"decode_tokens_per_s": 64 * (new - 1) / decode_s, "ttft_ms": ttft,
+                runs.append({"decode_tokens_per_s": 64 * (new - 1) / window, "ttft_ms": ttft,
                              "wall_s": time.perf_counter() - t_run})
+        concurrent_tokens = tokens
+    with NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=64, capacity=640) as model:
+        for rep in range(2):  # warmup, then one timed run
+            decode_s, seq_tokens, seq_ttft = xl_sequential(model, prompts, new)
+            if rep:
+                seq_runs.append({"decode_tokens_per_s": 64 * (new - 1) / decode_s, "ttft_ms": seq_ttft})
     rates = [r["decode_tokens_per_s"] for r in runs]
-    return {"decode_tokens_per_s": float(np.median(rates)), "samples": rates,
-            "ttft_ms_p50_per_batch": [float(np.median([r["ttft_ms"][i] for r in runs])) for i in (0, 1)],
-            "wall_s_per_run": float(np.median([r["wall_s"] for r in runs])),
-            "prompt_len_mean": float(lens.mean()), "requests": 64, "new_tokens": new,
-            "weights_bytes": int((d / "weights.bin").stat().st_size), "artifact_generation_s": gen_s,
-            "note": "two runtime batches of 32 (reference max_batch), KV slots 0..63, capacity 640"}
+    out = {"decode_tokens_per_s": float(np.median(rates)), "samples": rates,
+           "ttft_ms_p50_per_batch": [float(np.median([r["ttft_ms"][i] for r in runs])) for i in (0, 1)],
+           "wall_s_per_run": float(np.median([r["wall_s"] for r in runs])),
+           "prompt_len_mean": float(lens.mean()), "requests": 64, "new_tokens": new,
+           "weights_bytes": int((d / "weights.bin").stat().st_size), "artifact_generation_s": gen_s,
+           "plan": "dynamic batch of 64 as two contexts of 32 (reference max_batch) decoding at the same time, "
+                   "one host thread each; capacity 640",
+           "sequential": {"decode_tokens_per_s": seq_runs[0]["decode_tokens_per_s"],
+                          "ttft_ms_per_batch": seq_runs[0]["ttft_ms"],
+                          "plan": "the two batches of 32 one after the other in one context, KV slots 0..63"},
+           "tokens_identical_across_plans": concurrent_tokens == seq_tokens}
+    if parity:
+        out["greedy_parity"] = xl_greedy_parity(new)
+    return out
 
 
 def run_limits(rp):

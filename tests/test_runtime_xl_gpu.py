@@ -216,8 +216,47 @@ def test_xl_configs4_workload_vs_oracle(artifact):
             cpu.close()
     print(f"configs[4] greedy, 64 requests x {WORKLOAD_TOKENS} tokens: {64 - len(gaps)}/64 identical; "
           f"first divergence (request: index, oracle gap) {gaps}")
-    assert all(0 <= gap <= 1e-2 for _, gap in gaps.values()), gaps
-    assert len(gaps) <= 16, gaps
+    # Measured on MI355X: 53/64 requests identical over 128 tokens, every
+    # divergence at an oracle gap <= 0.0015 (a near-tie; the kernels and the
+    # oracle are deterministic, so the count is a property of the code, not of
+    # the run).  Bounds: at most 12 diverging requests, gaps <= 5e-3.
+    assert all(0 <= gap <= 5e-3 for _, gap in gaps.values()), gaps
+    assert len(gaps) <= 12, gaps
+
+
+def test_xl_configs4_concurrent_halves_equal_sequential(artifact):
+    """configs[4]'s dynamic batch of 64 as two contexts of 32 decoding at the same
+    time (one host thread each, as bench.py runs it) gives every request the
+    tokens the sequential plan (one context, the halves one after the other)
+    gives it: contexts share nothing and a request's sums do not depend on its
+    batch."""
+    import threading
+    from tinyinfer_amd import LLM_LIB
+    from tinyinfer_amd.runtime import NativeModel
+    prompts = configs4_prompts()
+    new = 32
+    say("configs[4] on the 2-layer XL-shaped artifact: sequential halves in one context")
+    with NativeModel(LLM_LIB, artifact, max_batch=32, cache_slots=64, capacity=640) as m:
+        seq = []
+        for sl in HALVES:
+            seq += m.greedy([prompts[i] for i in sl], new, slots=sl)["tokens"]
+    say("configs[4]: the two halves at once, two contexts, two threads")
+    with NativeModel(LLM_LIB, artifact, max_batch=32, cache_slots=32, capacity=640) as m0, \
+            NativeModel(LLM_LIB, artifact, max_batch=32, cache_slots=32, capacity=640) as m1:
+        out, errors = [None, None], []
+
+        def work(i, model):
+            try:
+                out[i] = model.greedy([prompts[j] for j in HALVES[i]], new)["tokens"]
+            except Exception as e:
+                errors.append(e)
+        threads = [threading.Thread(target=work, args=(i, mm)) for i, mm in enumerate((m0, m1))]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert not errors, errors
+    assert out[0] + out[1] == seq
 
 
 # ---------------------------------------------------------------- 48 layers: properties
