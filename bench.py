@@ -79,22 +79,29 @@ def gemv_bytes(m, k, n):
 
 def pmc_traffic(kernel):
     """HBM bytes per launch of the roofline GEMV from the two rocprofv3 PMC passes
-    (FETCH_SIZE, WRITE_SIZE; copy-calibrated) summarised in profiles/, with the
-    commit they were measured at.  Counters cannot be read inside this run (a
-    PMC pass is its own profiler run), so the figure is taken from that summary
-    only while it names the same kernel this run times; otherwise None."""
+    (FETCH_SIZE, WRITE_SIZE; copy-calibrated) summarised in profiles/.  Counters
+    cannot be read inside this run (a PMC pass is its own profiler run), so the
+    figure is taken from that summary only while it names exactly the kernel
+    this run times (full template) and was measured on this tree's kernel
+    source (its source_sha256 equals the SHA-256 of tinyinfer_amd/csrc/gemm.hip);
+    otherwise None, with the reason."""
+    import hashlib
     path = ROOT / "profiles" / "w8a16_gemv_m1_k3072_n768_pmc.md"
     if not path.is_file():
-        return None, None
+        return None, "no PMC summary"
     fields = {}
     for text in path.read_text().splitlines():
-        if ":" in text and text.split(":", 1)[0] in ("traffic_bytes_per_launch", "kernel", "commit"):
+        if ":" in text and text.split(":", 1)[0] in ("traffic_bytes_per_launch", "kernel", "commit", "source_sha256"):
             key, value = text.split(":", 1)
             fields[key] = value.strip()
-    if fields.get("kernel", "").split("<")[0] != kernel.split("<")[0] or "traffic_bytes_per_launch" not in fields:
-        return None, None
+    source = hashlib.sha256((ROOT / "tinyinfer_amd" / "csrc" / "gemm.hip").read_bytes()).hexdigest()
+    if fields.get("kernel") != kernel or "traffic_bytes_per_launch" not in fields:
+        return None, f"{path.relative_to(ROOT)} names {fields.get('kernel')!r}, not the timed {kernel!r}"
+    if fields.get("source_sha256") != source:
+        return None, f"{path.relative_to(ROOT)} was measured on another gemm.hip (stale)"
     return int(fields["traffic_bytes_per_launch"]), \
-        f"{path.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, commit {fields.get('commit', '?')})"
+        f"{path.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, commit {fields.get('commit', '?')}, " \
+        f"gemm.hip sha256 {source[:12]})"
 
 
 # ---------------------------------------------------------------- decode
@@ -882,11 +889,12 @@ def main():
         line["gemv"] = gemv
         line["gemv_row_major_abi"] = run_gemm(rp, sweep)
         dom = gemv["M1_K3072_N768"]
-        kernel = "gemv_part_kernel<W=8,LPW=3,QC=8>"
+        kernel = "gemv_part_kernel<8, 3, 8>"  # <W waves, LPW record pairs per wave, QC columns per workgroup>
         traffic, source = pmc_traffic(kernel)
         ceiling = line.get("limits", {}).get("stream_2.25MiB_best")
         line["roofline"] = {"bound": "hbm",
-                            "kernel": f"{kernel} (panel-packed int8, 8 columns per workgroup), M=1 K=3072 N=768, "
+                            "kernel": f"{kernel} (W=8 waves, 3 record pairs each, 8 columns per workgroup; "
+                                      "panel-packed int8), M=1 K=3072 N=768, "
                                       "fused bias+GELU; the standalone configs[1] GEMV: the runtime's decode runs "
                                       "the MFMA GEMV family instead, whose sums do not depend on the batch size",
                             "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

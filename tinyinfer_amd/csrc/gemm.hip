@@ -2045,7 +2045,10 @@ hipError_t launch_panel_cfg(const GemmArgs& g, const Scratch* s, hipStream_t str
   int splits = 1;
   const bool pool = s && s->queue_pool && !deferred && tiles <= kPoolTiles;
   const size_t capacity = pool ? kPoolFloats : (s && s->partials) ? s->partial_floats : 0;
-  if (may_split && capacity > 0 && tiles < 192) {
+  // Split K below ~one tile per CU; a pool plan also below two per CU (M =
+  // 512, 3072 -> 768 as 32 x 64 tiles in two K halves: 18.6 -> 14.5 us, the
+  // finisher re-reading 16 KB per tile).
+  if (may_split && capacity > 0 && tiles < (pool ? 384 : 192)) {
     splits = int(std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, p.kc / (S - 1))));
     while (splits > 1 && size_t(splits) * g.m * g.n > capacity) --splits;
     if (pool) splits = pool_splits(splits, tiles, BM * BN, kTileRounds * pool_max_splits(BM / (256 / (BN / 4))), p.kc);

@@ -1114,11 +1114,18 @@ struct ti_llm_model {
   // feeds its own ids forward) and the host waits once, at the end.  More
   // than kLaneRows requests split evenly over ceil(b / kLaneRows) lanes,
   // queued side by side.  tokens[t * b + i] is request i's token after step t.
-  void decode_run(const int32_t* s, const int32_t* ids, int b, int steps, int32_t* tokens) {
+  // Returns the steps that count: `steps`, or, when some step t produced an
+  // id outside the vocabulary (non-finite logits), t + 1 -- the reference's
+  // greedy loop runs the forwards of steps 0..t and then rejects that id as
+  // the next forward's input (reference runtime.cu:160, :197-199), so only
+  // those steps advance the lengths and the caller reports it as invalid.
+  int decode_run(const int32_t* s, const int32_t* ids, int b, int steps, int32_t* tokens) {
     check();
     if (b < 1 || b > opt.max_batch || steps < 1) throw Invalid("invalid decode run");
-    for (int i = 0; i < b; ++i)
+    for (int i = 0; i < b; ++i) {
       if (lengths[s[i]] + steps > opt.capacity) throw Invalid("decode run exceeds the cache capacity");
+      if (ids[i] < 0 || ids[i] >= V) throw Invalid("token ID outside the model vocabulary");
+    }
     const int parts = lane_count > 1 && b > kLaneRows && ln_fused(kLaneRows, 1) ? (b + kLaneRows - 1) / kLaneRows : 1;
     int first[kLanes] = {}, count[kLanes] = {};
     for (int l = 0; l < parts; ++l) {
@@ -1157,17 +1164,19 @@ struct ti_llm_model {
     }
     select_lane(0);
     for (int l = 0; l < parts; ++l) ck(hipStreamSynchronize(lanes[l].stream));
+    int valid = steps;
     for (int l = 0; l < parts; ++l)
       for (int j = 0; j < count[l]; ++j) {
         const int i = first[l] + j, base = lengths[s[i]] - lo[l];
         for (int t = 0; t < steps; ++t) {
           const int32_t id = lanes[l].h_run[size_t(base + t) * count[l] + j];
-          if (id < 0 || id >= V) throw GpuError("greedy id outside the vocabulary (non-finite logits)");
           tokens[size_t(t) * b + i] = id;
+          if ((id < 0 || id >= V) && t + 1 < valid) valid = t + 1;
         }
       }
-    for (int t = 0; t < steps; ++t) count_forward(true, true);
-    for (int i = 0; i < b; ++i) lengths[s[i]] += steps;
+    for (int t = 0; t < valid; ++t) count_forward(true, true);
+    for (int i = 0; i < b; ++i) lengths[s[i]] += valid;
+    return valid;
   }
 
   // reference runtime.cu:204-211
@@ -1381,15 +1390,18 @@ extern "C" int ti_llm_greedy_batch(ti_llm_model* m, const int32_t* slots, const 
       if (active.empty()) break;
       const int n = int(active.size());
       std::vector<int32_t> generated(size_t(steps) * n);
-      m->decode_run(active.data(), ids.data(), n, steps, generated.data());
+      const int valid = m->decode_run(active.data(), ids.data(), n, steps, generated.data());
       const double elapsed = ms_since(start);
       for (int j = 0; j < n; ++j) {
         const int i = owner[j];
-        for (int t = 0; t < steps; ++t) output[int64_t(i) * out_stride + done[i] + t] = generated[size_t(t) * n + j];
-        done[i] += steps;
-        next[i] = generated[size_t(steps - 1) * n + j];
+        for (int t = 0; t < valid; ++t) output[int64_t(i) * out_stride + done[i] + t] = generated[size_t(t) * n + j];
+        done[i] += valid;
+        next[i] = generated[size_t(valid - 1) * n + j];
         if (total && done[i] == requested[i]) total[i] = elapsed;
       }
+      // An id outside the vocabulary ends the call as the reference's next
+      // forward would: invalid, output so far kept, the model still usable.
+      if (valid < steps) throw Invalid("token ID outside the model vocabulary");
     }
     if (output_lengths)
       for (int i = 0; i < batch; ++i) output_lengths[i] = done[i];
