@@ -31,16 +31,18 @@ int ti_amd_legacy_gemm_f32_variant(int variant, const float* a, const float* b, 
 /* ti_amd_gemm_ex_i8_noalloc: no counterpart in the reference.  For callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): ti_v2_gemm_ex_i8 with the same
- * arguments, validation, status codes and result bits, but its split-K fp32
- * partials live in a fixed 8 MiB device array of the library (one per GPU,
- * held until the process ends) instead of the per-(device, stream) scratch
- * ti_v2_gemm_ex_i8 allocates on a stream's first call.  It calls no hipMalloc,
- * hipFree or allocating library routine.  A shape whose split plan needs more
- * than 8 MiB returns TI_V2_INVALID_ARGUMENT with the byte counts in
- * ti_v2_last_error() (no shape under the current plans does: the largest
- * needs at most 8 380 416 bytes).  Every call on one GPU shares that array: calls
- * that overlap in time on one GPU (different streams, or threads) race;
- * calls ordered on one stream do not. */
+ * arguments, validation, status codes and result bits.  It calls no hipMalloc,
+ * hipFree or allocating library routine, and neither does ti_v2_gemm_ex_i8
+ * any more: split-K work is finished by the last workgroup of the same launch,
+ * with its fp32 partials in static device arrays of the library, one 4 MiB
+ * slot per hardware queue (32 slots per GPU, held until the process ends).
+ * Limit: a plan is only split when its partials fit the slot (1 Mi floats,
+ * 1024 output tiles); larger shapes run unsplit, so no shape is refused.
+ * Dispatches on one hardware queue never overlap, so calls on one stream, or
+ * on streams that share a queue, do not race, and calls that overlap on
+ * different queues use different slots; only with more than 32 hardware
+ * queues in use on one GPU can two queues share a slot and overlapping calls
+ * on them race. */
 int ti_amd_gemm_ex_i8_noalloc(const uint16_t* a, const int8_t* b, const float* scales,
                               const uint16_t* bias, void* y, float* workspace, int m, int n, int k,
                               int dtype, int config, uintptr_t stream, int device);

@@ -44,7 +44,13 @@ int ti_llm_forward_batch(ti_llm_model*, const int32_t* slots, const int32_t* tok
                          const int32_t* lengths, int32_t batch, int32_t token_stride,
                          float* last_logits, int32_t* next_tokens);
 /* Greedy decode from empty distinct slots; every request generates exactly
- * max_new_tokens[b] tokens; the last generated token is not appended. */
+ * max_new_tokens[b] tokens; the last generated token is not appended.  A
+ * prompt id outside the vocabulary returns TI_LLM_INVALID before any work.  A
+ * generated id outside it (INT_MAX, the argmax of a row whose logits are all
+ * NaN, as in reference llm/src/runtime.cu:59-66) ends the call with
+ * TI_LLM_INVALID after writing the tokens up to and including that step, with
+ * the slot lengths advanced by the forwards that ran; the context stays usable
+ * (the reference's next forward rejects the id, llm/src/runtime.cu:160). */
 int ti_llm_greedy_batch(ti_llm_model*, const int32_t* slots, const int32_t* prompts,
                         const int32_t* prompt_lengths, const int32_t* max_new_tokens,
                         int32_t batch, int32_t prompt_stride, int32_t* output,
