@@ -67,10 +67,18 @@ def parse():
                    help="run one part only (for profiler passes; 'roofline' = the dominant GEMV shape only, "
                         "'copy' = a 512 MiB device copy used to calibrate the HBM byte counters, "
                         "'prefill' = the XL-shaped fp16-record prefill GEMM and the prefill attention cases only, "
-                        "'xl' = configs[4] GPT-2 XL, not part of 'all': its synthetic artifact takes ~2 min "
-                        "to write; 'cpu' = host-core baselines of configs[1..3], no GPU); the driver's JSON "
+                        "'xl' = configs[4] GPT-2 XL only (also in 'all', with steps // 5 timed runs; its synthetic "
+                        "artifact takes ~4 s to write on 16 cores); 'cpu' = host-core baselines of configs[1..3], no GPU); the driver's JSON "
                         "line needs 'all'")
     return p.parse_args()
+
+
+_T0 = time.perf_counter()
+
+
+def note(msg):
+    """A progress line on stderr (the JSON line stays alone on stdout)."""
+    print(f"[bench {time.perf_counter() - _T0:6.1f} s] {msg}", file=sys.stderr, flush=True)
 
 
 def gemv_bytes(m, k, n):
@@ -424,12 +432,14 @@ def xl_greedy_parity(new):
     with NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=32, capacity=640) as m0, \
             NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=32, capacity=640) as m1:
         _, gpu, _ = xl_concurrent((m0, m1), prompts, new)
+    note("xl greedy parity: GPU tokens done")
     man, tensors = load_tensors(m)
     t0 = time.perf_counter()
     cpu = oracle.Gpt2(tensors, man["architecture"], slots=65, capacity=640 + 1)
     halves = (list(range(32)), list(range(32, 64)))
     ref = [[] for _ in range(64)]
-    for sl in halves:
+    for h, sl in enumerate(halves):
+        note(f"xl greedy parity: oracle, half {h + 1} of 2 ({new} tokens)")
         _, nxt = cpu.forward(sl, [prompts[i] for i in sl], logits=False)
         for i, t in zip(sl, nxt):
             ref[i].append(int(t))
@@ -482,6 +492,7 @@ def run_xl(steps, parity=True):
                 runs.append({"decode_tokens_per_s": 64 * (new - 1) / window, "ttft_ms": ttft,
                              "wall_s": time.perf_counter() - t_run})
         concurrent_tokens = tokens
+    note("xl: sequential plan")
     with NativeModel(require(LLM_LIB), m, max_batch=32, cache_slots=64, capacity=640) as model:
         for rep in range(2):  # warmup, then one timed run
             decode_s, seq_tokens, seq_ttft = xl_sequential(model, prompts, new)
@@ -500,6 +511,7 @@ def run_xl(steps, parity=True):
                           "plan": "the two batches of 32 one after the other in one context, KV slots 0..63"},
            "tokens_identical_across_plans": concurrent_tokens == seq_tokens}
     if parity:
+        note("xl: greedy parity on the 2-layer XL-shaped artifact")
         out["greedy_parity"] = xl_greedy_parity(new)
     return out
 
@@ -758,7 +770,9 @@ def cpu_baseline_and_parity(manifest, gpu_b1, gpu_b32):
     from tinyinfer_amd.artifact import load_tensors
     man, tensors = load_tensors(manifest)
     cpu = oracle.Gpt2(tensors, man["architecture"], slots=33, capacity=PROMPT + NEW + 1)
+    note("cpu baseline: oracle GPT-2 small, batch 32")
     tok32, steps32, dt32 = _oracle_decode(cpu, 32)
+    note("cpu baseline: oracle GPT-2 small, batch 1")
     tok1, steps1, dt1 = _oracle_decode(cpu, 1)
     parity = {}
     if gpu_b32 is not None:
@@ -826,6 +840,7 @@ def main():
     line = {}
     gpu_tokens = {}
     if args.part in ("all", "decode"):
+        note("decode: GPT-2 small artifact")
         manifest = artifact_path()
         with NativeModel(require(LLM_LIB), manifest, max_batch=32, cache_slots=32,
                          capacity=PROMPT + NEW) as model:
@@ -835,6 +850,7 @@ def main():
         # The configs[0] prompt length is ambiguous (32 ids literally; the
         # reference's evaluation uses 128, llm/configs/evaluation.json:7): the
         # 128-id prompts are reported beside the headline.
+        note("decode: 128-id prompts")
         with NativeModel(require(LLM_LIB), manifest, max_batch=32, cache_slots=32,
                          capacity=128 + NEW) as model:
             b1_128 = run_decode(model, 1, max(2, args.steps // 2), 1, 128)
@@ -875,6 +891,7 @@ def main():
         print(json.dumps({"roofline_gemv": run_gemm(rp, ((1, 3072, 768),), packed=True)}))
         return
     if args.part in ("all", "kernels"):
+        note("kernels: prefill GEMMs, row ops, attention")
         prefill = ((64, 768, 3072), (64, 3072, 768), (512, 768, 3072), (512, 3072, 768))
         prefill_xl = prefill + ((8192, 1600, 6400),)  # a GPT-2 XL c_fc prefill of 32 x 256 tokens
         line["kernels"] = {"gemm_prefill": run_gemm(rp, prefill_xl, packed=True),
@@ -882,8 +899,10 @@ def main():
                            "gemm_prefill_row_major_abi": run_gemm(rp, prefill),
                            "rowops_f32": run_rowops(rp), "decode_attention": run_decode_attention(rp),
                            "prefill_attention": run_prefill_attention(rp)}
+        note("limits: launch floor and streaming reads")
         line["limits"] = run_limits(rp)
     if args.part in ("all", "gemv"):
+        note("gemv: configs[1] sweep and LM head")
         sweep = ((1, 3072, 768), (1, 768, 3072), (8, 3072, 768), (8, 768, 3072))
         gemv = run_gemm(rp, sweep + ((1, 768, 50257), (32, 768, 50257)), packed=True)
         line["gemv"] = gemv
@@ -903,11 +922,14 @@ def main():
                             "single_launch_read_ceiling_GBps": ceiling["GBps"] if ceiling else None,
                             "frac_of_single_launch_ceiling": dom["GBps"] / ceiling["GBps"] if ceiling else None}
     if args.part == "all":
+        note("xl: configs[4]")
         line["xl"] = run_xl(max(1, args.steps // 5))
     if args.part == "all" and not args.skip_cpu:
         base, parity = cpu_baseline_and_parity(artifact_path(), gpu_tokens.get("b1"), gpu_tokens.get("b32"))
         line["greedy_parity"] = parity
+        note("cpu baseline: configs[1..3] kernels")
         base["kernels"] = cpu_baseline_kernels()
+        note("cpu baseline: GPT-2 XL layers")
         base["xl"] = cpu_baseline_xl(xl_artifact_path())
         line["cpu_baseline"] = base
     print(json.dumps(line), flush=True)
