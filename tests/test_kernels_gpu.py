@@ -209,10 +209,12 @@ def test_pack_w8_layout_bit_exact(ops, k, n):
 
 @pytest.mark.parametrize("m", [1, 8, 17, 32])
 @pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768), (768, 2304), (128, 100), (64, 50257), (768, 50257),
-                                 (1024, 16400), (1600, 6400)])
+                                 (1024, 16400), (1600, 6400), (1600, 1600), (2048, 1000), (6400, 1600)])
 def test_packed_gemv_against_oracle(ops, m, k, n):
     """Decode GEMV over panel-packed weights: bias, bias+GELU and in-place residual
-    epilogues against the oracle's fp32-accumulate linear."""
+    epilogues against the oracle's fp32-accumulate linear.  Through the C ABI,
+    fewer than 128 column blocks over a long K (3072 -> 768 at M > 8, 6400 ->
+    1600) split K and finish in the launch."""
     t = torch()
     rng = np.random.default_rng(7 * m + k + n)
     a = f16(rng.standard_normal((m, k)))
@@ -300,10 +302,14 @@ def test_packed_gemv_column_block_groups(ops, m, k, n):
 
 @pytest.mark.parametrize("m,k,n", [(33, 768, 3072), (64, 3072, 768), (130, 128, 100), (512, 64, 2000),
                                    (512, 768, 3072), (512, 3072, 768), (2048, 768, 2304), (4100, 1600, 6400),
-                                   (2050, 64, 8200)])
+                                   (2050, 64, 8200), (48, 1600, 6400), (64, 6400, 1600), (40, 64, 8200),
+                                   (64, 768, 3072), (57, 768, 50257)])
 def test_packed_prefill_gemm_against_oracle(ops, m, k, n):
     """Prefill (M > 32) GEMM over panel-packed weights: ragged row and column tiles,
-    bias and bias+GELU epilogues against the oracle; fp32-accumulate tolerance."""
+    bias and bias+GELU epilogues against the oracle; fp32-accumulate tolerance.
+    33..64 rows over at most 192 column blocks and K <= 3072 run the four-tile
+    packed GEMV (K split and finished in the launch where the grid is short of
+    column blocks); the in-place residual epilogue at M <= 64."""
     t = torch()
     rng = np.random.default_rng(11 * m + k + n)
     a = f16(rng.standard_normal((m, k)))
@@ -318,6 +324,12 @@ def test_packed_prefill_gemm_against_oracle(ops, m, k, n):
     close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, bias_bits=bias)))
     _packed(ops.lib, ad, packed, sd, None, y, None, m, n, k, 1)
     close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, gelu=True)))
+    if m <= 64:
+        ref = oracle.linear(a, q=q, scales=s, bias_bits=bias)
+        res = dev(f16(rng.standard_normal((m, n))), t.float16)
+        expect = (h(hbits(res)) + h(ref)).astype(np.float16).astype(np.float64)
+        _packed(ops.lib, ad, packed, sd, bd, res, res, m, n, k, 2)
+        close(h(hbits(res)), expect)
 
 
 def _pack16_gpu(lib, q_dev, s_dev, k, n):

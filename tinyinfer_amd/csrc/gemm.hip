@@ -69,6 +69,8 @@ constexpr int pool_max_splits(int per_thread) { return kPoolLoads / per_thread; 
 // Rounds of loads the tile finisher takes at most (its tile is read by one
 // workgroup, so more splits mostly add bytes for one CU to fetch).
 constexpr int kTileRounds = 2;
+// Most K splits of a pool GEMV (M <= 32) launch.
+constexpr int kPoolGemvSplits = 8;
 // A pool split plan over `tiles` tiles of `tile_floats` floats: at most
 // `max_splits` splits, the tile-contiguous partials within the slot, and
 // rounded to whole ranges of `units` (K steps or chunks).
@@ -551,7 +553,10 @@ __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scal
 // fragments before the MFMAs; the launch then covers K in one round of one
 // split (W * CPW >= kc).  PA: A is P32 fragment-packed (each A fragment one
 // contiguous KiB).
-template <int MT, int W, int CPW, int CBG, bool LNA = false, bool PA = false, bool CW = false>
+// POOL (the C ABIs): a split launch finishes in the kernel -- every
+// workgroup stores its reduced sums to the queue pool and the last of a column
+// group's splits to arrive adds them in split order and runs the epilogue.
+template <int MT, int W, int CPW, int CBG, bool LNA = false, bool PA = false, bool CW = false, bool POOL = false>
 __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   __shared__ float red[W][CBG][MT * 256];
   __shared__ float stat[LNA ? W : 1][MT * 16];  // per-wave LayerNorm partial sums
@@ -570,7 +575,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   const int cb0 = grp * CBG;
   const int c_begin = split * p.chunks_per_split;
   const int c_end = min(p.kc, c_begin + p.chunks_per_split);
-  const bool epi_now = p.splits == 1 && !p.defer;
+  const bool epi_now = (POOL || p.splits == 1) && !p.defer;
   const bool has_bias = epi_now && p.epi.kind != EPI_RAW_F32 && p.epi.bias;
 
   const u32x4_t* wb[CBG];
@@ -787,6 +792,50 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   // the main loop).
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
+  if constexpr (POOL) {
+    if (p.splits > 1) {
+      // Split s of column group grp at ((grp * splits + s) * kTileOut + o), o
+      // the output index of the epilogue loop; the finisher loads every
+      // split of its outputs in one round.
+      constexpr int kTileOut = CBG * MT * 256, SMAX = kPoolLoads / kOutIters;
+      const PoolSlot slot = gemm_pool_slot();
+      const float* tile_parts = slot.parts + int64_t(grp) * p.splits * kTileOut;
+#pragma unroll
+      for (int it = 0; it < kOutIters; ++it) {
+        const int o = tid + it * W * 64, r = o / per_block, rem = o - r * per_block;
+        if (o >= CBG * per_block) continue;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) v += red[w][r][rem];
+        st_agent(const_cast<float*>(tile_parts) + int64_t(split) * kTileOut + o, v);
+      }
+      if (!wg_arrive_last(slot.ctr + grp * kCounterStride, p.splits)) return;
+      float part[kOutIters][SMAX];
+#pragma unroll
+      for (int it = 0; it < kOutIters; ++it) {
+        const int o = tid + it * W * 64;
+#pragma unroll
+        for (int u = 0; u < SMAX; ++u)
+          part[it][u] = (u < p.splits && o < CBG * per_block) ? ld_agent(tile_parts + int64_t(u) * kTileOut + o) : 0.f;
+      }
+      depart(slot.ctr + grp * kCounterStride);
+#pragma unroll
+      for (int it = 0; it < kOutIters; ++it) {
+        const int o = tid + it * W * 64, r = o / per_block, rem = o - r * per_block;
+        const int row = rem >> 4, n = (cb0 + r) * 16 + (rem & 15);
+        if (o >= CBG * per_block || cb0 + r >= p.nb || n >= p.n) continue;
+        float v = part[it][0];
+#pragma unroll
+        for (int u = 1; u < SMAX; ++u)
+          if (u < p.splits) v += part[it][u];
+        uint16_t braw = bias_raw[0];
+#pragma unroll
+        for (int q = 1; q < CBG; ++q) braw = r == q ? bias_raw[q] : braw;
+        apply_epilogue(p.epi, row, n, v, has_bias ? h2f(braw) : 0.f, has_res ? h2f(res_raw[it]) : 0.f);
+      }
+      return;
+    }
+  }
   float amax_val = -__builtin_huge_valf();  // MT = 1: this thread's (single) output
   int amax_col = INT_MAX;
 #pragma unroll
@@ -1840,11 +1889,11 @@ GemvShape gemv_shape(int mt, int chunks, bool one_round, int nb) {
   return s;
 }
 
-template <int MT, bool LNA, bool PA, bool CW = false>
+template <int MT, bool LNA, bool PA, bool CW = false, bool POOL = false>
 hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipStream_t st) {
 #define TIA_GEMV(W_, C_, B_)                                                                            \
   if (sh.w == W_ && sh.cpw == C_ && sh.cbg == B_) {                                                     \
-    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA, PA, CW>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
+    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA, PA, CW, POOL>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
     return hipGetLastError();                                                                           \
   }
   TIA_GEMV(4, 3, 1)
@@ -1975,11 +2024,22 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
     return hipGetLastError();
   }
   int splits = 1;
+  // A C-ABI call over few column blocks and a long K splits K and finishes in
+  // the launch (queue pool): >= 12 chunks per split, ~192 workgroups.  The
+  // finish costs about a microsecond, so only where the unsplit launch is long
+  // (timed, unsplit -> split: 3072 -> 768 at M = 16 6.05 -> 5.27 us, M = 32
+  // 8.54 -> 6.41, 6400 -> 1600 at M = 8 8.81 -> 7.77; but M = 8 3072 -> 768
+  // 5.09 -> 5.11, 1600 -> 1600 4.42 -> 5.26, 2048 -> 1000 4.41 -> 5.21, and
+  // M = 32 1600 -> 1600 6.62 -> 6.71).
+  const bool pool = s && s->queue_pool && !deferred && !ln && !g.a_p32 &&
+                    ((g.m > 8 && p.kc >= 48) || p.kc >= 64);
   if (deferred && !ln && s && s->partials) {
     const int groups = p.nb;
     const int target = std::max(1, g.defer_workgroups);
     splits = std::max(1, std::min((target + groups - 1) / groups, p.kc / 4));
     while (splits > 1 && size_t(splits) * g.m * g.n > s->partial_floats) --splits;
+  } else if (pool && p.nb < 128 && p.kc >= 24) {
+    splits = std::max(1, std::min({kPoolGemvSplits, (192 + p.nb - 1) / p.nb, p.kc / 12}));
   }
   p.chunks_per_split = (p.kc + splits - 1) / splits;
   splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
@@ -1995,6 +2055,14 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
     p.amax_v = g.amax_v;
     p.amax_i = g.amax_i;
     *g.amax_groups = grid;
+  }
+  if (pool && splits > 1) {
+    // The finisher holds every split of its outputs in registers.
+    const int out_iters = (sh.cbg * MT * 256 + sh.w * 64 - 1) / (sh.w * 64);
+    if (splits > kPoolLoads / out_iters || int64_t(grid / splits) > kPoolTiles ||
+        int64_t(grid) * sh.cbg * MT * 256 > int64_t(kPoolFloats))
+      return hipErrorInvalidValue;
+    return launch_gemv_shape<MT, false, false, false, true>(p, sh, grid, stream);
   }
   if (g.a_p32) {
     if constexpr (MT == 1) {
@@ -2012,6 +2080,55 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
   }
   return ln ? launch_gemv_shape<MT, true, false>(p, sh, grid, stream)
             : launch_gemv_shape<MT, false, false>(p, sh, grid, stream);
+}
+
+// 33..64 rows through the C ABI (queue pool) over at most 192 column blocks
+// and K <= 3072: the packed GEMV with four 16-row MFMA tiles (MT = 4), K split
+// to ~192 workgroups of at most 24 chunks and finished in the launch.  The
+// weights stream once and A (at most 64 rows) is re-read from L2 by every
+// column block, against the panel GEMM's 64 x 64 tiles, which at these M run
+// few tiles over a long K (timed, panel -> GEMV: M = 64 768 -> 3072 8.85 ->
+// 7.23 us, 3072 -> 768 10.1 -> 9.04, M = 33 768 -> 3072 8.72 -> 5.79; wider
+// or longer shapes lose, their A re-reads growing with N or K: M = 48
+// 1600 -> 6400 11.4 -> 21.3, M = 64 6400 -> 1600 12.9 -> 18.8).  W <= 8
+// waves: four A tiles per chunk hold 140-235 registers.
+template <bool POOL>
+hipError_t launch_gemv4_shape(const PackedParams& p, GemvShape sh, int grid, hipStream_t st) {
+#define TIA_GEMV4(W_, C_)                                                                               \
+  if (sh.w == W_ && sh.cpw == C_ && sh.cbg == 1) {                                                      \
+    hipLaunchKernelGGL((gemv_packed_kernel<4, W_, C_, 1, false, false, false, POOL>), dim3(unsigned(grid)), \
+                       dim3(W_ * 64), 0, st, p);                                                         \
+    return hipGetLastError();                                                                           \
+  }
+  TIA_GEMV4(4, 3)
+  TIA_GEMV4(4, 4)
+  TIA_GEMV4(8, 3)
+  TIA_GEMV4(8, 4)
+#undef TIA_GEMV4
+  return hipErrorInvalidValue;
+}
+
+// Returns hipErrorNotSupported (nothing launched) for a plan it does not take.
+hipError_t launch_packed4(const GemmArgs& g, hipStream_t stream) {
+  PackedParams p{};
+  p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
+  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.nb = (g.n + 15) / 16;
+  p.kc = g.k / 64;
+  int splits = std::max((p.kc + 23) / 24, std::min((192 + p.nb - 1) / p.nb, p.kc / 12));
+  splits = std::max(1, std::min(splits, kPoolGemvSplits));
+  p.chunks_per_split = (p.kc + splits - 1) / splits;
+  splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
+  p.splits = splits;
+  const GemvShape sh = gemv_shape(4, p.chunks_per_split, false, p.nb);
+  const int out_iters = (4 * 256 + sh.w * 64 - 1) / (sh.w * 64);
+  if (sh.w > 8 || sh.cbg != 1 || splits > kPoolLoads / out_iters || (splits > 1 && p.nb > kPoolTiles) ||
+      int64_t(p.nb) * splits * 4 * 256 > int64_t(kPoolFloats))
+    return hipErrorNotSupported;
+  const int64_t grid = int64_t(p.nb) * splits;
+  if (grid > (int64_t(1) << 30)) return hipErrorNotSupported;
+  return splits > 1 ? launch_gemv4_shape<true>(p, sh, int(grid), stream)
+                    : launch_gemv4_shape<false>(p, sh, int(grid), stream);
 }
 
 // 64x64 tiles, S = 4 stages of 12 KiB (48 KiB of LDS: three workgroups per CU,
@@ -2464,6 +2581,10 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
     if (part_gemv_preferred(g)) return launch_part(g, s, stream, deferred);
     if (g.m <= 16) return launch_packed<1>(g, s, stream, deferred);
     if (g.m <= 32) return launch_packed<2>(g, s, stream, deferred);
+    if (g.m <= 64 && s && s->queue_pool && !deferred && (g.n + 15) / 16 <= 192 && g.k <= 3072) {
+      const hipError_t e = launch_packed4(g, stream);
+      if (e != hipErrorNotSupported) return e;
+    }
     return launch_panel(g, s, stream, deferred);
   }
   if (g.m <= 16) return g.w_int8 ? launch_skinny<true, 1>(g, wvec, avec, s, stream, deferred)
