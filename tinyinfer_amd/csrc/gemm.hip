@@ -2478,9 +2478,10 @@ hipError_t launch_f16(const GemmArgs& g, const Scratch* s, hipStream_t stream, i
 
 // Row-major W (the reference ABI's [K, N]).  Each K step of a workgroup waits
 // for one global round trip, so a grid of few tiles (M = 64, 3072 -> 768: 12
-// tiles x 96 steps, 138 us) splits K over the library scratch until >= 256
-// workgroups run (at least 4 steps each), then splitk_epilogue_kernel sums the
-// splits in a fixed order and applies the epilogue.  Canonical (batch-invariant)
+// tiles x 96 steps, 138 us) splits K until >= 256 workgroups run (at least 4
+// steps each); the splits are summed in a fixed order and the epilogue applied
+// by the last workgroup of each tile (queue pool, capped split count) or by
+// splitk_epilogue_kernel over caller scratch.  Canonical (batch-invariant)
 // calls stay unsplit: their K order must not depend on M.
 // Split count of the row-major M > 32 kernel (0 capacity or a canonical call:
 // one split), after rounding to whole step ranges.
