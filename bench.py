@@ -824,6 +824,53 @@ def cpu_baseline_xl(manifest, steps=3, short=2, long=6):
                       f"48-layer step = {full * 1e3:.0f} ms by the per-layer difference"}
 
 
+def summary(line):
+    """The headline figures in one compact object, printed as the line's last key
+    (a reader that keeps only the end of the output still sees them): decode
+    tokens/s, greedy parity, every kernel row's microseconds and roofline
+    fraction, GPT-2 XL, the machine-limit reads and the host baseline."""
+    r3 = lambda x: None if x is None else float(f"{x:.4g}")
+    out = {}
+    if "decode_b32" in line:
+        out["decode_tok_s"] = {k: r3(line[f"decode_{k}"]["tokens_per_s"])
+                               for k in ("b32", "b1", "b32_prompt128", "b1_prompt128") if f"decode_{k}" in line}
+    if "greedy_parity" in line:
+        out["greedy_parity"] = {k: f"{v['identical_requests']}/{v['batch']} identical, max gap {r3(v['max_oracle_gap'])}"
+                                for k, v in line["greedy_parity"].items()}
+
+    def rows(d, frac):
+        return {k: [r3(v["us_per_launch"]), r3(v[frac])] for k, v in d.items() if "us_per_launch" in v}
+    if "gemv" in line:
+        out["gemv_us_hbmfrac"] = rows(line["gemv"], "hbm_frac")
+        out["gemv_row_major_abi_us_hbmfrac"] = rows(line["gemv_row_major_abi"], "hbm_frac")
+    k = line.get("kernels")
+    if k:
+        out["prefill_gemm_us_mfmafrac"] = rows(k["gemm_prefill"], "mfma_frac")
+        out["prefill_gemm_row_major_abi_us_mfmafrac"] = rows(k["gemm_prefill_row_major_abi"], "mfma_frac")
+        out["rowops_f32_us_hbmfrac"] = rows(k["rowops_f32"], "hbm_frac")
+        da = k["decode_attention"]
+        out["decode_attention_us_hbmfrac"] = [r3(da["us_per_launch"]), r3(da["hbm_frac"])]
+        out["prefill_attention_us_mfmafrac_hbmfrac"] = {
+            n: [r3(v["us_per_launch"]), r3(v["mfma_frac"]), r3(v["hbm_frac"])] for n, v in k["prefill_attention"].items()}
+    lim = line.get("limits")
+    if lim:
+        out["limits_us"] = {"empty_kernel": r3(lim["empty_kernel_us_per_launch"]),
+                            **{f"read_{n}": r3(lim[f"stream_{n}_best"]["us_per_launch"])
+                               for n in ("2.25MiB", "38.6MB", "50.9MB")}}
+    x = line.get("xl")
+    if x:
+        gp = x.get("greedy_parity", {})
+        out["xl"] = {"decode_tok_s": r3(x["decode_tokens_per_s"]),
+                     "sequential_tok_s": r3(x["sequential"]["decode_tokens_per_s"]),
+                     "same_tokens": x["tokens_identical_across_plans"],
+                     "parity_2layer": f"{gp.get('identical_requests')}/64 identical over 128, max gap "
+                                      f"{r3(gp.get('max_oracle_gap'))}"}
+    cb = line.get("cpu_baseline")
+    if cb:
+        out["cpu_tok_s"] = {"b32": r3(cb["value"]), "b1": r3(cb["decode_b1"]["value"]), "cores": cb["cores"]}
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -932,6 +979,8 @@ def main():
         note("cpu baseline: GPT-2 XL layers")
         base["xl"] = cpu_baseline_xl(xl_artifact_path())
         line["cpu_baseline"] = base
+    if args.part == "all":
+        line["summary"] = summary(line)
     print(json.dumps(line), flush=True)
 
 
