@@ -612,13 +612,31 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   const int rows = min(p.m, MT * 16), per_block = rows * 16;
   const bool has_res = epi_now && p.epi.kind == EPI_RESIDUAL;
   const uint16_t* rsrc = has_res ? p.epi.residual : p.a;
+  // Output o of the epilogue: block r = o / per_block, element rem (with one
+  // block, o itself: no division).
+  auto block_of = [&](int o, int& r, int& rem) {
+    if constexpr (CBG == 1) {
+      r = 0;
+      rem = o;
+    } else {
+      r = o / per_block;
+      rem = o - r * per_block;
+    }
+  };
   uint16_t res_raw[kOutIters];
 #pragma unroll
   for (int it = 0; it < kOutIters; ++it) {
-    const int o = threadIdx.x + it * W * 64, r = o / per_block, rem = o - r * per_block;
-    const int n = (cb0 + r) * 16 + (rem & 15);
-    const bool ok = has_res && o < CBG * per_block && cb0 + r < p.nb && n < p.n;
-    res_raw[it] = ldg_u16(rsrc + (ok ? r_off(p.epi, rem >> 4, n) : 0));
+    // The offset arithmetic only under a residual epilogue (a uniform branch);
+    // the load itself stays unconditional.
+    int64_t roff = 0;
+    if (has_res) {
+      const int o = threadIdx.x + it * W * 64;
+      int r, rem;
+      block_of(o, r, rem);
+      const int n = (cb0 + r) * 16 + (rem & 15);
+      if (o < CBG * per_block && cb0 + r < p.nb && n < p.n) roff = r_off(p.epi, rem >> 4, n);
+    }
+    res_raw[it] = ldg_u16(rsrc + roff);
   }
 
   float4_t acc[MT][CBG];
@@ -802,7 +820,9 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
       const float* tile_parts = slot.parts + int64_t(grp) * p.splits * kTileOut;
 #pragma unroll
       for (int it = 0; it < kOutIters; ++it) {
-        const int o = tid + it * W * 64, r = o / per_block, rem = o - r * per_block;
+        const int o = tid + it * W * 64;
+        int r, rem;
+        block_of(o, r, rem);
         if (o >= CBG * per_block) continue;
         float v = 0.f;
 #pragma unroll
@@ -821,7 +841,9 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
       depart(slot.ctr + grp * kCounterStride);
 #pragma unroll
       for (int it = 0; it < kOutIters; ++it) {
-        const int o = tid + it * W * 64, r = o / per_block, rem = o - r * per_block;
+        const int o = tid + it * W * 64;
+        int r, rem;
+        block_of(o, r, rem);
         const int row = rem >> 4, n = (cb0 + r) * 16 + (rem & 15);
         if (o >= CBG * per_block || cb0 + r >= p.nb || n >= p.n) continue;
         float v = part[it][0];
@@ -840,7 +862,9 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   int amax_col = INT_MAX;
 #pragma unroll
   for (int it = 0; it < kOutIters; ++it) {
-    const int o = tid + it * W * 64, r = o / per_block, rem = o - r * per_block;
+    const int o = tid + it * W * 64;
+    int r, rem;
+    block_of(o, r, rem);
     const int row = rem >> 4, n = (cb0 + r) * 16 + (rem & 15);
     if (o >= CBG * per_block || cb0 + r >= p.nb || n >= p.n) continue;
     float s = 0.f;
