@@ -16,6 +16,7 @@
 // are dot(q,k) * D^-1/2, keys j < kv_valid (and j <= offset + qi when causal),
 // rows with no visible key (or padded queries) are exactly zero.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -237,17 +238,21 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
     x = dpp_add(x, 2);
     return dpp_add(x, 3);
   };
-  auto process = [&](const KVTile<NI>& t, int k0, const half8_t& qf, bool select_v = false) {
+  // PLAIN: every key of the tile is visible and none is the new token (the
+  // FUSEDQKV substitution), so the masks and selects below are no-ops and are
+  // left out (the same values, ~40 % fewer VALU instructions per tile).
+  auto process_t = [&](auto plain_c, const KVTile<NI>& t, int k0, const half8_t& qf, bool select_v) {
+    constexpr bool PLAIN = decltype(plain_c)::value;
     float s[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + kg + KPI * i;
       float part = 0.f;
-      const half8_t kv8 = FUSEDQKV && key >= end - 1 ? kfresh : t.k[i];
+      const half8_t kv8 = !PLAIN && FUSEDQKV && key >= end - 1 ? kfresh : t.k[i];
 #pragma unroll
       for (int e = 0; e < 8; ++e) part += float(qf[e]) * float(kv8[e]);
       part = group_sum(part);
-      s[i] = key < end ? part * p.scale : kNegInf;
+      s[i] = PLAIN || key < end ? part * p.scale : kNegInf;
     }
     float tmax = s[0];
 #pragma unroll
@@ -260,13 +265,20 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + kg + KPI * i;
-      const float pr = key < end ? __expf(s[i] - nm) : 0.f;
+      const float pr = PLAIN || key < end ? __expf(s[i] - nm) : 0.f;
       l += pr;
-      const half8_t vv8 = FUSEDQKV && key >= end - 1 ? vfresh : t.v[i];
+      const half8_t vv8 = !PLAIN && FUSEDQKV && key >= end - 1 ? vfresh : t.v[i];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += select_v && key >= end ? 0.f : pr * float(vv8[e]);
+      for (int e = 0; e < 8; ++e) acc[e] += !PLAIN && select_v && key >= end ? 0.f : pr * float(vv8[e]);
     }
     m = nm;
+  };
+  // The tile test is uniform over the wave (k0 and end are), so it is a scalar
+  // branch between the two forms.
+  auto process = [&](const KVTile<NI>& t, int k0, const half8_t& qf, bool select_v = false) {
+    const bool plain = FUSEDQKV ? k0 + TK < end : k0 + TK <= end;
+    if (__builtin_amdgcn_readfirstlane(int(plain))) process_t(std::true_type{}, t, k0, qf, false);
+    else process_t(std::false_type{}, t, k0, qf, select_v);
   };
 
   // Wave kw takes tiles kw, kw + KW, ... in pairs: both tiles' loads are issued
