@@ -112,56 +112,76 @@ __global__ void gather_last_kernel(const uint16_t* x, uint16_t* out, const int32
 // reference runtime.cu:25-30), and the first layer's LayerNorm of it into
 // norm: one wave, lane owns the 8-wide column groups lane + 64 i (hidden <=
 // 2048).  p32: x and norm are written P32 fragment-packed (rows <= 32, hidden
-// % 64 == 0).
+// % 64 == 0).  The position row and gamma/beta do not depend on the token, so
+// a caller that knows the position early fetches them first (EmbedRow::fetch)
+// and issues the token-row load alone once the id is known.
+struct EmbedRow {
+  static constexpr int NV = 4;
+  tia::half8_t p[NV], gg[NV], bb[NV];
+  __device__ __forceinline__ void fetch(int lane, bool valid, int pos, const uint16_t* wpe, const uint16_t* g,
+                                        const uint16_t* bt, int hidden) {
+    const int groups = hidden / 8;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int gi = min(lane + 64 * i, groups - 1);
+      p[i] = *reinterpret_cast<const tia::half8_t*>(wpe + int64_t(valid ? pos : 0) * hidden + 8 * gi);
+      gg[i] = *reinterpret_cast<const tia::half8_t*>(g + 8 * gi);
+      bb[i] = *reinterpret_cast<const tia::half8_t*>(bt + 8 * gi);
+    }
+  }
+  __device__ __forceinline__ void finish(int lane, bool valid, int id, const uint16_t* wte, uint16_t* x,
+                                         uint16_t* norm, int row, int hidden, bool p32) const {
+    const int groups = hidden / 8;
+    float v[NV][8];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int gi = lane + 64 * i;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[i][k] = 0.f;
+      if (gi < groups) {
+        if (valid) {
+          const tia::half8_t e = *reinterpret_cast<const tia::half8_t*>(wte + int64_t(id) * hidden + 8 * gi);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) v[i][k] = float(tia::f16r(float(e[k]) + float(p[i][k])));
+        }
+        tia::half8_t o;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          o[k] = tia::f16(v[i][k]);
+          s += v[i][k];
+        }
+        *reinterpret_cast<tia::half8_t*>(x + (p32 ? tia::p32_off(row, 8 * gi) : int64_t(row) * hidden + 8 * gi)) = o;
+      }
+    }
+    const float mean = tia::wave_sum(s) / float(hidden);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < groups) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss += (v[i][k] - mean) * (v[i][k] - mean);
+      }
+    const float inv = rsqrtf(tia::wave_sum(ss) / float(hidden) + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int gi = lane + 64 * i;
+      if (gi < groups) {
+        tia::half8_t o;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = tia::f16r((v[i][k] - mean) * inv * float(gg[i][k]) + float(bb[i][k]));
+        *reinterpret_cast<tia::half8_t*>(norm + (p32 ? tia::p32_off(row, 8 * gi) : int64_t(row) * hidden + 8 * gi)) = o;
+      }
+    }
+  }
+};
+
 __device__ __forceinline__ void embed_ln_row(int lane, bool valid, int id, int pos, const uint16_t* wte,
                                              const uint16_t* wpe, const uint16_t* g, const uint16_t* bt,
                                              uint16_t* x, uint16_t* norm, int row, int hidden, bool p32) {
-  constexpr int NV = 4;
-  const int groups = hidden / 8;
-  float v[NV][8];
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int gi = lane + 64 * i;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[i][k] = 0.f;
-    if (gi < groups) {
-      if (valid) {
-        const tia::half8_t e = *reinterpret_cast<const tia::half8_t*>(wte + int64_t(id) * hidden + 8 * gi);
-        const tia::half8_t p = *reinterpret_cast<const tia::half8_t*>(wpe + int64_t(pos) * hidden + 8 * gi);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[i][k] = float(tia::f16r(float(e[k]) + float(p[k])));
-      }
-      tia::half8_t o;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        o[k] = tia::f16(v[i][k]);
-        s += v[i][k];
-      }
-      *reinterpret_cast<tia::half8_t*>(x + (p32 ? tia::p32_off(row, 8 * gi) : int64_t(row) * hidden + 8 * gi)) = o;
-    }
-  }
-  const float mean = tia::wave_sum(s) / float(hidden);
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (lane + 64 * i < groups) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) ss += (v[i][k] - mean) * (v[i][k] - mean);
-    }
-  const float inv = rsqrtf(tia::wave_sum(ss) / float(hidden) + 1e-5f);
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int gi = lane + 64 * i;
-    if (gi < groups) {
-      const tia::half8_t gg = *reinterpret_cast<const tia::half8_t*>(g + 8 * gi);
-      const tia::half8_t bb = *reinterpret_cast<const tia::half8_t*>(bt + 8 * gi);
-      tia::half8_t o;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) o[k] = tia::f16r((v[i][k] - mean) * inv * float(gg[k]) + float(bb[k]));
-      *reinterpret_cast<tia::half8_t*>(norm + (p32 ? tia::p32_off(row, 8 * gi) : int64_t(row) * hidden + 8 * gi)) = o;
-    }
-  }
+  EmbedRow r;
+  r.fetch(lane, valid, pos, wpe, g, bt, hidden);
+  r.finish(lane, valid, id, wte, x, norm, row, hidden, p32);
 }
 
 // Embedding rows of a pass, row = b * qlen + t (or, over compact rows,
@@ -310,6 +330,15 @@ __global__ __launch_bounds__(1024) void greedy_feed_kernel(FeedArgs a) {
   __shared__ float sv[16];
   __shared__ int si[16];
   const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nt = blockDim.x;
+  // Wave 0 reads the row's position and fetches the next position's wpe row
+  // and ln_1's gamma/beta while the partials are merged: only the token row
+  // waits for the id.
+  int pos = 0;
+  EmbedRow emb;
+  if (wave == 0) {
+    pos = a.offsets[row];
+    emb.fetch(lane, pos + 1 < a.positions, pos + 1, a.wpe, a.g, a.bt, a.hidden);
+  }
   int id;
   if (a.groups > 0) {
     // Four partials per thread in flight at a time.
@@ -344,7 +373,6 @@ __global__ __launch_bounds__(1024) void greedy_feed_kernel(FeedArgs a) {
     if (wave != 0) return;
     id = a.next[row];
   }
-  const int pos = a.offsets[row];
   if (lane == 0) {
     a.next[row] = id;
     a.run[int64_t(pos) * a.b + row] = id;
@@ -353,7 +381,7 @@ __global__ __launch_bounds__(1024) void greedy_feed_kernel(FeedArgs a) {
   }
   if (pos + 1 < a.positions) {
     const bool ok = id >= 0 && id < a.vocab;
-    embed_ln_row(lane, true, ok ? id : 0, pos + 1, a.wte, a.wpe, a.g, a.bt, a.x, a.norm, row, a.hidden, a.p32);
+    emb.finish(lane, true, ok ? id : 0, a.wte, a.x, a.norm, row, a.hidden, a.p32);
   }
 }
 
