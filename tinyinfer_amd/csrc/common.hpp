@@ -42,10 +42,21 @@ __device__ __forceinline__ float h2f(uint16_t bits) { return float(__builtin_bit
 __device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, f16r(v)); }
 __device__ __forceinline__ float rt16(float v) { return float(f16r(v)); }
 
-// tanh-approximated GELU (GPT-2 "gelu_new"): 0.5 z (1 + tanh(sqrt(2/pi) (z + 0.044715 z^3))).
-// tanhf is ROCm's device libm.
+// tanh(x) = sign(x) (1 - 2 / (exp(2 |x|) + 1)) on the hardware exp2 and
+// reciprocal (about 2e-7 absolute error; exp overflows to +inf for large |x|,
+// giving exactly +-1).  Against the device libm's tanhf: fewer instructions
+// and no branches, in the configs[1] GEMM epilogue M = 512,
+// 768 -> 3072 12.76 -> 11.53 us, and over all 63 488 finite fp16 inputs the
+// fp16 GELU below differs from the CPU oracle's (std::tanh) in 5 values by
+// one ulp (1 with tanhf).
+__device__ __forceinline__ float tanh_exp(float x) {
+  const float e = __builtin_amdgcn_exp2f(fabsf(x) * 2.8853900817779268f);  // exp(2|x|) = 2^(2 log2(e) |x|)
+  return copysignf(1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f), x);
+}
+// tanh-approximated GELU (GPT-2 "gelu_new"): 0.5 z (1 + tanh(sqrt(2/pi) (z + 0.044715 z^3))),
+// the reference's expression (reference kernels/src/cuda/tc/elementwise.cu:29-31).
 __device__ __forceinline__ float gelu_tanh(float z) {
-  return 0.5f * z * (1.f + tanhf(0.7978845608028654f * (z + 0.044715f * z * z * z)));
+  return 0.5f * z * (1.f + tanh_exp(0.7978845608028654f * (z + 0.044715f * z * z * z)));
 }
 
 // Workgroup barrier that orders LDS accesses only: outstanding global loads
