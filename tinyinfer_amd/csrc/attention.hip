@@ -387,7 +387,32 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
       if (!arrive_last(counter, active)) return;
       constexpr int DPL = D / 64;  // dims per lane in the merge
       float gm = kNegInf;
-      for (int c0 = 0; c0 < active; c0 += 8) {
+      float tl = 0.f, tacc[DPL] = {};
+      if (active <= 8) {
+        // Up to 8 chunks (1024 keys at 128 per chunk): every state in one
+        // round of loads, the common maximum and the sums from registers.
+        float cm[8], cl[8], ca[8][DPL];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float* pc = base + min(c, active - 1) * (2 + D);
+          cm[c] = ld_agent(pc);
+          cl[c] = ld_agent(pc + 1);
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) ca[c][e] = ld_agent(pc + 2 + DPL * lane + e);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (c < active && cl[c] > 0.f) gm = fmaxf(gm, cm[c]);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          if (c >= active) break;
+          const float f = cl[c] > 0.f ? __expf(cm[c] - gm) : 0.f;
+          tl += cl[c] * f;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) tacc[e] += ca[c][e] * f;
+        }
+      }
+      for (int c0 = 0; active > 8 && c0 < active; c0 += 8) {
         float cm[8], cl[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -399,8 +424,7 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
         for (int c = 0; c < 8; ++c)
           if (c0 + c < active && cl[c] > 0.f) gm = fmaxf(gm, cm[c]);
       }
-      float tl = 0.f, tacc[DPL] = {};
-      for (int c0 = 0; c0 < active; c0 += 8) {
+      for (int c0 = 0; active > 8 && c0 < active; c0 += 8) {
         float cm[8], cl[8], ca[8][DPL];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
