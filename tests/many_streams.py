@@ -1,7 +1,8 @@
 """A fresh process whose first library calls run on eight streams at once:
 every split plan that finishes in its launch through the library's
 per-hardware-queue pool (row-major skinny and tiled GEMMs, the packed K-split
-GEMV, the four-tile GEMV, the split panel GEMM, split-key decode attention) is
+GEMV, the four-tile GEMV, the split panel GEMM, split-key decode attention, split-key causal
+prefill attention) is
 enqueued on every stream with no synchronisation between them, three times
 over, and each result must equal, bit for bit, the same call made alone on
 one stream afterwards.  Streams map onto the hardware queues round-robin, so
@@ -72,7 +73,22 @@ def main():
                 k=gpu(f16(rng.standard_normal((B, H, K, D)) / 8), torch.float16),
                 v=gpu(f16(rng.standard_normal((B, H, K, D)) / 8), torch.float16),
                 meta=[gpu(np.asarray(x, np.int32)) for x in ([1] * B, L, L - 1)])
+    # Causal prefill over few query tiles: heavy tiles split their keys over
+    # two workgroups merged through the prefill pool.
+    PB, PH, PN = 1, 4, 1024
+    pre = dict(q=gpu(f16(rng.standard_normal((PB, PH, PN, D)) * 0.5), torch.float16),
+               k=gpu(f16(rng.standard_normal((PB, PH, PN, D)) * 0.5), torch.float16),
+               v=gpu(f16(rng.standard_normal((PB, PH, PN, D))), torch.float16),
+               ql=gpu(np.full(PB, PN, np.int32)), off=gpu(np.zeros(PB, np.int32)))
     torch.cuda.synchronize()
+
+    def run_prefill(st):
+        out = torch.empty((PB, PH, PN, D), dtype=torch.float16, device="cuda")
+        r = lib.ti_v2_attention_f16(pre["q"].data_ptr(), pre["k"].data_ptr(), pre["v"].data_ptr(), out.data_ptr(),
+                                    pre["ql"].data_ptr(), pre["ql"].data_ptr(), pre["off"].data_ptr(), PB, PH, PN, PN,
+                                    D, 1, 0, st, 0)
+        assert r == 0, lib.ti_v2_last_error()
+        return out
 
     def run(c, st):
         y = torch.empty((c["m"], c["n"]), dtype=torch.float16, device="cuda")
@@ -93,7 +109,8 @@ def main():
         assert r == 0, lib.ti_v2_last_error()
         return out
 
-    print(f"[streams] {len(cases)} GEMMs and split attention on {STREAMS} streams at once, 3 rounds", flush=True)
+    print(f"[streams] {len(cases)} GEMMs, split decode and prefill attention on {STREAMS} streams at once, 3 rounds",
+          flush=True)
     streams = [torch.cuda.Stream() for _ in range(STREAMS)]
     got = []
     for rnd in range(3):
@@ -103,13 +120,13 @@ def main():
                 # Each stream walks the cases from a different start.
                 order = cases[i % len(cases):] + cases[:i % len(cases)]
                 res = {id(c): run(c, sm.cuda_stream) for c in order}
-                outs.append([res[id(c)] for c in cases] + [run_attn(sm.cuda_stream)])
+                outs.append([res[id(c)] for c in cases] + [run_attn(sm.cuda_stream), run_prefill(sm.cuda_stream)])
         torch.cuda.synchronize()
         got.extend(outs)
 
     print("[streams] the same calls alone on one stream", flush=True)
     st = torch.cuda.current_stream().cuda_stream
-    want = [run(c, st) for c in cases] + [run_attn(st)]
+    want = [run(c, st) for c in cases] + [run_attn(st), run_prefill(st)]
     torch.cuda.synchronize()
     bad = []
     for r, outs in enumerate(got):

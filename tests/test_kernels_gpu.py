@@ -709,6 +709,28 @@ def test_attention_prefill_many_tiles(ops, causal):
 
 
 @pytest.mark.parametrize("causal", [0, 1])
+def test_attention_prefill_four_key_groups(ops, causal):
+    """At most 256 workgroups of 64 queries (2 x 4 x 17): the 16-wave kernel with
+    four key groups, each taking every fourth key tile, merged at the end;
+    ragged lengths and offsets, and queries past a request's length zero."""
+    t = torch()
+    rng = np.random.default_rng(41 + causal)
+    B, H, D, nq, nk = 2, 4, 64, 1088, 1200
+    ql = [1088, 701]
+    kl = [1200, 760]
+    off = [kv - qv for qv, kv in zip(ql, kl)]
+    q = f16(rng.standard_normal((B, H, nq, D)) * 0.5)
+    k = f16(rng.standard_normal((B, H, nk, D)) * 0.5)
+    v = f16(rng.standard_normal((B, H, nk, D)))
+    say("attention prefill four key groups", causal)
+    out = ops.attention(dev(q, t.float16), dev(k, t.float16), dev(v, t.float16), q_lengths=ql,
+                        kv_lengths=kl, query_offsets=off, causal=bool(causal))
+    got = h(hbits(out))
+    close(got, h(oracle.attention_f16(q, k, v, ql, kl, off, bool(causal))))
+    assert not got[1, :, 701:].any()
+
+
+@pytest.mark.parametrize("causal", [0, 1])
 def test_attention_prefill_two_query_blocks(ops, causal):
     """At least 768 workgroups of 128 queries (4 x 12 x 16): the 4-wave kernel
     with two 16-query blocks per wave.  Ragged lengths put a block boundary

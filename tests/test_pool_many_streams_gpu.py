@@ -16,10 +16,10 @@ ROOT = Path(__file__).resolve().parents[1]
 
 
 def test_split_plans_on_eight_streams_equal_lone_calls():
-    print("[case] many_streams.py: 7 GEMM plans + split attention on 8 streams, 3 rounds", flush=True)
+    print("[case] many_streams.py: 7 GEMM plans + split decode and prefill attention on 8 streams, 3 rounds", flush=True)
     res = subprocess.run([sys.executable, str(ROOT / "tests" / "many_streams.py")], cwd=ROOT,
                          capture_output=True, text=True, timeout=110)
     print(res.stdout[-4000:], res.stderr[-4000:], flush=True)
     assert res.returncode == 0, f"many_streams.py exited {res.returncode}"
     report = json.loads(res.stdout.strip().splitlines()[-1])
-    assert report["ok"] and report["calls"] == 3 * 8 * 8
+    assert report["ok"] and report["calls"] == 3 * 8 * 9

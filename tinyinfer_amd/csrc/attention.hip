@@ -16,6 +16,7 @@
 // are dot(q,k) * D^-1/2, keys j < kv_valid (and j <= offset + qi when causal),
 // rows with no visible key (or padded queries) are exactly zero.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
@@ -505,8 +506,21 @@ constexpr int prefill_waves_per_simd(int d, int ks, int qb) {
   return (d == 64 ? 4 : 2) / ks / qb > 0 ? (d == 64 ? 4 : 2) / ks / qb : 1;
 }
 
-template <int D, int KS, int QB = 1>
+// Causal prefill with few query tiles (C ABI): a query tile with at least
+// kPrefillSplitTiles key tiles is split into two workgroups over the two halves
+// of its key tiles, so the heaviest tiles spread over twice the CUs; each half
+// stores its (m, l, acc) state in the calling queue's slot of this pool and the
+// tile's last half to arrive merges both (half 0 first).  A queue that finds
+// every slot taken runs each tile whole in its first workgroup.
+constexpr int kPrefillSlots = 4;
+constexpr int kPrefillPoolTiles = 256;
+constexpr int kPrefillSplitTiles = 8;
+constexpr size_t kPrefillPoolFloats = size_t(kPrefillPoolTiles) * 2 * 256 * (64 / 16 * 4 + 2);  // acc, then (m, l)
+TIA_QUEUE_POOL_N(pf_pool, kPrefillSlots, kPrefillPoolFloats, kPrefillPoolTiles)
+
+template <int D, int KS, int QB = 1, bool SPLITKV = false>
 __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void prefill_mfma_kernel(AttnParams p) {
+  static_assert(!SPLITKV || (D == 64 && QB == 1), "split prefill: 64-dim heads, one query block");
   constexpr int BQ = 64 * QB, BT = 64, KPK = D + 16, KPV = D + 16;
   constexpr int SEGS = D / 8;                 // 16-byte pieces per key row
   constexpr int PIECES = BT * SEGS / 256;     // per thread per tile (2 or 4)
@@ -517,8 +531,9 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   auto vs = reinterpret_cast<f16(*)[KS][BT][KPV]>(lds_raw + 2 * KS * BT * KPK * sizeof(f16));
   const AttnArgs& a = p.a;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // KS = 2: waves 4..7 are a second key group taking the odd tiles of each
-  // step; each group stages its own tile and the two merge at the end.
+  // KS > 1: waves 4g .. 4g + 3 form key group g, which takes tile g of each
+  // step (tiles KS s + g); each group stages its own tile and the groups merge
+  // at the end.
   const int grp = wave >> 2, qw = wave & 3, gt = int(threadIdx.x & 255);
   const int j = lane & 15, g = lane >> 4;
   // Workgroups go to the 8 XCDs round-robin by linear id.  Taken as is, the
@@ -528,12 +543,32 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   // eight L2s.  Instead ids are regrouped into 8 contiguous runs (one per XCD)
   // of whole (b, h) rows, and within a row the query tiles alternate light and
   // heavy (0, n-1, 1, n-2, ...), so a run that splits a row is balanced too.
-  int b, h, q0;
+  // SPLITKV: an XCD's run of R ids (R even) holds half 0 of its R / 2 tiles
+  // in its first R / 2 ids and half 1 of the same tiles, in reverse order, in
+  // the rest, so the two workgroups a CU takes in turn (run positions c and
+  // c + R / 2) pair a light tile's half with a heavy tile's.
+  int b, h, q0, part = 0, tile_id = 0;
   {
-    const int nq = int(gridDim.x), nh = int(gridDim.y);
-    const int n = nq * nh * int(gridDim.z), n8 = n & ~7;
-    const int id = int(blockIdx.x) + nq * (int(blockIdx.y) + nh * int(blockIdx.z));
-    const int li = id < n8 ? (id & 7) * (n8 >> 3) + (id >> 3) : id;
+    constexpr int PARTS = SPLITKV ? 2 : 1;
+    const int nx = int(gridDim.x), nq = nx / PARTS, nh = int(gridDim.y);
+    const int n = nx * nh * int(gridDim.z);
+    const int id = int(blockIdx.x) + nx * (int(blockIdx.y) + nh * int(blockIdx.z));
+    int li;
+    if constexpr (SPLITKV) {
+      const int n16 = n & ~15;
+      if (id < n16) {
+        const int c = id >> 3, run = n16 >> 3, half = run >> 1;
+        part = c < half ? 0 : 1;
+        li = (id & 7) * half + (c < half ? c : run - 1 - c);
+      } else {
+        part = id & 1;
+        li = id >> 1;
+      }
+    } else {
+      const int n8 = n & ~7;
+      li = id < n8 ? (id & 7) * (n8 >> 3) + (id >> 3) : id;
+    }
+    tile_id = li;
     const int k = li % nq, row = li / nq;
     h = row % nh;
     b = row / nh;
@@ -546,7 +581,18 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   const int last_q = min(q0 + BQ, q_valid) - 1;
   const int key_end = last_q < q0 ? 0 : int(min<int64_t>(kvv, a.causal ? off + last_q + 1 : kvv));
   const int ntiles = (key_end + BT - 1) / BT;
-  const int nsteps = (ntiles + KS - 1) / KS;
+  // Key tiles [t_begin, t_end) of this workgroup.
+  int t_begin = 0, t_end = ntiles, pf_slot = -1;
+  if constexpr (SPLITKV) {
+    if (ntiles >= kPrefillSplitTiles) pf_slot = queue_slot_claim(pf_pool_keys, kPrefillSlots);
+    if (pf_slot < 0 && part == 1) return;  // the whole tile runs in part 0
+    if (pf_slot >= 0) {
+      const int half = (ntiles + 1) / 2;
+      t_begin = part * half;
+      t_end = min(ntiles, t_begin + half);
+    }
+  }
+  const int nsteps = (t_end - t_begin + KS - 1) / KS;
   const int64_t slot = a.kv_slot ? int64_t(a.kv_slot[b]) : int64_t(b);
   const uint16_t* kbase = a.k + slot * a.kv_sb + int64_t(h) * a.kv_sh;
   const uint16_t* vbase = a.v + slot * a.kv_sb + int64_t(h) * a.kv_sh;
@@ -586,7 +632,7 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   };
   Staged st0, st1;
   auto load_tile = [&](Staged& r_, int step) {
-    const int t = step * KS + grp;
+    const int t = t_begin + step * KS + grp;
 #pragma unroll
     for (int r = 0; r < PIECES; ++r) {
       const int piece = gt + 256 * r, key = piece / SEGS, seg = piece % SEGS;
@@ -628,9 +674,9 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   // the other buffer (its loads were issued two steps ago), then the loads of
   // step s + 3 into the registers just freed.
   auto step = [&](int s_, Staged& next) {
-    const int buf = s_ & 1, t = s_ * KS + grp;
+    const int buf = s_ & 1, t = t_begin + s_ * KS + grp;
     // This wave's queries see nothing of this tile: skip the math, keep the barriers.
-    if (t < ntiles && wq0 < q_valid && t * BT < wave_end) {
+    if (t < t_end && wq0 < q_valid && t * BT < wave_end) {
       float4_t sc[QB][4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
@@ -742,13 +788,16 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
     step(s_, st1);
     if (s_ + 1 < nsteps) step(s_ + 1, st0);
   }
-  if constexpr (KS == 2) {
-    // Group 1 hands its (m, l, acc) per lane and block to group 0 through LDS
-    // (free after the last barrier); group 0 merges on the larger reference:
-    // the states are sums of 2^(x - m).
+  if constexpr (KS > 1) {
+    // Groups 1 .. KS - 1 hand their (m, l, acc) per lane and block to group 0
+    // through LDS (free after the last barrier); group 0 merges them in group
+    // order on the largest reference: the states are sums of 2^(x - m).
     constexpr int PER = D / 16 * 4 + 2;
-    float* xs = reinterpret_cast<float*>(lds_raw) + (qw * 64 + lane) * PER * QB;
-    if (grp == 1) {
+    auto slot = [&](int g) {
+      return reinterpret_cast<float*>(lds_raw) + ((g - 1) * 256 + qw * 64 + lane) * PER * QB;
+    };
+    if (grp >= 1) {
+      float* xs = slot(grp);
 #pragma unroll
       for (int u = 0; u < QB; ++u) {
 #pragma unroll
@@ -760,22 +809,89 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
       }
     }
     __syncthreads();
-    if (grp == 1) return;
+    // (A split tile's groups all take part in the arrival below.)
+    if (grp >= 1 && pf_slot < 0) return;
 #pragma unroll
-    for (int u = 0; u < QB; ++u) {
+    for (int u = 0; grp == 0 && u < QB; ++u) {
       const float l = accl[u][0];
-      const float m1 = xs[u * PER + PER - 2], l1 = xs[u * PER + PER - 1];
-      const float nm = fmaxf(l > 0.f ? m[u] : kNegInf, l1 > 0.f ? m1 : kNegInf);
+      float nm = l > 0.f ? m[u] : kNegInf;
+#pragma unroll
+      for (int g = 1; g < KS; ++g) {
+        const float* xs = slot(g);
+        if (xs[u * PER + PER - 1] > 0.f) nm = fmaxf(nm, xs[u * PER + PER - 2]);
+      }
       const float f0 = l > 0.f ? __builtin_amdgcn_exp2f(m[u] - nm) : 0.f;
-      const float f1 = l1 > 0.f ? __builtin_amdgcn_exp2f(m1 - nm) : 0.f;
       // Explicit fmas: with contraction left to the compiler, a * f0 + b * f1
       // may fuse either product, and differently per instantiation (the bits
       // of a query would then depend on QB).
-      accl[u][0] = fmaf(l1, f1, l * f0);
+      float tl = l * f0;
 #pragma unroll
       for (int d = 0; d < D / 16; ++d)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[u][d][v] = fmaf(xs[u * PER + 4 * d + v], f1, acc[u][d][v] * f0);
+        for (int v = 0; v < 4; ++v) acc[u][d][v] *= f0;
+#pragma unroll
+      for (int g = 1; g < KS; ++g) {
+        const float* xs = slot(g);
+        const float lg = xs[u * PER + PER - 1];
+        const float fg = lg > 0.f ? __builtin_amdgcn_exp2f(xs[u * PER + PER - 2] - nm) : 0.f;
+        tl = fmaf(lg, fg, tl);
+#pragma unroll
+        for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[u][d][v] = fmaf(xs[u * PER + 4 * d + v], fg, acc[u][d][v]);
+      }
+      accl[u][0] = tl;
+      m[u] = nm;  // the merged state's reference (a split tile's half stores it)
+    }
+  }
+  if constexpr (SPLITKV) {
+    if (pf_slot >= 0) {
+      // This half's state (group 0's lanes) to the pool, then the arrival;
+      // the tile's last half merges half 0's state, then half 1's.  Layout:
+      // acc as float4 [tile][half][d][lane] (every store and load instruction
+      // one contiguous KiB), then (m, l) pairs [tile][half][lane].
+      const int lid = qw * 64 + lane;
+      const auto rs = agent_rsrc(pf_pool_data[pf_slot], uint32_t(kPrefillPoolFloats * sizeof(float)));
+      auto acc_at = [&](int pt, int d) {
+        return uint32_t((((tile_id * 2 + pt) * (D / 16) + d) * 256 + lid) * 16);
+      };
+      auto ml_at = [&](int pt) {
+        return pf_pool_data[pf_slot] + size_t(kPrefillPoolTiles) * 2 * (D / 16) * 256 * 4 +
+               (size_t(tile_id * 2 + pt) * 256 + lid) * 2;
+      };
+      if (grp == 0) {
+#pragma unroll
+        for (int d = 0; d < D / 16; ++d)
+          st_agent4(rs, acc_at(part, d), f32x4_t{acc[0][d][0], acc[0][d][1], acc[0][d][2], acc[0][d][3]});
+        st_agent(ml_at(part), m[0]);
+        st_agent(ml_at(part) + 1, accl[0][0]);
+      }
+      unsigned* counter = pf_pool_ctr[pf_slot] + tile_id * kCounterStride;
+      // The flag reuses the first word of the tile buffers (read by now): a
+      // static LDS word would push two workgroups of 80 KiB past a CU's LDS.
+      if (!wg_arrive_last(counter, 2, reinterpret_cast<int*>(lds_raw)) || grp >= 1) return;
+      float oacc[D / 16][4];
+#pragma unroll
+      for (int d = 0; d < D / 16; ++d) {
+        const f32x4_t o = ld_agent4(rs, acc_at(1 - part, d));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) oacc[d][v] = o[v];
+      }
+      const float om = ld_agent(ml_at(1 - part)), ol = ld_agent(ml_at(1 - part) + 1);
+      depart(counter);
+      const float mA = part == 0 ? m[0] : om, lA = part == 0 ? accl[0][0] : ol;
+      const float mB = part == 0 ? om : m[0], lB = part == 0 ? ol : accl[0][0];
+      const float nm = fmaxf(lA > 0.f ? mA : kNegInf, lB > 0.f ? mB : kNegInf);
+      const float fA = lA > 0.f ? __builtin_amdgcn_exp2f(mA - nm) : 0.f;
+      const float fB = lB > 0.f ? __builtin_amdgcn_exp2f(mB - nm) : 0.f;
+      accl[0][0] = fmaf(lB, fB, lA * fA);
+#pragma unroll
+      for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float aA = part == 0 ? acc[0][d][v] : oacc[d][v], aB = part == 0 ? oacc[d][v] : acc[0][d][v];
+          acc[0][d][v] = fmaf(aB, fB, aA * fA);
+        }
     }
   }
 
@@ -795,16 +911,29 @@ __global__ __launch_bounds__(256 * KS, prefill_waves_per_simd(D, KS, QB)) void p
   }
 }
 
-// K and V rows (pitch D + 16), two buffers per key group; the KS = 2 merge
+// LDS bytes a workgroup may use on the current device (cached per device).
+size_t max_lds_per_block() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return size_t(n);
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || n <= 0) return 0;
+  cached[dev].store(n, std::memory_order_relaxed);
+  return size_t(n);
+}
+
+// K and V rows (pitch D + 16), two buffers per key group; the key-group merge
 // reuses them.
-template <int D, int KS, int QB>
+template <int D, int KS, int QB, bool SPLITKV = false>
 hipError_t launch_prefill(dim3 grid, const AttnParams& p, hipStream_t stream) {
   constexpr size_t lds = size_t(KS) * 2 * 2 * 64 * (D + 16) * 2;
-  static_assert(KS == 1 || size_t(256) * (D / 16 * 4 + 2) * QB * 4 <= lds, "merge fits the tile buffers");
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<D, KS, QB>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+  static_assert(KS == 1 || size_t(KS - 1) * 256 * (D / 16 * 4 + 2) * QB * 4 <= lds, "merge fits the tile buffers");
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&prefill_mfma_kernel<D, KS, QB, SPLITKV>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      int(lds));
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((prefill_mfma_kernel<D, KS, QB>), grid, dim3(256 * KS), lds, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<D, KS, QB, SPLITKV>), grid, dim3(256 * KS), lds, stream, p);
   return hipGetLastError();
 }
 
@@ -876,6 +1005,18 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
       if constexpr (D == 64) {
         if (two_blocks)
           return split_keys ? launch_prefill<D, 2, 2>(grid, p, stream) : launch_prefill<D, 1, 2>(grid, p, stream);
+        // At most one workgroup per CU.  Causal: the heavy query tiles split
+        // their key tiles over two workgroups (the tile count per CU evens
+        // out); otherwise every tile is equally heavy, and four key groups
+        // (16 waves, all 160 KiB of LDS) give each CU more waves to hide
+        // latency with.
+        if (split_keys && wgs <= 256 && a.causal && wgs <= kPrefillPoolTiles) {
+          dim3 g2 = grid;
+          g2.x *= 2;
+          return launch_prefill<D, 2, 1, true>(g2, p, stream);
+        }
+        if (split_keys && wgs <= 256 && max_lds_per_block() >= size_t(4) * 2 * 2 * 64 * (D + 16) * 2)
+          return launch_prefill<D, 4, 1>(grid, p, stream);
       }
       return split_keys ? launch_prefill<D, 2, 1>(grid, p, stream) : launch_prefill<D, 1, 1>(grid, p, stream);
     } else {

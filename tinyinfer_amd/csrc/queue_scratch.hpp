@@ -31,6 +31,14 @@ constexpr int kQueueSlots = 32;
 // Counters sit 32 apart (one 128-byte line each).
 constexpr int kCounterStride = 32;
 
+// A pool of `slots` (at most kQueueSlots) slots whose dispatches, when every
+// slot is taken by other queues, get no slot (queue_slot_claim returns -1) and
+// must then run a plan that needs none.
+#define TIA_QUEUE_POOL_N(prefix, slots, data_floats, counter_count)                                 \
+  static __device__ __align__(256) unsigned long long prefix##_keys[(slots)];                      \
+  static __device__ __align__(256) float prefix##_data[(slots)][(data_floats)];                    \
+  static __device__ __align__(256) unsigned prefix##_ctr[(slots)][(counter_count) * ::tia::kCounterStride];
+
 #define TIA_QUEUE_POOL(prefix, data_floats, counter_count)                                          \
   static __device__ __align__(256) unsigned long long prefix##_keys[::tia::kQueueSlots];            \
   static __device__ __align__(256) float prefix##_data[::tia::kQueueSlots][(data_floats)];          \
@@ -58,6 +66,34 @@ __device__ __forceinline__ int queue_slot_resolve(unsigned long long* keys, unsi
     if (prev == 0 || prev == me) return e;
   }
   return int((me >> 12) % kQueueSlots);
+}
+
+// The slot of the calling dispatch's queue in a pool of `slots` entries, or
+// -1 when every entry belongs to another queue.  Called by a whole wave;
+// every wave of a dispatch gets the same answer (a key once claimed is final).
+__device__ __forceinline__ int queue_slot_claim(unsigned long long* keys, int slots) {
+  const unsigned long long me = reinterpret_cast<unsigned long long>(__builtin_amdgcn_queue_ptr());
+  const int lane = int(threadIdx.x & 63);
+  const unsigned long long key = lane < slots ? keys[lane] : ~0ull;
+  const unsigned long long hit = __ballot(lane < slots && key == me);
+  if (hit) return __builtin_ffsll(static_cast<long long>(hit)) - 1;
+  unsigned long long cand = __ballot(lane < slots && key == 0);
+  while (cand) {
+    const int e = __builtin_ffsll(static_cast<long long>(cand)) - 1;
+    cand &= cand - 1;
+    unsigned long long prev = 0;
+    if (lane == 0)
+      __hip_atomic_compare_exchange_strong(keys + e, &prev, me, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0, 64);
+    if (prev == 0 || prev == me) return e;
+  }
+  // Entries read as taken may have been claimed by this queue since: one
+  // more look at the whole table.
+  const unsigned long long again = lane < slots ? __hip_atomic_load(keys + lane, __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+  const unsigned long long hit2 = __ballot(lane < slots && again == me);
+  return hit2 ? __builtin_ffsll(static_cast<long long>(hit2)) - 1 : -1;
 }
 
 // Relaxed agent-scope accesses: visible to every XCD (the hardware writes these
@@ -104,15 +140,20 @@ __device__ __forceinline__ bool arrive_last(unsigned* counter, int parties) {
 // The same for a whole workgroup whose waves all stored shares: each wave
 // waits for its own stores, the workgroup meets, one thread moves the counter,
 // and every thread learns whether this workgroup arrived last.
-__device__ __forceinline__ bool wg_arrive_last(unsigned* counter, int parties) {
-  __shared__ int last;
+// `flag` is an int of LDS the workgroup no longer reads (the overload without
+// it declares one: a kernel sized to fill LDS exactly passes its own).
+__device__ __forceinline__ bool wg_arrive_last(unsigned* counter, int parties, int* flag) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == unsigned(parties - 1);
+    *flag = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == unsigned(parties - 1);
   __syncthreads();
-  return last != 0;
+  return *flag != 0;
+}
+__device__ __forceinline__ bool wg_arrive_last(unsigned* counter, int parties) {
+  __shared__ int last;
+  return wg_arrive_last(counter, parties, &last);
 }
 // Leaves the counter at zero for the next dispatch on this queue (called by
 // the last arriver once; any thread of it).
