@@ -28,9 +28,10 @@ namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
-// Split decode of the C ABI: per hardware queue, 2 MiB of chunk states
-// [B][H][chunks][2 + D] and one arrival counter per (b, h) row
-// (queue_scratch.hpp); a call beyond either runs the one-pass kernel.
+// Split decode of the C ABI: per hardware queue, 2 MiB of chunk states (acc
+// [B][H][chunks][D], then (m, l) [B][H][chunks]) and one arrival counter per
+// (b, h) row (queue_scratch.hpp); a call beyond either runs the one-pass
+// kernel.
 constexpr size_t kAttnPoolFloats = size_t(1) << 19;
 constexpr int kAttnPoolRows = 4096;
 TIA_QUEUE_POOL(attn_pool, kAttnPoolFloats, kAttnPoolRows)
@@ -50,9 +51,9 @@ struct AttnParams {
   AttnArgs a;
   float scale;
   bool vec;       // every pointer and stride allows 16-byte accesses
-  bool split;     // split decode: key chunks of each (b, h) over workgroups, the
-                  // states [B][H][chunks][2 + D] = (m, l, unnormalized acc) in the
-                  // queue's pool slot, merged by the row's last chunk to finish
+  bool split;     // split decode: key chunks of each (b, h) over workgroups, each
+                  // chunk's (m, l, unnormalized acc) in the queue's pool slot,
+                  // merged by the row's last chunk to finish
   int chunks;     // split decode: key chunks per (b, h)
 };
 
@@ -373,17 +374,22 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
       const int lane64 = int(threadIdx.x & 63);
       const unsigned long long key = lane64 < kQueueSlots ? attn_pool_keys[lane64] : 0ull;
       const int sl = queue_slot_resolve(attn_pool_keys, key);
+      // Layout: acc [row][chunk][D] (a key group's lanes write it as 16-byte
+      // pieces), then (m, l) [row][chunk].
       const int64_t row = int64_t(b) * a.heads + h;
-      float* base = attn_pool_data[sl] + row * p.chunks * (2 + D);
+      const int64_t states = int64_t(a.batch) * a.heads * p.chunks;
+      float* base = attn_pool_data[sl] + row * p.chunks * D;
+      float* mlb = attn_pool_data[sl] + states * D + row * p.chunks * 2;
       unsigned* counter = attn_pool_ctr[sl] + row * kCounterStride;
       if (kg == 0) {
-        float* part = base + chunk_id * (2 + D);
+        const auto rs = agent_rsrc(attn_pool_data[sl], uint32_t(kAttnPoolFloats * sizeof(float)));
+        const uint32_t at = uint32_t(((row * p.chunks + chunk_id) * D + 8 * ds) * sizeof(float));
+        st_agent4(rs, at, f32x4_t{acc[0], acc[1], acc[2], acc[3]});
+        st_agent4(rs, at + 16, f32x4_t{acc[4], acc[5], acc[6], acc[7]});
         if (lane == 0) {
-          st_agent(part, m);
-          st_agent(part + 1, l);
+          st_agent(mlb + 2 * chunk_id, m);
+          st_agent(mlb + 2 * chunk_id + 1, l);
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) st_agent(part + 2 + 8 * ds + e, acc[e]);
       }
       if (!arrive_last(counter, active)) return;
       constexpr int DPL = D / 64;  // dims per lane in the merge
@@ -395,11 +401,11 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
         float cm[8], cl[8], ca[8][DPL];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          const float* pc = base + min(c, active - 1) * (2 + D);
-          cm[c] = ld_agent(pc);
-          cl[c] = ld_agent(pc + 1);
+          const int cc = min(c, active - 1);
+          cm[c] = ld_agent(mlb + 2 * cc);
+          cl[c] = ld_agent(mlb + 2 * cc + 1);
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) ca[c][e] = ld_agent(pc + 2 + DPL * lane + e);
+          for (int e = 0; e < DPL; ++e) ca[c][e] = ld_agent(base + cc * D + DPL * lane + e);
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c)
@@ -417,9 +423,9 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
         float cm[8], cl[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          const float* pc = base + min(c0 + c, active - 1) * (2 + D);
-          cm[c] = ld_agent(pc);
-          cl[c] = ld_agent(pc + 1);
+          const int cc = min(c0 + c, active - 1);
+          cm[c] = ld_agent(mlb + 2 * cc);
+          cl[c] = ld_agent(mlb + 2 * cc + 1);
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c)
@@ -429,11 +435,11 @@ __global__ __launch_bounds__(QW * KW * 64) void attention_kernel(AttnParams p) {
         float cm[8], cl[8], ca[8][DPL];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          const float* pc = base + min(c0 + c, active - 1) * (2 + D);
-          cm[c] = ld_agent(pc);
-          cl[c] = ld_agent(pc + 1);
+          const int cc = min(c0 + c, active - 1);
+          cm[c] = ld_agent(mlb + 2 * cc);
+          cl[c] = ld_agent(mlb + 2 * cc + 1);
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) ca[c][e] = ld_agent(pc + 2 + DPL * lane + e);
+          for (int e = 0; e < DPL; ++e) ca[c][e] = ld_agent(base + cc * D + DPL * lane + e);
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
