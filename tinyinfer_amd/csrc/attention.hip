@@ -951,13 +951,17 @@ hipError_t launch(const AttnParams& p, hipStream_t stream) {
     // Decode: one workgroup per (b, h) whose KW waves split the keys.  Each
     // wave keeps at least 4 tiles of 32/16 keys (two double-buffered rounds;
     // fewer make the LDS merge of the waves cost more than the parallelism
-    // gains; timed on GPT-2 small, 96 keys: KW 1; GPT-2 XL, 640 keys and 800
-    // heads: KW 4).  KW follows the cache length only, not the batch, so a
-    // request's result does not depend on the requests decoded with it.
+    // gains; timed on GPT-2 XL, 640 keys and 800 heads: KW 4), except that a
+    // cache of 3 to 7 tiles takes two waves, so every tile's loads go out in
+    // one round (GPT-2 small, 96 / 192 keys: b = 1 decode 3.55 -> 3.65 K tok/s
+    // at 192, b = 32 unchanged or +0.6 %).  KW follows the cache length only,
+    // not the batch, so a request's result does not depend on the requests
+    // decoded with it.
     const int tile_keys = D == 64 ? 32 : 16;
     const int tiles = (a.kv_len + tile_keys - 1) / tile_keys;
     int kw = 1;
     while (kw < 8 && kw * 2 * 4 <= tiles) kw *= 2;
+    if (kw == 1 && tiles >= 3) kw = 2;
     dim3 grid = blocks_per;
     grid.x = 1;
     if (p.split) {
