@@ -1,6 +1,6 @@
 """A fresh process whose first library calls run on eight streams at once:
 every split plan that finishes in its launch through the library's
-per-hardware-queue pool (row-major skinny and tiled GEMMs, the packed K-split
+per-hardware-queue pool (row-major GEMV, skinny and tiled GEMMs, the packed K-split
 GEMV, the four-tile GEMV, the split panel GEMM, split-key decode attention, split-key causal
 prefill attention) is
 enqueued on every stream with no synchronisation between them, three times
@@ -51,7 +51,8 @@ def main():
     lib.ti_v2_attention_f16.argtypes = [P] * 7 + [I] * 7 + [ctypes.c_size_t, I]
 
     cases = []
-    for kind, m, k, n in (("rowmajor", 1, 768, 3072), ("rowmajor", 8, 3072, 768), ("rowmajor", 64, 768, 3072),
+    for kind, m, k, n in (("rowmajor", 1, 768, 3072), ("rowmajor", 8, 3072, 768), ("rowmajor", 24, 3072, 768),
+                          ("rowmajor", 64, 768, 3072),
                           ("rowmajor", 512, 3072, 768), ("packed", 32, 3072, 768), ("packed", 64, 3072, 768),
                           ("packed", 512, 3072, 768)):
         rng = np.random.default_rng(m * 7 + k + n)

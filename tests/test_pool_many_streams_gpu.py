@@ -22,4 +22,4 @@ def test_split_plans_on_eight_streams_equal_lone_calls():
     print(res.stdout[-4000:], res.stderr[-4000:], flush=True)
     assert res.returncode == 0, f"many_streams.py exited {res.returncode}"
     report = json.loads(res.stdout.strip().splitlines()[-1])
-    assert report["ok"] and report["calls"] == 3 * 8 * 9
+    assert report["ok"] and report["calls"] == 3 * 8 * 10

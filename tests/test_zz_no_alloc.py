@@ -53,7 +53,7 @@ def _run(lib, name, dev, m, n, k, dtype, config):
 # (M, N, K, dtype, config) pairs: the second call of each pair is smaller and
 # reuses the array the first one filled.  Every shape here splits K.
 PAIRS = [
-    ((64, 768, 3072, 0, 0), (1, 768, 768, 0, 0)),       # 22-way split tiled, then 24-way split skinny
+    ((64, 768, 3072, 0, 0), (1, 768, 768, 0, 0)),       # 22-way split tiled, then 12-way split row GEMV
     ((32, 3072, 768, 1, 7), (8, 2304, 768, 0, 2)),      # workspace epilogue + fp32 out, then fused fp16
 ]
 

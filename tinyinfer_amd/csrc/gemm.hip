@@ -11,6 +11,11 @@
 //    takes the part-block kernel instead when the caller does not batch rows
 //    (standalone GEMV calls): no MFMA, 8 columns per workgroup, twice the
 //    workgroups of the 16-column MFMA blocks.
+//  * row GEMV (M <= 16, row-major weights of the C ABIs, aligned operands):
+//    about 192 workgroups, each one 64-column tile over a K range of at most
+//    16 32-row steps per wave, every load of a wave in flight at once, the
+//    skinny kernel's fragments and MFMAs; K splits finish in the launch
+//    through the queue pool (rowgemv_kernel).
 //  * skinny (M <= 32, row-major weights of the ABI): every wave streams weight fragments straight from
 //    HBM into MFMA B-operand registers (no LDS for weights), dequantises them in
 //    registers as fp16_rn(float(q) * scale[n]) and runs v_mfma_f32_16x16x32_f16
@@ -441,6 +446,90 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_kernel(SkinnyParams p) 
       else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
     }
   }
+}
+
+// Row-major int8 GEMV of the C ABIs at M <= 16 (q [K][N] as the reference
+// keeps it, reference kernels/src/cuda/tc/gemm.cu:21): workgroup (tile, split)
+// covers one 64-column tile over at most W * S 32-row K steps; wave w takes
+// steps w, w + W, ... with every load of the wave in flight before its first
+// MFMA (the skinny kernel's fragments and dequantisation).  The waves meet in
+// LDS; with one split the workgroup runs the epilogue, otherwise each split's
+// sums go to the queue's pool slot and the tile's last split to arrive adds
+// them in split order (one round of loads) and runs it.  The plan depends on N
+// and K only, so a row's result does not depend on M.
+constexpr int kRowSplits = 16;
+template <int W, int S>
+__global__ __launch_bounds__(W * 64) void rowgemv_kernel(SkinnyParams p) {
+  __shared__ float red[W][16][65];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  // Consecutive (tile, split) ids per XCD (blocks go round-robin over the 8
+  // XCDs): the two tiles that share a 128-byte weight line read it through one L2.
+  const int nb = gridDim.x, bid = blockIdx.x;
+  const int logical = (nb % 8 == 0) ? (bid % 8) * (nb / 8) + bid / 8 : bid;
+  const int tile = logical % p.ntile, split = logical / p.ntile;
+  const int s0 = split * p.steps_per_block, s1 = min(p.steps, s0 + p.steps_per_block);
+  const int n0 = tile * 64, col = n0 + 4 * j;
+  float sc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) sc[c] = col + c < p.n ? p.scales[col + c] : 0.f;
+  WFrag<true> f[S];
+  half8_t a[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int st = s0 + wave + W * i;
+    if (st < s1) {
+      load_wfrag<true, true>(f[i], p.w, p.k, p.n, p.ldw, st * 32 + 8 * g, col);
+      a[i] = afrag<true>(p.a, p.lda, p.m, p.k, j, st * 32 + 8 * g);
+    }
+  }
+  float4_t acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    if (s0 + wave + W * i < s1) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bfrag<true>(f[i], c, sc[c]), acc[c], 0, 0, 0);
+    }
+  }
+  // MFMA output: lane holds rows 4g + v (v = 0..3) of column j of each 16x16 block.
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave][4 * g + v][4 * j + c] = acc[c][v];
+  __syncthreads();
+  auto wave_sum = [&](int row, int cc) {
+    float s = red[0][row][cc];
+#pragma unroll
+    for (int w = 1; w < W; ++w) s += red[w][row][cc];
+    return s;
+  };
+  if (p.splits == 1) {
+    for (int e = threadIdx.x; e < p.m * 64; e += W * 64) {
+      const int row = e >> 6, cc = e & 63, n = n0 + cc;
+      if (n < p.n) apply_epilogue(p.epi, row, n, wave_sum(row, cc));
+    }
+    return;
+  }
+  // Split sp of the tile at parts + sp * 1024 + (row * 64 + column).
+  const PoolSlot slot = gemm_pool_slot();
+  float* parts = slot.parts + int64_t(tile) * p.splits * 1024;
+  for (int e = threadIdx.x; e < p.m * 64; e += W * 64) st_agent(parts + split * 1024 + e, wave_sum(e >> 6, e & 63));
+  if (!wg_arrive_last(slot.ctr + tile * kCounterStride, p.splits)) return;
+  for (int e = threadIdx.x; e < p.m * 64; e += W * 64) {
+    float v[kRowSplits];
+#pragma unroll
+    for (int u = 0; u < kRowSplits; ++u) v[u] = u < p.splits ? ld_agent(parts + u * 1024 + e) : 0.f;
+    float s = v[0];
+#pragma unroll
+    for (int u = 1; u < kRowSplits; ++u)
+      if (u < p.splits) s += v[u];
+    const int n = n0 + (e & 63);
+    if (n < p.n) apply_epilogue(p.epi, e >> 6, n, s);
+  }
+  depart(slot.ctr + tile * kCounterStride);
 }
 
 // Second pass of a split-K launch: C[m][n] = sum of the split partials in split
@@ -1828,6 +1917,42 @@ int skinny_splits(int m, int n, int k, size_t capacity) {
   return (steps + spb - 1) / spb;
 }
 
+// Plan of rowgemv_kernel: about 192 workgroups (a 2.4 MB GEMV is latency-bound:
+// one round of loads per wave over most CUs, each workgroup reading a few
+// hundred weight rows), K split into equal whole-step ranges of at most
+// 4 x 16 steps; 8 waves when a split has at most 8 steps, else 16.  Depends
+// on N and K only.  hipErrorNotSupported when the shape does not fit (more
+// than kRowSplits splits, or partials beyond the pool): the caller then takes
+// the skinny kernel.
+constexpr int kRowTargetBlocks = 192;
+template <int W, int S>
+hipError_t launch_rowgemv_ws(const SkinnyParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((rowgemv_kernel<W, S>), dim3(unsigned(p.ntile) * unsigned(p.splits)), dim3(W * 64), 0, stream, p);
+  return hipGetLastError();
+}
+hipError_t launch_rowgemv(const GemmArgs& g, hipStream_t stream) {
+  SkinnyParams p{};
+  p.a = g.a; p.lda = g.lda; p.w = g.w; p.scales = g.scales;
+  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.ldw = g.ldw > 0 ? g.ldw : g.n;
+  p.ntile = (g.n + 63) / 64;
+  p.steps = (g.k + 31) / 32;
+  int splits = std::clamp((kRowTargetBlocks + p.ntile / 2) / p.ntile, 1, kRowSplits);
+  splits = std::max(splits, (p.steps + 63) / 64);
+  if (splits > kRowSplits) return hipErrorNotSupported;
+  const int spb = (p.steps + splits - 1) / splits;
+  splits = (p.steps + spb - 1) / spb;
+  if (splits > 1 && (p.ntile > kPoolTiles || int64_t(p.ntile) * splits * 1024 > int64_t(kPoolFloats)))
+    return hipErrorNotSupported;
+  p.steps_per_block = spb;
+  p.splits = splits;
+  p.pool = splits > 1;
+  if (spb <= 8) return launch_rowgemv_ws<8, 1>(p, stream);
+  if (spb <= 16) return launch_rowgemv_ws<16, 1>(p, stream);
+  if (spb <= 32) return launch_rowgemv_ws<16, 2>(p, stream);
+  return launch_rowgemv_ws<16, 4>(p, stream);
+}
+
 // The skinny finisher spreads a tile's splits over its idle threads: rows
 // below M of each 16-row pass take 16 threads each, and the 256 threads form
 // skinny_groups(M) such groups, each summing a run of at most
@@ -2611,6 +2736,10 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
       if (e != hipErrorNotSupported) return e;
     }
     return launch_panel(g, s, stream, deferred);
+  }
+  if (g.m <= 16 && g.w_int8 && wvec && avec && s && s->queue_pool && !deferred) {
+    const hipError_t e = launch_rowgemv(g, stream);
+    if (e != hipErrorNotSupported) return e;
   }
   if (g.m <= 16) return g.w_int8 ? launch_skinny<true, 1>(g, wvec, avec, s, stream, deferred)
                                  : launch_skinny<false, 1>(g, wvec, avec, s, stream, deferred);
