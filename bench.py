@@ -151,33 +151,42 @@ def run_decode(model, batch, steps, warmup, prompt_len=None):
 # ---------------------------------------------------------------- graph-replay timing
 class Replay:
     """Captures a list of native launches (ctypes calls on one torch stream) in a
-    HIP graph and times back-to-back replays with HIP events on that stream."""
+    HIP graph and times back-to-back replays with HIP events on that stream.
+    The graph holds the list repeated to at least 64 launches, so the gap
+    between two replays is a small share of the timed region even for kernels
+    whose inputs rotate over few sets; the result is the median of 5 rounds of
+    `reps` replays, per launch."""
 
     def __init__(self):
         import torch
         self.torch = torch
         self.stream = torch.cuda.Stream()
 
-    def time_us(self, launches, reps=5):
+    def time_us(self, launches, reps=5, rounds=5, min_launches=64):
         t = self.torch
         with t.cuda.stream(self.stream):
             launches[0]()  # the first call on a stream creates the library's split-K scratch
         t.cuda.synchronize()
+        per_graph = list(launches) * -(-min_launches // len(launches))
         graph = t.cuda.CUDAGraph()
         with t.cuda.graph(graph, stream=self.stream):
-            for fn in launches:
+            for fn in per_graph:
                 fn()
+        times = []
         with t.cuda.stream(self.stream):
             graph.replay()
             t.cuda.synchronize()
-            e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-            e0.record(self.stream)
-            for _ in range(reps):
-                graph.replay()
-            e1.record(self.stream)
+            for _ in range(rounds):
+                e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+                e0.record(self.stream)
+                for _ in range(reps):
+                    graph.replay()
+                e1.record(self.stream)
+                e1.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3 / (reps * len(per_graph)))
         t.cuda.synchronize()
         del graph
-        return e0.elapsed_time(e1) * 1e3 / (reps * len(launches))
+        return float(np.median(times))
 
 
 def _lib():
