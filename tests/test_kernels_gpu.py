@@ -102,7 +102,8 @@ def test_gemm_reference_gate_shapes(ops, golden, config, int8):
 
 @pytest.mark.parametrize("m,n,k", [(1, 768, 3072), (3, 100, 1000), (8, 3072, 768), (20, 2304, 768),
                                    (32, 768, 3072), (33, 70, 129), (64, 3072, 768), (100, 50, 40),
-                                   (2, 50257, 768), (64, 768, 3072), (512, 768, 3072), (40, 130, 2000)])
+                                   (2, 50257, 768), (64, 768, 3072), (512, 768, 3072), (40, 130, 2000),
+                                   (40, 1000, 776), (100, 1000, 1000), (700, 264, 1000), (1024, 768, 768)])
 def test_gemm_split_k_and_tiled_paths(ops, m, n, k):
     say("gemm paths", m, n, k)
     gemm_case(ops, m, n, k, 0, True, seed=1)

@@ -11,12 +11,14 @@
 //    takes the part-block kernel instead when the caller does not batch rows
 //    (standalone GEMV calls): no MFMA, 8 columns per workgroup, twice the
 //    workgroups of the 16-column MFMA blocks.
-//  * row GEMV (M <= 16, row-major weights of the C ABIs, aligned operands):
-//    about 192 workgroups, each one 64-column tile over a K range of at most
-//    16 32-row steps per wave, every load of a wave in flight at once, the
-//    skinny kernel's fragments and MFMAs; K splits finish in the launch
-//    through the queue pool (rowgemv_kernel).
-//  * skinny (M <= 32, row-major weights of the ABI): every wave streams weight fragments straight from
+//  * row GEMV / GEMM (M <= 1024, row-major weights of the C ABIs, aligned
+//    operands): about 192 workgroups, each one 64-column tile of 16 (M <= 64)
+//    or 32 rows over a range of 32-row K steps, every load of a wave's round
+//    in flight at once, the skinny kernel's fragments and MFMAs; K splits
+//    finish in the launch through the queue pool (rowgemv_kernel at M <= 16,
+//    rowgemm_kernel above).
+//  * skinny (M <= 32, row-major weights, where the row GEMV does not apply:
+//    unaligned operands, no queue pool): every wave streams weight fragments straight from
 //    HBM into MFMA B-operand registers (no LDS for weights), dequantises them in
 //    registers as fp16_rn(float(q) * scale[n]) and runs v_mfma_f32_16x16x32_f16
 //    with A padded to 16/32 rows.  A lane loads one dword (4 consecutive output
@@ -29,7 +31,7 @@
 //    of the tile in the same launch (partials in the queue's slot of a static
 //    pool, written and read with agent-scope accesses, so no L2-wide
 //    writeback or invalidate is needed; queue_scratch.hpp).
-//  * tiled (M > 32, prefill): 64x64x32 tiles, A and the dequantised weight tile
+//  * tiled (M > 32 where the row GEMM does not apply, M > 1024): 64x64x32 tiles, A and the dequantised weight tile
 //    staged in LDS (weights transposed to [n][k] so both MFMA operands are one
 //    ds_read_b128 per lane), double buffered, same fused epilogues.
 // Dequantisation mirrors reference kernels/src/cuda/tc/gemm.cu:21,24 and the
@@ -205,6 +207,7 @@ struct SkinnyParams {
   int m, n, k;
   int64_t ldw;         // row stride of W in elements (>= n)
   int ntile;           // ceil(N / 64)
+  int rblocks;         // row blocks (rowgemm_kernel)
   int steps;           // ceil(K / 32)
   int steps_per_block; // K steps owned by one workgroup (its waves take every 4th)
   int splits;
@@ -531,6 +534,130 @@ __global__ __launch_bounds__(W * 64) void rowgemv_kernel(SkinnyParams p) {
   }
   depart(slot.ctr + tile * kCounterStride);
 }
+
+// Row-major int8 GEMM of the C ABIs at 16 < M <= 1024 (q [K][N] as the reference
+// keeps it, reference kernels/src/cuda/tc/gemm.cu:21), built like the skinny
+// kernel (weight fragments from HBM straight into MFMA B registers, dequantised
+// there, no LDS staging): workgroup (tile, row block, split) covers one
+// 64-column tile and 16 * MT rows over a range of 32-row K steps; wave w takes
+// steps w, w + W, ..., S of them per round with every load of the round in
+// flight before its first MFMA.  The waves meet in LDS; with one split the
+// workgroup runs the epilogue, otherwise each split's sums go to the queue's
+// pool slot as float4s and the unit's last split to arrive adds them in split
+// order (one round of loads) and runs it.  The plan depends on N, K and the row
+// block size only (16 rows up to M = 64, then 32), so within one block size a
+// row's result does not depend on M.
+template <int MT, int W, int S>
+__global__ __launch_bounds__(W * 64) void rowgemm_kernel(SkinnyParams p) {
+  constexpr int R = 16 * MT, NT = W * 64;
+  constexpr int OUT4 = (R * 16 + NT - 1) / NT;  // float4 outputs of a finishing thread
+  constexpr int SMAX = kPoolLoads / OUT4;       // splits its one round of loads covers
+  __shared__ float red[W][R][65];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  // Consecutive ids per XCD (blocks go round-robin over the 8 XCDs), column
+  // tile fastest: the two tiles that share a 128-byte weight line, and the
+  // tiles that share a row block's A rows, are read through one L2.
+  const int nb = gridDim.x, bid = blockIdx.x;
+  const int logical = (nb % 8 == 0) ? (bid % 8) * (nb / 8) + bid / 8 : bid;
+  const int tile = logical % p.ntile, rest = logical / p.ntile;
+  const int rb = rest % p.rblocks, split = rest / p.rblocks;
+  const int m0 = rb * R, rows = min(R, p.m - m0);
+  const int s0 = split * p.steps_per_block, s1 = min(p.steps, s0 + p.steps_per_block);
+  const int n0 = tile * 64, col = n0 + 4 * j;
+  float sc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) sc[c] = col + c < p.n ? p.scales[col + c] : 0.f;
+  float4_t acc[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[t][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int base = s0 + wave; base < s1; base += W * S) {
+    WFrag<true> f[S];
+    half8_t a[S][MT];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int st = base + W * i;
+      if (st < s1) {
+        load_wfrag<true, true>(f[i], p.w, p.k, p.n, p.ldw, st * 32 + 8 * g, col);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) a[i][t] = afrag<true>(p.a, p.lda, p.m, p.k, m0 + 16 * t + j, st * 32 + 8 * g);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      if (base + W * i < s1) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const half8_t b = bfrag<true>(f[i], c, sc[c]);
+#pragma unroll
+          for (int t = 0; t < MT; ++t) acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][t], b, acc[t][c], 0, 0, 0);
+        }
+      }
+    }
+  }
+  // MFMA output: lane holds rows 4g + v (v = 0..3) of column j of each 16x16 block.
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][16 * t + 4 * g + v][4 * j + c] = acc[t][c][v];
+  __syncthreads();
+  // float4 output q of the unit: row q / 16, columns 4 (q % 16) .. + 3.
+  const int tid = int(threadIdx.x), nq = rows * 16;
+  auto wave_sum4 = [&](int q) {
+    const int r = q >> 4, c0 = 4 * (q & 15);
+    f32x4_t v;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float x = red[0][r][c0 + c];
+#pragma unroll
+      for (int w = 1; w < W; ++w) x += red[w][r][c0 + c];
+      v[c] = x;
+    }
+    return v;
+  };
+  auto epilogue4 = [&](int q, const f32x4_t& v) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int n = n0 + 4 * (q & 15) + c;
+      if (n < p.n) apply_epilogue(p.epi, m0 + (q >> 4), n, v[c]);
+    }
+  };
+  if (p.splits == 1) {
+    for (int q = tid; q < nq; q += NT) epilogue4(q, wave_sum4(q));
+    return;
+  }
+  const PoolSlot slot = gemm_pool_slot();
+  const auto rs = agent_rsrc(slot.parts, uint32_t(kPoolFloats * sizeof(float)));
+  const int unit = tile * p.rblocks + rb;
+  auto off = [&](int sp, int q) { return uint32_t(((int64_t(unit) * p.splits + sp) * (R * 16) + q) * 16); };
+  for (int q = tid; q < nq; q += NT) st_agent4(rs, off(split, q), wave_sum4(q));
+  if (!wg_arrive_last(slot.ctr + unit * kCounterStride, p.splits)) return;
+  f32x4_t v[OUT4][SMAX];
+#pragma unroll
+  for (int o = 0; o < OUT4; ++o)
+#pragma unroll
+    for (int u = 0; u < SMAX; ++u) {
+      const int q = tid + o * NT;
+      v[o][u] = q < nq && u < p.splits ? ld_agent4(rs, off(u, q)) : f32x4_t{};
+    }
+  depart(slot.ctr + unit * kCounterStride);
+#pragma unroll
+  for (int o = 0; o < OUT4; ++o) {
+    const int q = tid + o * NT;
+    if (q >= nq) continue;
+    f32x4_t sum = v[o][0];
+#pragma unroll
+    for (int u = 1; u < SMAX; ++u)
+      if (u < p.splits) sum += v[o][u];
+    epilogue4(q, sum);
+  }
+}
+// Most splits of a rowgemm_kernel<MT, W, S> plan.
+constexpr int rowgemm_max_splits(int mt, int w) { return kPoolLoads / ((16 * mt * 16 + w * 64 - 1) / (w * 64)); }
 
 // Second pass of a split-K launch: C[m][n] = sum of the split partials in split
 // order, then the epilogue.  The kernel boundary orders it after every partial.
@@ -1953,6 +2080,52 @@ hipError_t launch_rowgemv(const GemmArgs& g, hipStream_t stream) {
   return launch_rowgemv_ws<16, 4>(p, stream);
 }
 
+// Plan of rowgemm_kernel (16 < M <= kRowMaxM): rows in blocks of 16 up to
+// M = 64, then 32 (timed, configs[1] row-major shapes: M = 40 / 64 768->3072
+// 7.7 / 7.8 us in 16-row blocks against 8.5 / 8.8 in 32-row ones, M = 512
+// 24.4 against 16.2 us; 64-row blocks, four waves, lost everywhere: M = 64
+// 14.3, M = 512 18.5 us); about 192 workgroups as above, K split within the
+// finisher's one round of loads and the pool slot; 8 waves, 16 once a split
+// of 16-row blocks has more than 8 steps; S steps a round, rounds repeated
+// over longer splits.
+constexpr int kRowMaxM = 1024;
+template <int MT, int W, int S>
+hipError_t launch_rowgemm_ws(const SkinnyParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((rowgemm_kernel<MT, W, S>), dim3(unsigned(p.ntile * p.rblocks * p.splits)), dim3(W * 64), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+hipError_t launch_rowgemm(const GemmArgs& g, hipStream_t stream) {
+  SkinnyParams p{};
+  p.a = g.a; p.lda = g.lda; p.w = g.w; p.scales = g.scales;
+  p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
+  p.ldw = g.ldw > 0 ? g.ldw : g.n;
+  p.ntile = (g.n + 63) / 64;
+  p.steps = (g.k + 31) / 32;
+  const int mt = g.m <= 64 ? 1 : 2;
+  p.rblocks = (g.m + 16 * mt - 1) / (16 * mt);
+  const int64_t units = int64_t(p.ntile) * p.rblocks;
+  int splits = int(std::clamp<int64_t>((kRowTargetBlocks + units / 2) / units, 1, rowgemm_max_splits(mt, 8)));
+  while (splits > 1 && units * splits * 16 * mt * 64 > int64_t(kPoolFloats)) --splits;
+  if (splits > 1 && units > kPoolTiles) splits = 1;
+  const int spb = (p.steps + splits - 1) / splits;
+  splits = (p.steps + spb - 1) / spb;
+  if (units * splits > INT_MAX / 2) return hipErrorNotSupported;
+  p.steps_per_block = spb;
+  p.splits = splits;
+  p.pool = splits > 1;
+  if (mt == 1) {
+    if (spb <= 8) return launch_rowgemm_ws<1, 8, 1>(p, stream);
+    if (spb <= 16) return launch_rowgemm_ws<1, 16, 1>(p, stream);
+    if (spb <= 32) return launch_rowgemm_ws<1, 16, 2>(p, stream);
+    return launch_rowgemm_ws<1, 16, 4>(p, stream);
+  }
+  if (spb <= 8) return launch_rowgemm_ws<2, 8, 1>(p, stream);
+  if (spb <= 16) return launch_rowgemm_ws<2, 8, 2>(p, stream);
+  return launch_rowgemm_ws<2, 8, 4>(p, stream);
+}
+
+
 // The skinny finisher spreads a tile's splits over its idle threads: rows
 // below M of each 16-row pass take 16 threads each, and the 256 threads form
 // skinny_groups(M) such groups, each summing a run of at most
@@ -2737,8 +2910,8 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
     }
     return launch_panel(g, s, stream, deferred);
   }
-  if (g.m <= 16 && g.w_int8 && wvec && avec && s && s->queue_pool && !deferred) {
-    const hipError_t e = launch_rowgemv(g, stream);
+  if (g.m <= kRowMaxM && g.w_int8 && wvec && avec && s && s->queue_pool && !deferred) {
+    const hipError_t e = g.m <= 16 ? launch_rowgemv(g, stream) : launch_rowgemm(g, stream);
     if (e != hipErrorNotSupported) return e;
   }
   if (g.m <= 16) return g.w_int8 ? launch_skinny<true, 1>(g, wvec, avec, s, stream, deferred)
