@@ -4,7 +4,7 @@ GEMM through NativeOps.gemm_int8 at M in {1, 8, 64, 512} x both configs[1]
 shapes, configs 0 (fused) and 6 (caller workspace); ti_amd_pack_w8 then
 ti_amd_gemm_w8p_fused (bias + GELU) over the packed weights at shapes that
 take each packed kernel (M=1 part-block GEMV, M=16 / 32 K-split GEMV, M=64
-four-tile GEMV split and unsplit, M=512 split panel GEMM); and
+row-block GEMV, M=512 split panel GEMM); and
 ti_v2_attention_f16 at the configs[3] shape (B=32, H=12, D=64, ragged
 U[128,1024]).  Neither may
 allocate (the reference ABI's contract, backend/include/tinyinfer_backend_v2.h:13),

@@ -1,8 +1,8 @@
 """A fresh process whose first library calls run on eight streams at once:
 every split plan that finishes in its launch through the library's
 per-hardware-queue pool (row-major GEMV, skinny and tiled GEMMs, the packed K-split
-GEMV, the four-tile GEMV, the split panel GEMM, split-key decode attention, split-key causal
-prefill attention) is
+GEMV, the split panel GEMM, split-key decode attention, split-key causal
+prefill attention), and the packed row-block GEMV beside them, is
 enqueued on every stream with no synchronisation between them, three times
 over, and each result must equal, bit for bit, the same call made alone on
 one stream afterwards.  Streams map onto the hardware queues round-robin, so

@@ -308,9 +308,9 @@ def test_packed_gemv_column_block_groups(ops, m, k, n):
 def test_packed_prefill_gemm_against_oracle(ops, m, k, n):
     """Prefill (M > 32) GEMM over panel-packed weights: ragged row and column tiles,
     bias and bias+GELU epilogues against the oracle; fp32-accumulate tolerance.
-    33..64 rows over at most 192 column blocks and K <= 3072 run the four-tile
-    packed GEMV (K split and finished in the launch where the grid is short of
-    column blocks); the in-place residual epilogue at M <= 64."""
+    33..64 rows over at most 192 column blocks and K <= 3072 run the packed GEMV
+    over row blocks of 16 (the last one partly filled at M = 33, 40, 48, 57);
+    the in-place residual epilogue at M <= 64."""
     t = torch()
     rng = np.random.default_rng(11 * m + k + n)
     a = f16(rng.standard_normal((m, k)))

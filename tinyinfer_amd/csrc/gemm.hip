@@ -743,6 +743,7 @@ struct PackedParams {
   // output and its column, as the wide GEMV leaves them for greedy decoding.
   float* amax_v;
   int32_t* amax_i;
+  int rblocks;          // RB launches: row blocks of 16 * MT rows
 };
 
 
@@ -772,7 +773,8 @@ __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float scal
 // POOL (the C ABIs): a split launch finishes in the kernel -- every
 // workgroup stores its reduced sums to the queue pool and the last of a column
 // group's splits to arrive adds them in split order and runs the epilogue.
-template <int MT, int W, int CPW, int CBG, bool LNA = false, bool PA = false, bool CW = false, bool POOL = false>
+template <int MT, int W, int CPW, int CBG, bool LNA = false, bool PA = false, bool CW = false, bool POOL = false,
+          bool RB = false>
 __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   __shared__ float red[W][CBG][MT * 256];
   __shared__ float stat[LNA ? W : 1][MT * 16];  // per-wave LayerNorm partial sums
@@ -787,7 +789,12 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   const int nbk = gridDim.x, bid = blockIdx.x;
   const int logical = (nbk % 8 == 0) ? (bid % 8) * (nbk / 8) + bid / 8 : bid;
   const int groups = (p.nb + CBG - 1) / CBG;
-  const int grp = logical % groups, split = logical / groups;
+  // RB: row block rb (16 * MT rows from m0) varies fastest, so the row blocks
+  // of a column group read its records through one XCD's L2.
+  const int rb = RB ? logical % p.rblocks : 0;
+  const int unit = RB ? logical / p.rblocks : logical;
+  const int grp = unit % groups, split = unit / groups;
+  const int m0 = RB ? rb * 16 * MT : 0, mrow = p.m - m0;
   const int cb0 = grp * CBG;
   const int c_begin = split * p.chunks_per_split;
   const int c_end = min(p.kc, c_begin + p.chunks_per_split);
@@ -814,18 +821,18 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
   }
   const uint16_t* arow[MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) arow[t] = p.a + int64_t(min(16 * t + j, p.m - 1)) * p.lda + 8 * g;
+  for (int t = 0; t < MT; ++t) arow[t] = p.a + (int64_t(m0) + min(16 * t + j, mrow - 1)) * p.lda + 8 * g;
   // PA: lane offset inside a fragment, rows past M clamped to row M - 1 like
   // the row-major path (at M = 1 a fragment load then touches one cache line).
   int pa_lane[MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) pa_lane[t] = (min(16 * t + j, p.m - 1) - 16 * t + 16 * g) * 8;
+  for (int t = 0; t < MT; ++t) pa_lane[t] = (min(16 * t + j, mrow - 1) - 16 * t + 16 * g) * 8;
 
   // Outputs of this thread in the epilogue: o = threadIdx.x + it * W * 64 over
   // CBG blocks of rows x 16.  Their residuals are loaded now, unconditionally
   // (A's first element stands in), like the bias.
   constexpr int kOutIters = (CBG * MT * 256 + W * 64 - 1) / (W * 64);
-  const int rows = min(p.m, MT * 16), per_block = rows * 16;
+  const int rows = min(mrow, MT * 16), per_block = rows * 16;
   const bool has_res = epi_now && p.epi.kind == EPI_RESIDUAL;
   const uint16_t* rsrc = has_res ? p.epi.residual : p.a;
   // Output o of the epilogue: block r = o / per_block, element rem (with one
@@ -850,7 +857,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
       int r, rem;
       block_of(o, r, rem);
       const int n = (cb0 + r) * 16 + (rem & 15);
-      if (o < CBG * per_block && cb0 + r < p.nb && n < p.n) roff = r_off(p.epi, rem >> 4, n);
+      if (o < CBG * per_block && cb0 + r < p.nb && n < p.n) roff = r_off(p.epi, m0 + (rem >> 4), n);
     }
     res_raw[it] = ldg_u16(rsrc + roff);
   }
@@ -1069,7 +1076,7 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
         uint16_t braw = bias_raw[0];
 #pragma unroll
         for (int q = 1; q < CBG; ++q) braw = r == q ? bias_raw[q] : braw;
-        apply_epilogue(p.epi, row, n, v, has_bias ? h2f(braw) : 0.f, has_res ? h2f(res_raw[it]) : 0.f);
+        apply_epilogue(p.epi, m0 + row, n, v, has_bias ? h2f(braw) : 0.f, has_res ? h2f(res_raw[it]) : 0.f);
       }
       return;
     }
@@ -1090,8 +1097,8 @@ __global__ __launch_bounds__(W * 64) void gemv_packed_kernel(PackedParams p) {
 #pragma unroll
     for (int q = 1; q < CBG; ++q) braw = r == q ? bias_raw[q] : braw;
     const float bias = has_bias ? h2f(braw) : 0.f;
-    if (epi_now) apply_epilogue(p.epi, row, n, s, bias, has_res ? h2f(res_raw[it]) : 0.f);
-    else p.partials[(int64_t(split) * p.m + row) * p.n + n] = s;
+    if (epi_now) apply_epilogue(p.epi, m0 + row, n, s, bias, has_res ? h2f(res_raw[it]) : 0.f);
+    else p.partials[(int64_t(split) * p.m + m0 + row) * p.n + n] = s;
     if (MT == 1) {
       amax_val = s + bias;  // the EPI_F32 value
       amax_col = n;
@@ -2211,11 +2218,11 @@ GemvShape gemv_shape(int mt, int chunks, bool one_round, int nb) {
   return s;
 }
 
-template <int MT, bool LNA, bool PA, bool CW = false, bool POOL = false>
+template <int MT, bool LNA, bool PA, bool CW = false, bool POOL = false, bool RB = false>
 hipError_t launch_gemv_shape(const PackedParams& p, GemvShape sh, int grid, hipStream_t st) {
 #define TIA_GEMV(W_, C_, B_)                                                                            \
   if (sh.w == W_ && sh.cpw == C_ && sh.cbg == B_) {                                                     \
-    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA, PA, CW, POOL>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
+    hipLaunchKernelGGL((gemv_packed_kernel<MT, W_, C_, B_, LNA, PA, CW, POOL, RB>), dim3(unsigned(grid)), dim3(W_ * 64), 0, st, p); \
     return hipGetLastError();                                                                           \
   }
   TIA_GEMV(4, 3, 1)
@@ -2404,54 +2411,28 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
             : launch_gemv_shape<MT, false, false>(p, sh, grid, stream);
 }
 
-// 33..64 rows through the C ABI (queue pool) over at most 192 column blocks
-// and K <= 3072: the packed GEMV with four 16-row MFMA tiles (MT = 4), K split
-// to ~192 workgroups of at most 24 chunks and finished in the launch.  The
-// weights stream once and A (at most 64 rows) is re-read from L2 by every
-// column block, against the panel GEMM's 64 x 64 tiles, which at these M run
-// few tiles over a long K (timed, panel -> GEMV: M = 64 768 -> 3072 8.85 ->
-// 7.23 us, 3072 -> 768 10.1 -> 9.04, M = 33 768 -> 3072 8.72 -> 5.79; wider
-// or longer shapes lose, their A re-reads growing with N or K: M = 48
-// 1600 -> 6400 11.4 -> 21.3, M = 64 6400 -> 1600 12.9 -> 18.8).  W <= 8
-// waves: four A tiles per chunk hold 140-235 registers.
-template <bool POOL>
-hipError_t launch_gemv4_shape(const PackedParams& p, GemvShape sh, int grid, hipStream_t st) {
-#define TIA_GEMV4(W_, C_)                                                                               \
-  if (sh.w == W_ && sh.cpw == C_ && sh.cbg == 1) {                                                      \
-    hipLaunchKernelGGL((gemv_packed_kernel<4, W_, C_, 1, false, false, false, POOL>), dim3(unsigned(grid)), \
-                       dim3(W_ * 64), 0, st, p);                                                         \
-    return hipGetLastError();                                                                           \
-  }
-  TIA_GEMV4(4, 3)
-  TIA_GEMV4(4, 4)
-  TIA_GEMV4(8, 3)
-  TIA_GEMV4(8, 4)
-#undef TIA_GEMV4
-  return hipErrorInvalidValue;
-}
-
-// Returns hipErrorNotSupported (nothing launched) for a plan it does not take.
-hipError_t launch_packed4(const GemmArgs& g, hipStream_t stream) {
+// 33..64 rows through the C ABI over at most 192 column blocks and K <= 3072:
+// the single-tile (MT = 1) GEMV over row blocks of 16 in one launch, no K
+// split: a column block's row blocks read its records through one XCD's L2
+// (cached loads), and each workgroup does a 16-row GEMV's work (timed: M = 64
+// 768->3072 6.3 -> 5.45 us, 3072->768 8.2 -> 6.4 us against four 16-row MFMA
+// tiles per wave with 4 K splits finished in the launch; M = 40 3072->768
+// 7.1 -> 6.3 us; at 17..32 rows the two-tile GEMV stays faster, M = 32 4.4 /
+// 5.9 against 4.6 / 6.4 us; wider or longer shapes keep the panel GEMM).
+hipError_t launch_packed_rb(const GemmArgs& g, hipStream_t stream) {
   PackedParams p{};
   p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
   p.m = g.m; p.n = g.n; p.k = g.k; p.epi = g.epi;
   p.nb = (g.n + 15) / 16;
   p.kc = g.k / 64;
-  int splits = std::max((p.kc + 23) / 24, std::min((192 + p.nb - 1) / p.nb, p.kc / 12));
-  splits = std::max(1, std::min(splits, kPoolGemvSplits));
-  p.chunks_per_split = (p.kc + splits - 1) / splits;
-  splits = (p.kc + p.chunks_per_split - 1) / p.chunks_per_split;
-  p.splits = splits;
-  const GemvShape sh = gemv_shape(4, p.chunks_per_split, false, p.nb);
-  const int out_iters = (4 * 256 + sh.w * 64 - 1) / (sh.w * 64);
-  if (sh.w > 8 || sh.cbg != 1 || splits > kPoolLoads / out_iters || (splits > 1 && p.nb > kPoolTiles) ||
-      int64_t(p.nb) * splits * 4 * 256 > int64_t(kPoolFloats))
-    return hipErrorNotSupported;
-  const int64_t grid = int64_t(p.nb) * splits;
-  if (grid > (int64_t(1) << 30)) return hipErrorNotSupported;
-  return splits > 1 ? launch_gemv4_shape<true>(p, sh, int(grid), stream)
-                    : launch_gemv4_shape<false>(p, sh, int(grid), stream);
+  p.chunks_per_split = p.kc;
+  p.splits = 1;
+  p.rblocks = (g.m + 15) / 16;
+  if (int64_t(p.nb) * p.rblocks > INT_MAX / 2) return hipErrorNotSupported;
+  const GemvShape sh = gemv_shape(1, p.kc, false, p.nb);
+  return launch_gemv_shape<1, false, false, true, false, true>(p, sh, p.nb * p.rblocks, stream);
 }
+
 
 // 64x64 tiles, S = 4 stages of 12 KiB (48 KiB of LDS: three workgroups per CU,
 // three chunks in flight each; six stages measured slower, since occupancy
@@ -2904,8 +2885,9 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
     if (part_gemv_preferred(g)) return launch_part(g, s, stream, deferred);
     if (g.m <= 16) return launch_packed<1>(g, s, stream, deferred);
     if (g.m <= 32) return launch_packed<2>(g, s, stream, deferred);
-    if (g.m <= 64 && s && s->queue_pool && !deferred && (g.n + 15) / 16 <= 192 && g.k <= 3072) {
-      const hipError_t e = launch_packed4(g, stream);
+    if (g.m <= 64 && s && s->queue_pool && !deferred && !g.ln_gamma && !g.a_p32 && !g.amax_groups &&
+        (g.n + 15) / 16 <= 192 && g.k <= 3072) {
+      const hipError_t e = launch_packed_rb(g, stream);
       if (e != hipErrorNotSupported) return e;
     }
     return launch_panel(g, s, stream, deferred);
