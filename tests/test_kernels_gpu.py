@@ -114,9 +114,10 @@ def test_gemm_split_k_and_tiled_paths(ops, m, n, k):
 @pytest.mark.parametrize("config", [0, 6])
 def test_gemm_rowmajor_gemv_shapes(ops, m, n, k, config):
     """Row-major int8 W at M <= 8 through the reference ABI (fused config 0 and
-    separate-workspace config 6), the skinny split-K path: K not a multiple of
-    32 (a ragged last step), N across several 64-column tiles with a part-filled
-    last one, N = 16 and 48 (one tile), and K = 4096."""
+    separate-workspace config 6): the row GEMV where rows and weight rows are
+    4/8-element aligned (K not a multiple of 32: a ragged last step; N across
+    several 64-column tiles with a part-filled last one; N = 48, one tile;
+    K = 4096), the skinny split-K kernel where they are not (N = 16, K = 17)."""
     say("gemm row-major gemv", m, n, k, "config", config)
     gemm_case(ops, m, n, k, config, True, seed=3)
 
