@@ -122,6 +122,18 @@ def test_gemm_rowmajor_gemv_shapes(ops, m, n, k, config):
     gemm_case(ops, m, n, k, config, True, seed=3)
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 3072, 768), (17, 768, 3072), (64, 1000, 1000), (65, 3072, 768),
+                                   (130, 768, 3072)])
+@pytest.mark.parametrize("config", [0, 6])
+def test_gemm_rowmajor_row_blocks(ops, m, n, k, config):
+    """Row-major int8 W through the reference ABI across the row GEMV / GEMM
+    boundaries: 16 rows (one block, the row GEMV), 17 (two 16-row blocks, the
+    second one row), 64 with ragged N and K, 65 (three 32-row blocks, the last
+    one row), 130; fused (config 0) and caller-workspace fp32 (config 6)."""
+    say("gemm row-major row blocks", m, n, k, "config", config)
+    gemm_case(ops, m, n, k, config, True, seed=5)
+
+
 @pytest.mark.parametrize("config", [0, 6])
 def test_gemm_tiled_split_k_fp16_weights(ops, config):
     """Row-major fp16 W over few tiles (M = 64, 3072 -> 768): K split over the
