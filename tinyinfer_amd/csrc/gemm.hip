@@ -544,9 +544,10 @@ __global__ __launch_bounds__(W * 64) void rowgemv_kernel(SkinnyParams p) {
 // flight before its first MFMA.  The waves meet in LDS; with one split the
 // workgroup runs the epilogue, otherwise each split's sums go to the queue's
 // pool slot as float4s and the unit's last split to arrive adds them in split
-// order (one round of loads) and runs it.  The plan depends on N, K and the row
-// block size only (16 rows up to M = 64, then 32), so within one block size a
-// row's result does not depend on M.
+// order (one round of loads) and runs it.  Row blocks are 16 rows up to M = 64,
+// then 32; the K split follows the count of (tile, row block) units, so unlike
+// the M <= 16 GEMV a row's sums may differ between M values (the reference ABI
+// promises no batch invariance; the runtime never takes this path).
 template <int MT, int W, int S>
 __global__ __launch_bounds__(W * 64) void rowgemm_kernel(SkinnyParams p) {
   constexpr int R = 16 * MT, NT = W * 64;
