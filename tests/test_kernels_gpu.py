@@ -317,13 +317,15 @@ def test_packed_gemv_column_block_groups(ops, m, k, n):
 @pytest.mark.parametrize("m,k,n", [(33, 768, 3072), (64, 3072, 768), (130, 128, 100), (512, 64, 2000),
                                    (512, 768, 3072), (512, 3072, 768), (2048, 768, 2304), (4100, 1600, 6400),
                                    (2050, 64, 8200), (48, 1600, 6400), (64, 6400, 1600), (40, 64, 8200),
-                                   (64, 768, 3072), (57, 768, 50257)])
+                                   (64, 768, 3072), (57, 768, 50257), (65, 768, 1000), (100, 3072, 768),
+                                   (128, 768, 3072)])
 def test_packed_prefill_gemm_against_oracle(ops, m, k, n):
     """Prefill (M > 32) GEMM over panel-packed weights: ragged row and column tiles,
     bias and bias+GELU epilogues against the oracle; fp32-accumulate tolerance.
-    33..64 rows over at most 192 column blocks and K <= 3072 run the packed GEMV
-    over row blocks of 16 (the last one partly filled at M = 33, 40, 48, 57);
-    the in-place residual epilogue at M <= 64."""
+    33..128 rows over at most 192 column blocks and K <= 3072 run the packed GEMV
+    over row blocks of 16 up to 64 rows (the last one partly filled at M = 33,
+    40, 57) and of 32 above (M = 65: a one-row last block; 100, 128); the
+    in-place residual epilogue at M <= 128."""
     t = torch()
     rng = np.random.default_rng(11 * m + k + n)
     a = f16(rng.standard_normal((m, k)))
@@ -338,7 +340,7 @@ def test_packed_prefill_gemm_against_oracle(ops, m, k, n):
     close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, bias_bits=bias)))
     _packed(ops.lib, ad, packed, sd, None, y, None, m, n, k, 1)
     close(h(hbits(y)), h(oracle.linear(a, q=q, scales=s, gelu=True)))
-    if m <= 64:
+    if m <= 128:
         ref = oracle.linear(a, q=q, scales=s, bias_bits=bias)
         res = dev(f16(rng.standard_normal((m, n))), t.float16)
         expect = (h(hbits(res)) + h(ref)).astype(np.float16).astype(np.float64)

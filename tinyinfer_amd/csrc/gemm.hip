@@ -2412,14 +2412,17 @@ hipError_t launch_packed(const GemmArgs& g, const Scratch* s, hipStream_t stream
             : launch_gemv_shape<MT, false, false>(p, sh, grid, stream);
 }
 
-// 33..64 rows through the C ABI over at most 192 column blocks and K <= 3072:
-// the single-tile (MT = 1) GEMV over row blocks of 16 in one launch, no K
-// split: a column block's row blocks read its records through one XCD's L2
-// (cached loads), and each workgroup does a 16-row GEMV's work (timed: M = 64
+// 33..128 rows through the C ABI over at most 192 column blocks and K <= 3072:
+// the single-tile (MT = 1) GEMV over row blocks of 16 up to 64 rows, the
+// two-tile one over row blocks of 32 above, in one launch, no K split: a
+// column block's row blocks read its records through one XCD's L2 (cached
+// loads), and each workgroup does a 16- or 32-row GEMV's work (timed: M = 64
 // 768->3072 6.3 -> 5.45 us, 3072->768 8.2 -> 6.4 us against four 16-row MFMA
 // tiles per wave with 4 K splits finished in the launch; M = 40 3072->768
-// 7.1 -> 6.3 us; at 17..32 rows the two-tile GEMV stays faster, M = 32 4.4 /
-// 5.9 against 4.6 / 6.4 us; wider or longer shapes keep the panel GEMM).
+// 7.1 -> 6.3 us; M = 128 against the panel GEMM 8.9 -> 7.6 us and 10.3 ->
+// 9.2 us; at 17..32 rows the two-tile GEMV stays faster, M = 32 4.4 / 5.9
+// against 4.6 / 6.4 us; from M = 256 the panel GEMM, 9.1 / 11.8 against 12.0 /
+// 14.8 us, and wider or longer shapes keep it too).
 hipError_t launch_packed_rb(const GemmArgs& g, hipStream_t stream) {
   PackedParams p{};
   p.a = g.a; p.lda = g.lda; p.w = static_cast<const u32x4_t*>(g.w_packed); p.scales = g.scales;
@@ -2428,10 +2431,14 @@ hipError_t launch_packed_rb(const GemmArgs& g, hipStream_t stream) {
   p.kc = g.k / 64;
   p.chunks_per_split = p.kc;
   p.splits = 1;
-  p.rblocks = (g.m + 15) / 16;
+  const int mt = g.m <= 64 ? 1 : 2;
+  p.rblocks = (g.m + 16 * mt - 1) / (16 * mt);
   if (int64_t(p.nb) * p.rblocks > INT_MAX / 2) return hipErrorNotSupported;
-  const GemvShape sh = gemv_shape(1, p.kc, false, p.nb);
-  return launch_gemv_shape<1, false, false, true, false, true>(p, sh, p.nb * p.rblocks, stream);
+  GemvShape sh = gemv_shape(mt, p.kc, false, p.nb);
+  sh.cbg = 1;
+  if (mt == 1) return launch_gemv_shape<1, false, false, true, false, true>(p, sh, p.nb * p.rblocks, stream);
+  sh.w = std::min(sh.w, 8);  // two A tiles per chunk: at most 8 waves, K in rounds
+  return launch_gemv_shape<2, false, false, true, false, true>(p, sh, p.nb * p.rblocks, stream);
 }
 
 
@@ -2886,7 +2893,7 @@ hipError_t gemm(const GemmArgs& g, const Scratch* s, hipStream_t stream, int* de
     if (part_gemv_preferred(g)) return launch_part(g, s, stream, deferred);
     if (g.m <= 16) return launch_packed<1>(g, s, stream, deferred);
     if (g.m <= 32) return launch_packed<2>(g, s, stream, deferred);
-    if (g.m <= 64 && s && s->queue_pool && !deferred && !g.ln_gamma && !g.a_p32 && !g.amax_groups &&
+    if (g.m <= 128 && s && s->queue_pool && !deferred && !g.ln_gamma && !g.a_p32 && !g.amax_groups &&
         (g.n + 15) / 16 <= 192 && g.k <= 3072) {
       const hipError_t e = launch_packed_rb(g, stream);
       if (e != hipErrorNotSupported) return e;
