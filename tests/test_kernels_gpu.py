@@ -165,11 +165,12 @@ def _fused(ops_lib, a, q, s, bias, y, res, m, n, k, epi):
     assert st == 0, ops_lib.ti_v2_last_error()
 
 
-@pytest.mark.parametrize("m", [1, 8, 64, 512])
+@pytest.mark.parametrize("m", [1, 8, 64, 512, 1024])
 @pytest.mark.parametrize("k,n", [(768, 3072), (3072, 768)])
 def test_w8a16_sweep_fused_bias_gelu(ops, m, k, n):
     """A ~ N(0,1) fp16, q ~ U[-127,127], scales U[1e-3,1e-2] drawn
-    as fp16 and widened to fp32, bias N(0,0.02), fused bias+GELU, fp16 output."""
+    as fp16 and widened to fp32, bias N(0,0.02), fused bias+GELU, fp16 output
+    (and M = 1024, the row GEMM's largest M)."""
     t = torch()
     rng = np.random.default_rng(20261101 + m + n)
     a = f16(rng.standard_normal((m, k)))
